@@ -1,0 +1,217 @@
+/*
+ * gbs_sample.h -- C ABI of the MI355X (gfx950) token-sampling library `libgbsample_hip.so`.
+ *
+ * Two groups of entry points:
+ *
+ *  1. Drop-ins for the launchers REXL3's model runtime binds for this path (same names, same argument meaning, same
+ *     return codes). Each declaration cites the reference launcher it replaces.
+ *  2. `gbs_*` entry points with no single reference launcher: the fused keyed sampler (top-(k+8) plus the keyed draw of
+ *     `crates/sampling::try_choose` in one launch), the device accept steps of `crates/spec`, and the extended pipeline
+ *     (penalties, grammar mask, temperature, top-k/top-p/min-p, inverse-CDF draw from a caller uniform, speculative
+ *     rejection acceptance).
+ *
+ * Conventions (all entry points; they follow crates/cuda/csrc/common.cuh:1-12 and crates/cuda/csrc/glue.cu:1076-1104):
+ *  - raw device pointers; `stream` is a hipStream_t passed as void* (NULL = the default stream);
+ *  - launches are asynchronous and never synchronise the stream;
+ *  - return 0 on success, GBS_ERR_INVALID (1, the value of hipErrorInvalidValue and cudaErrorInvalidValue) for an
+ *    argument outside the contract (nothing is launched), otherwise the HIP launch error;
+ *  - rows == 0 is a successful no-op;
+ *  - the caller owns every buffer and workspace and keeps them alive until the stream has drained them.
+ *
+ * Row status codes mirror `gb_sampling::SamplingError` (crates/sampling/src/lib.rs:70-76).
+ */
+#ifndef GBS_SAMPLE_H
+#define GBS_SAMPLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GBS_OK 0
+#define GBS_ERR_INVALID 1
+
+/* per-row status (crates/sampling/src/lib.rs:70-76) */
+#define GBS_ROW_OK 0
+#define GBS_ROW_NO_CANDIDATES 1
+#define GBS_ROW_NAN_LOGIT 2
+#define GBS_ROW_INVALID_PARAMS 3
+
+/* logits element types */
+#define GBS_DTYPE_F32 0
+#define GBS_DTYPE_BF16 1
+#define GBS_DTYPE_F16 2
+
+/* Largest vocabulary the extended pipeline accepts: 2^19 tokens keeps every row's integer mass sum below 2^63. */
+#define GBS_MAX_VOCAB 524288
+/* Candidates per row of the exact top-count kernels (crates/cuda/csrc/glue.cu:1088). */
+#define GBS_MAX_COUNT 64
+
+/*
+ * The keyed sampling record of one row, 48 bytes, field for field the `KeyedRow` of crates/cuda/csrc/glm_mtp.cu:258-264:
+ * the row samples `try_choose` at absolute position first_position + depth.
+ */
+typedef struct GbsKeyedRow {
+    uint64_t seed;
+    uint64_t first_position;
+    double temperature;
+    double top_p;
+    double min_p;
+    int32_t top_k;
+    int32_t keyed;
+} GbsKeyedRow;
+
+/*
+ * The extended pipeline's per-row parameters (32 bytes). No reference counterpart: REXL3 refuses penalties and grammar
+ * masks (crates/server/src/api.rs:196-206). Per element, with c = counts[i]:
+ *   l = x;  if c > 0: l = (l > 0 ? l * (1/repetition) : l * repetition);  l = l - ((float)c * frequency + presence);
+ *   if the mask bit of i is clear: l = -inf.
+ * temperature 0 is exact greedy. top_k 0 = off. top_p outside (0,1) = off. min_p 0 = off.
+ */
+typedef struct GbsRowParams {
+    float temperature;
+    float top_p;
+    float min_p;
+    float repetition;
+    float presence;
+    float frequency;
+    int32_t top_k;
+    int32_t reserved;
+} GbsRowParams;
+
+/* ------------------------------------------------------------------------------------------------------------------
+ * 1. Reference drop-ins
+ * ------------------------------------------------------------------------------------------------------------------ */
+
+/* Replaces crates/cuda/csrc/glue.cu:1078-1081 (gb_topk_valid_workspace_bytes). 0 for a shape outside the contract. */
+size_t gb_topk_valid_workspace_bytes(int rows, int valid, int count);
+/* Replaces crates/cuda/csrc/glue.cu:1083 (gb_topk_workspace_bytes). */
+size_t gb_topk_workspace_bytes(int rows, int vocab, int count);
+
+/*
+ * Replaces crates/cuda/csrc/glue.cu:1089-1100 (gb_topk_valid). bf16 logits [rows, stride]; per row the exact `count`
+ * largest of columns [0, valid) by (value desc, id asc); NaN is ordered and reported as -inf, -0 ties +0 (and is
+ * reported as +0). ids i32 [rows, count], vals f32 [rows, count]. 1 <= count <= min(64, valid), valid <= stride.
+ * Workspace: gb_topk_valid_workspace_bytes(rows, valid, count) bytes, 16-byte aligned; contents on entry do not matter.
+ */
+int gb_topk_valid(const void* logits, int rows, int stride, int valid, int count, int* ids, float* vals, void* workspace,
+                  size_t ws_bytes, void* stream);
+/* Replaces crates/cuda/csrc/glue.cu:1103-1106 (gb_topk): gb_topk_valid with valid == stride == vocab. */
+int gb_topk(const void* logits, int rows, int vocab, int count, int* ids, float* vals, void* workspace, size_t ws_bytes,
+            void* stream);
+
+/*
+ * Replaces crates/cuda/csrc/nemotron_glue.cu:504-522 (gb_nemo_glue_topk). f32 logits [rows, vocab]; the exact `count`
+ * largest by (value desc, id asc) with -0 == +0 and NaN below -inf (NaNs among themselves by id); values are returned
+ * as stored (NaN payload and zero sign kept). `blocks` >= 1 is the caller's block plan (crates/cuda/src/nemotron_glue.rs:172-176);
+ * the workspace must hold rows * blocks * 8 * count * 8 bytes, 8-byte aligned. The result does not depend on `blocks`.
+ * 1 <= count <= min(64, vocab), rows <= 65535.
+ */
+int gb_nemo_glue_topk(const void* logits, int rows, int vocab, int count, int blocks, void* ws, size_t ws_bytes, void* ids,
+                      void* vals, void* stream);
+
+/* Replaces crates/cuda/csrc/glm_glue.cu:270-315 (gb_glm_topk_f16_workspace_bytes / gb_glm_topk_f16): gb_topk_valid on
+ * fp16 logits (NaN ordered and reported as -inf, -0 ties +0 and is reported as +0). */
+size_t gb_glm_topk_f16_workspace_bytes(int rows, int valid, int count);
+int gb_glm_topk_f16(const void* logits, int rows, int stride, int valid, int count, int* ids, float* vals, void* workspace,
+                    size_t ws_bytes, void* stream);
+
+/*
+ * Replaces crates/cuda/csrc/glm_mtp.cu:272-280 (gb_glm_keyed_pick). ids i32 / vals f32 [rows, count] sorted by
+ * (value desc, id asc), count <= 64; params GbsKeyedRow[rows]. A keyed row with temperature > 0 takes
+ * `try_choose` (crates/sampling/src/lib.rs:210-267) over its first min(top_k, count) candidates (top_k 0 = all) at
+ * position first_position + depth; any other row takes the first candidate. out_ids i32 / out_vals f32 [rows].
+ */
+int gb_glm_keyed_pick(const int* ids, const float* vals, int count, int rows, const void* params, int depth, int* out_ids,
+                      float* out_vals, void* stream);
+
+/* Replaces crates/cuda/csrc/qfn_verify.cu:33-40 (gb_qfn_greedy_gather): column 0 of each candidate row; the value is
+ * NaN when any of the row's `count` candidates is NaN. */
+int gb_qfn_greedy_gather(const void* ids, const void* vals, int count, int rows, void* out_ids, void* out_vals, void* stream);
+
+/* ------------------------------------------------------------------------------------------------------------------
+ * 2. Fused and extended entry points
+ * ------------------------------------------------------------------------------------------------------------------ */
+
+/*
+ * Fills `bytes` bytes of a workspace with zeros by a kernel (not hipMemset, so it may be captured in a HIP graph).
+ * The gbs_* workspaces hold per-row arrival counters that must be zero before the first call; every call leaves them
+ * zero again. Calls that share one workspace must not overlap.
+ */
+int gbs_workspace_clear(void* ws, size_t bytes, void* stream);
+
+/*
+ * Fused keyed sampler: per row, the exact top-(top_k + 8) of logits[row, 0..valid) (dtype f32 / bf16 / f16 with the NaN
+ * rules of the matching drop-in above) and then `try_choose` (crates/sampling/src/lib.rs:210-267) over those candidates
+ * at position params[row].first_position + depth: what REXL3's decode round computes with gb_topk / gb_nemo_glue_topk,
+ * download_candidates and try_choose (crates/engine/src/lib.rs:2089-2117), without the candidate readback.
+ * params[row].top_k must be in [1, 56] (the API cap, crates/server/src/api.rs:43-44) -- otherwise the row's status is
+ * GBS_ROW_INVALID_PARAMS, as it is for the parameter checks of Sampling::validate (crates/sampling/src/lib.rs:56-67).
+ * `keyed` is ignored: every row is sampled.
+ * out_ids i32 [rows] (-1 on error), out_vals f32 [rows] (the chosen candidate's value; may be NULL),
+ * out_status i32 [rows] (may be NULL). Workspace: gbs_keyed_sample_workspace_bytes(rows, valid), 256-byte aligned,
+ * zeroed once (gbs_workspace_clear).
+ */
+size_t gbs_keyed_sample_workspace_bytes(int rows, int valid);
+int gbs_keyed_sample_rows(const void* logits, int dtype, int rows, int stride, int valid, const GbsKeyedRow* params, int depth,
+                          int* out_ids, float* out_vals, int* out_status, void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * Chain accept (crates/spec/src/lib.rs:30-35): for each of n_seq sequences, the longest prefix with
+ * drafts[s, i] == samples[s, i], i < width. drafts i32 [n_seq, width], samples i32 [n_seq, width + 1],
+ * accepted i32 [n_seq].
+ */
+int gbs_accept(const int* drafts, const int* samples, int n_seq, int width, int* accepted, void* stream);
+
+/*
+ * Tree accept (crates/spec/src/tree.rs:417-438): per tree, from row 0 follow the first child whose token equals the
+ * node's sample. tokens / parents / samples i32 [n_tree, nodes] (parents[0] = -1, parents come first);
+ * path i32 [n_tree, nodes] (the accepted rows root first, then -1), path_len i32 [n_tree].
+ */
+int gbs_accept_tree(const int* tokens, const int* parents, const int* samples, int n_tree, int nodes, int* path, int* path_len,
+                    void* stream);
+
+/*
+ * Extended sampling pipeline. logits [rows, stride] (dtype f32 or bf16, bf16 widened exactly), columns [0, vocab);
+ * counts i32 [rows, vocab] (NULL = all zero); mask u32 [rows, ceil(vocab/32)] (bit i%32 of word i/32 set = token
+ * allowed; NULL = all allowed); params GbsRowParams[rows]; uniforms f32 [rows], each in [0, 1).
+ * `kmax` in [1, 64] promises top_k in [1, kmax] on every row and selects the single-pass kernel (a row that breaks the
+ * promise gets GBS_ROW_INVALID_PARAMS); kmax == 0 selects the multi-pass full-distribution path (any top_k, 0 = off).
+ * Outputs (any but out_ids may be NULL): out_ids i32 [rows] (-1 on error), out_greedy i32 [rows] (argmax, ties to the
+ * lowest id), out_probs f32 [rows] (probability of the chosen token in the final kept distribution),
+ * out_logprobs f32 [rows] (log-softmax of the chosen token over every allowed token at temperature T, or 1 when T == 0),
+ * out_status i32 [rows].
+ * Workspace: gbs_sample_workspace_bytes(rows, vocab, kmax), 256-byte aligned, zeroed once (gbs_workspace_clear).
+ * vocab <= GBS_MAX_VOCAB.
+ */
+size_t gbs_sample_workspace_bytes(int rows, int vocab, int kmax);
+int gbs_sample_rows(const void* logits, int dtype, int rows, int stride, int vocab, const int32_t* counts, const uint32_t* mask,
+                    const GbsRowParams* params, const float* uniforms, int kmax, int* out_ids, int* out_greedy, float* out_probs,
+                    float* out_logprobs, int* out_status, void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * Speculative verification by rejection (Leviathan et al. 2023 / Chen et al. 2023), exact in integer masses.
+ * n_seq sequences of `width` drafts + 1 bonus row: target and draft f32 logits [n_seq * (width + 1), vocab] (row
+ * s * (width + 1) + j; draft rows j == width are not read); draft_ids i32 [n_seq, width]; temperatures f32
+ * [n_seq * (width + 1)]; u_accept f32 [n_seq, width] and u_resample f32 [n_seq], all in [0, 1).
+ * Draft j is accepted iff u_accept * q(x) < p(x), p and q the softmax at the row's temperature (temperature 0: x must be
+ * the target's argmax). At the first rejection the token is drawn from max(p - q, 0) (the target's argmax at
+ * temperature 0); after `width` acceptances the bonus token is drawn from the last row's p.
+ * out_accepted i32 [n_seq]; out_tokens i32 [n_seq, width + 1] (accepted drafts, then the drawn token, then -1);
+ * out_status i32 [n_seq] (may be NULL). Workspace: gbs_spec_verify_workspace_bytes(n_seq, width, vocab), zeroed once.
+ */
+size_t gbs_spec_verify_workspace_bytes(int n_seq, int width, int vocab);
+int gbs_spec_verify(const float* target, const float* draft, int n_seq, int width, int vocab, const int* draft_ids,
+                    const float* temperatures, const float* u_accept, const float* u_resample, int* out_accepted,
+                    int* out_tokens, int* out_status, void* ws, size_t ws_bytes, void* stream);
+
+/* Library version string. */
+const char* gbs_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GBS_SAMPLE_H */

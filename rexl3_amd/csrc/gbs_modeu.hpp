@@ -1,0 +1,133 @@
+// Exact integer arithmetic of the extended pipeline, device side. The definitions (the per-element penalty, the mass
+// of a token, the exact products with an f32 fraction) are the pipeline's specification; each helper states it.
+#pragma once
+#include "gbs_common.hpp"
+
+namespace gbs {
+namespace modeu {
+
+typedef unsigned __int128 u128;
+
+constexpr u32 NEG_INF_KEY = 0x007fffffu;  // okey_f32(-inf)
+constexpr u64 MASS_ONE = 1ull << 44;      // the mass of the row maximum
+
+struct RowParamsDev {
+    float temperature, top_p, min_p, repetition, presence, frequency;
+    int top_k, reserved;
+};
+static_assert(sizeof(RowParamsDev) == 32, "GbsRowParams is 32 bytes");
+
+__device__ __forceinline__ bool params_invalid(const RowParamsDev& p, float u) {
+    bool bad = !(isfinite(p.temperature) && p.temperature >= 0.0f);
+    bad |= !(p.top_p >= 0.0f && p.top_p <= 1.0f);
+    bad |= !(p.min_p >= 0.0f && p.min_p <= 1.0f);
+    bad |= !(isfinite(p.repetition) && p.repetition > 0.0f);
+    bad |= !isfinite(p.presence) || !isfinite(p.frequency);
+    bad |= p.top_k < 0;
+    bad |= !(u >= 0.0f && u < 1.0f);
+    return bad;
+}
+
+// penalties: if c > 0, l = (x > 0 ? x * rinv : x * rep) - ((float)c * freq + pres), each operation rounded to f32
+__device__ __forceinline__ float penalize(float x, int c, float rinv, float rep, float freq, float pres) {
+    if (c > 0) {
+        float l = x > 0.0f ? x * rinv : x * rep;
+        const float a = (float)c * freq;
+        const float b = a + pres;
+        return l - b;
+    }
+    return x;
+}
+
+// 2^f, f in [-0.5, 0.5]: degree-7 Taylor series of exp(f ln 2), Horner form in fused multiply-adds
+__device__ __forceinline__ float pow2_frac(float f) {
+    float p = 1.52527338e-05f;
+    p = fmaf(p, f, 1.54035304e-04f);
+    p = fmaf(p, f, 1.33335581e-03f);
+    p = fmaf(p, f, 9.61812911e-03f);
+    p = fmaf(p, f, 5.55041087e-02f);
+    p = fmaf(p, f, 2.40226507e-01f);
+    p = fmaf(p, f, 6.93147181e-01f);
+    p = fmaf(p, f, 1.0f);
+    return p;
+}
+
+// The integer mass of a token of logit l in a row of maximum M at c2 = log2(e) / T:
+// 2^44 if l == M; else y = (l - M) * c2; 0 unless y >= -64; n = rint(y), f = y - n; m = (u32)(2^f * 2^24);
+// mass = m * 2^(n + 20), truncated.
+__device__ __forceinline__ u64 mass(float l, float M, float c2) {
+    if (l == M) return MASS_ONE;
+    const float d = l - M;
+    const float y = d * c2;
+    if (!(y >= -64.0f)) return 0ull;
+    const float n = rintf(y);
+    const float f = y - n;
+    const float p = pow2_frac(f);
+    const u32 m = (u32)(p * 16777216.0f);
+    const int sh = (int)n + 20;
+    if (sh >= 0) return (u64)m << sh;
+    if (sh <= -32) return 0ull;
+    return (u64)(m >> (-sh));
+}
+
+__device__ __forceinline__ float temp_scale(float t) { return 1.44269504088896340736f / t; }
+
+// floor(x * z) for finite x >= 0 (x < 2^23), exactly; *exact = the product was an integer
+__device__ __forceinline__ u128 mul_floor(float x, u128 z, bool* exact) {
+    const u32 b = __float_as_uint(x);
+    const u32 e = (b >> 23) & 0xFFu;
+    u64 m = b & 0x7FFFFFu;
+    int sh;
+    if (e == 0) sh = 149;
+    else {
+        m |= 0x800000u;
+        sh = 150 - (int)e;
+    }
+    if (m == 0 || z == 0) {
+        if (exact) *exact = true;
+        return 0;
+    }
+    const u128 lo = (u128)m * (u64)z;
+    const u128 hi = (u128)m * (u64)(z >> 64);
+    u64 w0 = (u64)lo;
+    const u128 mid = (lo >> 64) + (u64)hi;
+    u64 w1 = (u64)mid;
+    u64 w2 = (u64)((hi >> 64) + (mid >> 64));
+    bool ex = true;
+    int s = sh;
+    while (s >= 64) {
+        ex &= w0 == 0;
+        w0 = w1;
+        w1 = w2;
+        w2 = 0;
+        s -= 64;
+    }
+    if (s > 0) {
+        ex &= (w0 & ((1ull << s) - 1)) == 0;
+        w0 = (w0 >> s) | (w1 << (64 - s));
+        w1 = (w1 >> s) | (w2 << (64 - s));
+    }
+    if (exact) *exact = ex;
+    return ((u128)w1 << 64) | w0;
+}
+
+__device__ __forceinline__ u64 mul_ceil64(float x, u64 z) {
+    bool ex;
+    const u64 f = (u64)mul_floor(x, (u128)z, &ex);
+    return f + (ex ? 0ull : 1ull);
+}
+
+// (max, sum of 2^((l - max) * c)) pairs: the online log-sum-exp, base 2
+struct Lse {
+    float m, s;
+};
+
+__device__ __forceinline__ Lse lse_merge(Lse a, Lse b, float c) {
+    if (b.m == -INFINITY) return a;
+    if (a.m == -INFINITY) return b;
+    const float M = fmaxf(a.m, b.m);
+    return Lse{M, a.s * exp2f((a.m - M) * c) + b.s * exp2f((b.m - M) * c)};
+}
+
+}  // namespace modeu
+}  // namespace gbs

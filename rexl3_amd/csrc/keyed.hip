@@ -1,0 +1,384 @@
+// REXL3's keyed sampler on the device.
+//
+//  - keyed_choose_wave: `try_choose` (crates/sampling/src/lib.rs:210-267) over a row's sorted candidates, one wave per
+//    row: the top_p / min_p cuts in double exactly as the reference orders them (numpy pairwise sum and the sequential
+//    cumsum run on lane 0, at most 64 terms), the Gumbel noise of each kept candidate on its own lane, and an argmax that
+//    keeps the first candidate on ties, as the reference's strict `>` does.
+//  - gb_glm_keyed_pick (crates/cuda/csrc/glm_mtp.cu:266-297), gb_qfn_greedy_gather (crates/cuda/csrc/qfn_verify.cu:11-40).
+//  - gbs_keyed_sample_rows: exact top-(top_k + 8) over the full row and the keyed draw in ONE launch. Grid (splits,
+//    rows); each block selects its chunk's best 64 keys, writes them to the workspace and counts its arrival; the last
+//    block of a row merges the row's lists and draws. Only the chosen id leaves the device.
+//  - gbs_accept / gbs_accept_tree: crates/spec/src/lib.rs:30-35 and crates/spec/src/tree.rs:417-438.
+#include "gbs_select.hpp"
+
+using namespace gbs;
+using namespace gbs::sel;
+
+namespace {
+
+__device__ __forceinline__ u64 sm_mix(u64 x) {
+    x ^= x >> 30;
+    x *= 0xBF58476D1CE4E5B9ull;
+    x ^= x >> 27;
+    x *= 0x94D049BB133111EBull;
+    return x ^ (x >> 31);
+}
+
+// crates/sampling/src/lib.rs:131-150
+__device__ __forceinline__ double keyed_uniform(u64 seed, u64 position, u64 id) {
+    u64 x = sm_mix(seed + 0x9E3779B97F4A7C15ull);
+    x = sm_mix(x ^ (position * 0xD1B54A32D192ED03ull));
+    x = sm_mix(x ^ id);
+    const double two_m53 = 1.0 / 9007199254740992.0;
+    const double u = (double)(x >> 11) * two_m53 + two_m53 * 0.5;
+    const double below_one = 1.0 - two_m53;
+    return u < below_one ? u : below_one;
+}
+
+// numpy's float64 pairwise sum for n <= 128 (crates/sampling/src/lib.rs:152-173)
+__device__ double pairwise_small(const double* a, int n) {
+    if (n < 8) {
+        double r = 0.0;
+        for (int i = 0; i < n; ++i) r += a[i];
+        return r;
+    }
+    double r[8];
+    for (int j = 0; j < 8; ++j) r[j] = a[j];
+    int i = 8;
+    for (; i < n - (n % 8); i += 8)
+        for (int j = 0; j < 8; ++j) r[j] += a[i + j];
+    double res = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
+    for (; i < n; ++i) res += a[i];
+    return res;
+}
+
+// `try_choose` over vals[0..k), ids[0..k) (LDS, already in (value desc, id asc) order, no NaN), temperature > 0.
+// Returns the chosen index (wave-uniform). s_tmp: 64 doubles of LDS.
+__device__ int keyed_choose_wave(const float* vals, const u32* ids, int k, u64 seed, double temperature, double top_p, double min_p,
+                                 u64 position, double* s_tmp) {
+    const int l = lane_id();
+    const double t = temperature > 1e-6 ? temperature : 1e-6;
+    const double sc = l < k ? (double)vals[l] / t : 0.0;
+    const double sc0 = __shfl(sc, 0, WAVE);
+    int keep = k;
+    if (top_p > 0.0 && top_p < 1.0) {
+        // the maximum of `scaled` is its first entry: the values are sorted and t > 0
+        s_tmp[l] = l < k ? exp(sc - sc0) : 0.0;
+        wave_lds_sync();
+        int kp = 0;
+        if (l == 0) {
+            const double total = pairwise_small(s_tmp, k);
+            double c = 0.0;
+            int below = 0;
+            for (int i = 0; i < k; ++i) {
+                c += s_tmp[i] / total;
+                if (c < top_p) ++below;
+            }
+            kp = below + 1 < k ? below + 1 : k;
+        }
+        keep = __shfl(kp, 0, WAVE);
+        wave_lds_sync();
+    }
+    if (min_p > 0.0) {
+        const double floor_v = sc0 + log(min_p);
+        const int cnt = __popcll(ballot(l < keep && sc >= floor_v));
+        keep = cnt > 1 ? cnt : 1;
+    }
+    // Gumbel argmax; a NaN or -inf score never wins (strict >), the first index wins ties, index 0 if nothing beats -inf
+    double score = -INFINITY;
+    if (l < keep) {
+        const double u = keyed_uniform(seed, position, (u64)ids[l]);
+        score = sc + (-log(-log(u)));
+    }
+    const bool live = score > -INFINITY;  // false for NaN
+    double best = live ? score : -INFINITY;
+#pragma unroll
+    for (int m = 1; m < WAVE; m <<= 1) best = fmax(best, __shfl_xor(best, m, WAVE));
+    const u64 hit = ballot(live && score == best);
+    return hit ? (int)__builtin_ctzll(hit) : 0;
+}
+
+// ------------------------------------------------------------------------------------------------ gb_glm_keyed_pick
+
+struct KeyedRowDev {
+    u64 seed, first_position;
+    double temperature, top_p, min_p;
+    int top_k, keyed;
+};
+static_assert(sizeof(KeyedRowDev) == 48, "KeyedRow is 48 bytes");
+
+__device__ __forceinline__ bool row_before(float va, u32 ia, int pa, float vb, u32 ib, int pb) {
+    const bool na = va != va, nb = vb != vb;
+    if (na != nb) return nb;  // a number before a NaN
+    if (!na && va != vb) return va > vb;
+    if (ia != ib) return ia < ib;
+    return pa < pb;
+}
+
+// one wave per row (4 rows per block)
+__global__ void __launch_bounds__(256) keyed_pick_k(const int* __restrict__ ids, const float* __restrict__ vals, int count, int rows,
+                                                    const KeyedRowDev* __restrict__ params, int depth, int* __restrict__ out_ids,
+                                                    float* __restrict__ out_vals) {
+    __shared__ float s_v[4][64];
+    __shared__ u32 s_i[4][64];
+    __shared__ u32 s_tid[4][64];
+    __shared__ double s_tmp[4][64];
+    const int w = threadIdx.x / WAVE, l = lane_id();
+    const int r = blockIdx.x * 4 + w;
+    if (r >= rows) return;
+    const int* c_row = ids + (size_t)r * count;
+    const float* v_row = vals + (size_t)r * count;
+    const KeyedRowDev p = params[r];
+    int pick = 0;
+    if (p.keyed && p.temperature > 0.0) {
+        const int k = p.top_k > 0 && p.top_k < count ? p.top_k : count;
+        // order the first k by (value desc, id asc), stable; rank by counting (k <= 64)
+        const float v = l < k ? v_row[l] : 0.f;
+        const u32 id = l < k ? (u32)c_row[l] : 0u;
+        int rank = 0;
+        bool nan_any = false;
+        for (int j = 0; j < k; ++j) {
+            const float vj = v_row[j];
+            const u32 ij = (u32)c_row[j];
+            nan_any |= vj != vj;
+            if (l < k && row_before(vj, ij, j, v, id, l)) ++rank;
+        }
+        // try_choose refuses a NaN among the candidates; such a row keeps the first candidate
+        if (!nan_any) {
+            if (l < k) {
+                s_v[w][rank] = v;
+                s_i[w][rank] = (u32)l;  // original index
+            }
+            wave_lds_sync();
+            // sorted token ids for the chooser
+            if (l < k) s_tid[w][l] = (u32)c_row[s_i[w][l]];
+            wave_lds_sync();
+            const int b = keyed_choose_wave(s_v[w], s_tid[w], k, p.seed, p.temperature, p.top_p, p.min_p,
+                                            p.first_position + (u64)depth, s_tmp[w]);
+            pick = (int)s_i[w][b];
+        }
+    }
+    if (l == 0) {
+        out_ids[r] = c_row[pick];
+        out_vals[r] = v_row[pick];
+    }
+}
+
+// ------------------------------------------------------------------------------------------------ greedy gather
+
+__global__ void greedy_gather_k(const int* __restrict__ ids, const float* __restrict__ vals, int count, int rows,
+                                int* __restrict__ out_ids, float* __restrict__ out_vals) {
+    const int r = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= rows) return;
+    const size_t base = (size_t)r * count;
+    bool nan = false;
+    for (int c = 0; c < count; ++c) nan |= vals[base + c] != vals[base + c];
+    out_ids[r] = ids[base];
+    out_vals[r] = nan ? __uint_as_float(0x7fc00000u) : vals[base];
+}
+
+// ------------------------------------------------------------------------------------------------ fused keyed sampler
+
+constexpr int KS_TARGET_BLOCKS = 1024;
+constexpr int KS_MIN_CHUNK = 4096;
+
+int keyed_splits(int rows, int valid) {
+    int s = (KS_TARGET_BLOCKS + rows - 1) / rows;
+    const int by_size = (valid + KS_MIN_CHUNK - 1) / KS_MIN_CHUNK;
+    if (s > by_size) s = by_size;
+    if (s < 1) s = 1;
+    return s;
+}
+
+size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+size_t keyed_ws_bytes(int rows, int valid) {
+    if (rows <= 0 || valid <= 0) return 0;
+    const int s = keyed_splits(rows, valid);
+    return align256((size_t)rows * 4) + (size_t)rows * s * WAVE * sizeof(u64);
+}
+
+__device__ __forceinline__ bool keyed_params_ok(const KeyedRowDev& p) {
+    const bool t_ok = isfinite(p.temperature) && p.temperature >= 0.0;
+    const bool p_ok = isfinite(p.top_p) && p.top_p >= 0.0 && p.top_p <= 1.0;
+    const bool m_ok = isfinite(p.min_p) && p.min_p >= 0.0 && p.min_p <= 1.0;
+    return t_ok && p_ok && m_ok && p.top_k >= 1 && p.top_k <= 56;
+}
+
+template <int DT>
+__global__ void __launch_bounds__(NT) keyed_sample_k(const void* logits, long long stride, int valid, int chunk,
+                                                     const KeyedRowDev* __restrict__ params, int depth, unsigned* counters, u64* parts,
+                                                     int* out_ids, float* out_vals, int* out_status) {
+    __shared__ u64 s_buf[NW][BUF];
+    __shared__ u64 s_list[NW][WAVE];
+    __shared__ float s_v[WAVE];
+    __shared__ u32 s_id[WAVE];
+    __shared__ double s_tmp[WAVE];
+    __shared__ unsigned s_flag;
+    const int S = gridDim.x, sp = blockIdx.x, r = blockIdx.y;
+    const size_t esz = DT == DT_F32 ? 4 : 2;
+    const void* row = (const char*)logits + (size_t)r * (size_t)stride * esz;
+    const KeyedRowDev p = params[r];
+    const bool ok = keyed_params_ok(p);
+    const int count = ok ? min(p.top_k + 8, valid) : min(WAVE, valid);
+    const int lo = sp * chunk;
+    const int hi = min(valid, lo + chunk);
+    const bool vec = (stride % 4 == 0) && aligned(logits, DT == DT_F32 ? 16 : 8);
+    WaveTop<BUF> wt;
+    wt.init(s_buf[threadIdx.x / WAVE], count, 0ull);
+    block_select<DT>(row, lo, hi, vec, count, wt, s_list);
+    if (threadIdx.x < WAVE) parts[((size_t)r * S + sp) * WAVE + threadIdx.x] = wt.list;
+    if (!arrive_last(&counters[r], (unsigned)S, &s_flag)) return;
+    if (threadIdx.x >= WAVE) return;
+    const int l = lane_id();
+    u64 list = 0;
+    for (int o = 0; o < S; ++o) list = wave_merge_desc(list, parts[((size_t)r * S + o) * WAVE + l]);
+    int status = ok ? GBS_ROW_OK : GBS_ROW_INVALID_PARAMS;
+    const u32 id = key_id(list);
+    float v = 0.f;
+    if (l < count) {
+        if (DT == DT_F32) v = ((const float*)row)[id];
+        else v = okey16_to_f32<DT == DT_F16>(key_ok(list));
+    }
+    if (status == GBS_ROW_OK && ballot(l < count && v != v)) status = GBS_ROW_NAN_LOGIT;
+    int pick = 0;
+    if (status == GBS_ROW_OK && p.temperature > 0.0) {
+        s_v[l] = v;
+        s_id[l] = id;
+        wave_lds_sync();
+        const int k = min(p.top_k, count);
+        pick = keyed_choose_wave(s_v, s_id, k, p.seed, p.temperature, p.top_p, p.min_p, p.first_position + (u64)depth, s_tmp);
+    }
+    const u32 pid = readlane32(id, pick);
+    const float pv = __uint_as_float(readlane32(__float_as_uint(v), pick));
+    if (l == 0) {
+        out_ids[r] = status == GBS_ROW_OK ? (int)pid : -1;
+        if (out_vals) out_vals[r] = status == GBS_ROW_OK ? pv : __uint_as_float(0x7fc00000u);
+        if (out_status) out_status[r] = status;
+    }
+}
+
+// ------------------------------------------------------------------------------------------------ accept steps
+
+__global__ void accept_k(const int* __restrict__ drafts, const int* __restrict__ samples, int n_seq, int width, int* accepted) {
+    const int s = blockIdx.x * blockDim.x + threadIdx.x;
+    if (s >= n_seq) return;
+    const int* d = drafts + (size_t)s * width;
+    const int* x = samples + (size_t)s * (width + 1);
+    int a = 0;
+    while (a < width && d[a] == x[a]) ++a;
+    accepted[s] = a;
+}
+
+__global__ void accept_tree_k(const int* __restrict__ tokens, const int* __restrict__ parents, const int* __restrict__ samples,
+                              int n_tree, int nodes, int* path, int* path_len) {
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= n_tree) return;
+    const int* tok = tokens + (size_t)t * nodes;
+    const int* par = parents + (size_t)t * nodes;
+    const int* smp = samples + (size_t)t * nodes;
+    int* out = path + (size_t)t * nodes;
+    int len = 0, cur = 0;
+    out[len++] = 0;
+    for (;;) {
+        const int s = smp[cur];
+        int next = -1;
+        for (int r = cur + 1; r < nodes; ++r)
+            if (par[r] == cur && tok[r] == s) {
+                next = r;
+                break;
+            }
+        if (next < 0) break;
+        out[len++] = next;
+        cur = next;
+    }
+    for (int i = len; i < nodes; ++i) out[i] = -1;
+    path_len[t] = len;
+}
+
+__global__ void clear_k(uint4* p, size_t n16, unsigned char* tail, size_t ntail) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t j = i; j < n16; j += stride) p[j] = make_uint4(0, 0, 0, 0);
+    if (i < ntail) tail[i] = 0;
+}
+
+}  // namespace
+
+GBS_EXPORT int gb_glm_keyed_pick(const int* ids, const float* vals, int count, int rows, const void* params, int depth, int* out_ids,
+                                 float* out_vals, void* stream) {
+    if (rows < 0 || count < 1 || count > GBS_MAX_COUNT || depth < 0) return GBS_ERR_INVALID;
+    if (rows == 0) return 0;
+    if (!ids || !vals || !params || !out_ids || !out_vals) return GBS_ERR_INVALID;
+    hipLaunchKernelGGL(keyed_pick_k, dim3((rows + 3) / 4), dim3(256), 0, to_stream(stream), ids, vals, count, rows,
+                       (const KeyedRowDev*)params, depth, out_ids, out_vals);
+    return launch_status();
+}
+
+GBS_EXPORT int gb_qfn_greedy_gather(const void* ids, const void* vals, int count, int rows, void* out_ids, void* out_vals, void* stream) {
+    if (!ids || !vals || !out_ids || !out_vals || rows < 0 || count <= 0 || count > GBS_MAX_COUNT) return GBS_ERR_INVALID;
+    if (rows == 0) return 0;
+    hipLaunchKernelGGL(greedy_gather_k, dim3((rows + 127) / 128), dim3(128), 0, to_stream(stream), (const int*)ids, (const float*)vals,
+                       count, rows, (int*)out_ids, (float*)out_vals);
+    return launch_status();
+}
+
+GBS_EXPORT int gbs_workspace_clear(void* ws, size_t bytes, void* stream) {
+    if (bytes == 0) return 0;
+    if (!ws || !aligned(ws, 16)) return GBS_ERR_INVALID;
+    const size_t n16 = bytes / 16, ntail = bytes % 16;
+    size_t blocks = (n16 + 255) / 256;
+    if (blocks < 1) blocks = 1;
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL(clear_k, dim3((unsigned)blocks), dim3(256), 0, to_stream(stream), (uint4*)ws, n16,
+                       (unsigned char*)ws + n16 * 16, ntail);
+    return launch_status();
+}
+
+GBS_EXPORT size_t gbs_keyed_sample_workspace_bytes(int rows, int valid) { return keyed_ws_bytes(rows, valid); }
+
+GBS_EXPORT int gbs_keyed_sample_rows(const void* logits, int dtype, int rows, int stride, int valid, const GbsKeyedRow* params, int depth,
+                                     int* out_ids, float* out_vals, int* out_status, void* ws, size_t ws_bytes, void* stream) {
+    if (rows < 0 || stride <= 0 || valid <= 0 || valid > stride || depth < 0) return GBS_ERR_INVALID;
+    if (dtype != GBS_DTYPE_F32 && dtype != GBS_DTYPE_BF16 && dtype != GBS_DTYPE_F16) return GBS_ERR_INVALID;
+    if (rows == 0) return 0;
+    if (rows > 65535 || !logits || !params || !out_ids || !ws || !aligned(ws, 256)) return GBS_ERR_INVALID;
+    if (ws_bytes < keyed_ws_bytes(rows, valid)) return GBS_ERR_INVALID;
+    const int S = keyed_splits(rows, valid);
+    int chunk = (valid + S - 1) / S;
+    chunk = (chunk + 3) / 4 * 4;
+    unsigned* counters = (unsigned*)ws;
+    u64* parts = (u64*)((char*)ws + align256((size_t)rows * 4));
+    const dim3 grid(S, rows);
+    const KeyedRowDev* p = (const KeyedRowDev*)params;
+    if (dtype == GBS_DTYPE_F32)
+        hipLaunchKernelGGL(keyed_sample_k<DT_F32>, grid, dim3(NT), 0, to_stream(stream), logits, (long long)stride, valid, chunk, p,
+                           depth, counters, parts, out_ids, out_vals, out_status);
+    else if (dtype == GBS_DTYPE_BF16)
+        hipLaunchKernelGGL(keyed_sample_k<DT_BF16>, grid, dim3(NT), 0, to_stream(stream), logits, (long long)stride, valid, chunk, p,
+                           depth, counters, parts, out_ids, out_vals, out_status);
+    else
+        hipLaunchKernelGGL(keyed_sample_k<DT_F16>, grid, dim3(NT), 0, to_stream(stream), logits, (long long)stride, valid, chunk, p,
+                           depth, counters, parts, out_ids, out_vals, out_status);
+    return launch_status();
+}
+
+GBS_EXPORT int gbs_accept(const int* drafts, const int* samples, int n_seq, int width, int* accepted, void* stream) {
+    if (n_seq < 0 || width < 0) return GBS_ERR_INVALID;
+    if (n_seq == 0) return 0;
+    if (!samples || !accepted || (width > 0 && !drafts)) return GBS_ERR_INVALID;
+    hipLaunchKernelGGL(accept_k, dim3((n_seq + 127) / 128), dim3(128), 0, to_stream(stream), drafts, samples, n_seq, width, accepted);
+    return launch_status();
+}
+
+GBS_EXPORT int gbs_accept_tree(const int* tokens, const int* parents, const int* samples, int n_tree, int nodes, int* path, int* path_len,
+                               void* stream) {
+    if (n_tree < 0 || nodes < 1) return GBS_ERR_INVALID;
+    if (n_tree == 0) return 0;
+    if (!tokens || !parents || !samples || !path || !path_len) return GBS_ERR_INVALID;
+    hipLaunchKernelGGL(accept_tree_k, dim3((n_tree + 63) / 64), dim3(64), 0, to_stream(stream), tokens, parents, samples, n_tree, nodes,
+                       path, path_len);
+    return launch_status();
+}
+
+GBS_EXPORT const char* gbs_version(void) { return "gbsample-hip 0.1 (gfx950)"; }

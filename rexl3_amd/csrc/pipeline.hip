@@ -1,0 +1,378 @@
+// The extended sampling pipeline (penalties, grammar bitmask, temperature, top-k/top-p/min-p, the inverse-CDF draw from
+// one caller uniform per row), exact in integer masses. The definition of every step is in gbs_modeu.hpp and in the
+// comment of sample_fast_k.
+//
+// Single-pass kernel (kmax in [1, 64]): grid (splits, rows) x 256 threads, one read of the row's logits, counts and
+// mask words. Per 4-element group a lane computes the penalised, masked logits, the order keys and the online log-sum-exp,
+// and offers the keys to its wave's gated top list. The block's lists, LSE and NaN flag go to the workspace; the last
+// block of the row merges them and finishes the row on one wave: masses of the <= 64 candidates, the exact top-p and
+// min-p cuts, and the draw in ascending id order.
+#include "gbs_modeu.hpp"
+
+using namespace gbs;
+using namespace gbs::modeu;
+
+namespace {
+
+constexpr int NT = 256;
+constexpr int NW = NT / WAVE;
+constexpr int GROUPS = 2;                  // 4-element groups per lane per step
+constexpr int BUF = WAVE * (GROUPS * 4 + 1);
+constexpr u64 FLOOR_KEY = ((u64)NEG_INF_KEY << 32) | 0xFFFFFFFFull;  // every -inf key is at or below it
+
+constexpr int FAST_TARGET_BLOCKS = 1024;
+constexpr int FAST_MIN_CHUNK = 4096;
+
+size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+int fast_splits(int rows, int vocab) {
+    int s = (FAST_TARGET_BLOCKS + rows - 1) / rows;
+    const int by_size = (vocab + FAST_MIN_CHUNK - 1) / FAST_MIN_CHUNK;
+    if (s > by_size) s = by_size;
+    if (s < 1) s = 1;
+    return s;
+}
+
+struct FastWs {
+    unsigned* counters;  // [rows]
+    u64* lists;          // [rows][S][64]
+    Lse* lse;            // [rows][S]
+    unsigned* nan;       // [rows][S]
+};
+
+size_t fast_ws_bytes(int rows, int vocab, int S) {
+    return align256((size_t)rows * 4) + align256((size_t)rows * S * WAVE * 8) + align256((size_t)rows * S * sizeof(Lse)) +
+           align256((size_t)rows * S * 4);
+}
+
+FastWs fast_ws(void* ws, int rows, int S) {
+    char* p = (char*)ws;
+    FastWs w;
+    w.counters = (unsigned*)p;
+    p += align256((size_t)rows * 4);
+    w.lists = (u64*)p;
+    p += align256((size_t)rows * S * WAVE * 8);
+    w.lse = (Lse*)p;
+    p += align256((size_t)rows * S * sizeof(Lse));
+    w.nan = (unsigned*)p;
+    return w;
+}
+
+template <int DT>
+__device__ __forceinline__ void load_x4(const void* row, int e, float (&x)[4]) {
+    if (DT == GBS_DTYPE_F32) {
+        const float4 v = *(const float4*)((const float*)row + e);
+        x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
+    } else {
+        const uint2 v = *(const uint2*)((const u16*)row + e);
+        x[0] = __uint_as_float(v.x << 16); x[1] = __uint_as_float(v.x & 0xFFFF0000u);
+        x[2] = __uint_as_float(v.y << 16); x[3] = __uint_as_float(v.y & 0xFFFF0000u);
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ float load_x1(const void* row, int e) {
+    if (DT == GBS_DTYPE_F32) return ((const float*)row)[e];
+    return __uint_as_float((u32)((const u16*)row)[e] << 16);
+}
+
+struct Group {
+    float x[4];
+    int c[4];
+    u32 mbits;  // the 4 mask bits of the group, bit q = element q
+    bool in[4];
+};
+
+template <int DT, bool COUNTS, bool MASK>
+__device__ __forceinline__ void load_group(const void* row, const int* crow, const u32* mrow, int e, int hi, bool vec, Group& g) {
+    if (vec && e + 4 <= hi) {
+        load_x4<DT>(row, e, g.x);
+        if (COUNTS) {
+            const int4 c = *(const int4*)(crow + e);
+            g.c[0] = c.x; g.c[1] = c.y; g.c[2] = c.z; g.c[3] = c.w;
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) g.in[q] = true;
+    } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            g.in[q] = e + q < hi;
+            g.x[q] = g.in[q] ? load_x1<DT>(row, e + q) : 0.f;
+            if (COUNTS) g.c[q] = g.in[q] ? crow[e + q] : 0;
+        }
+    }
+    if (!COUNTS) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) g.c[q] = 0;
+    }
+    g.mbits = 0xFu;
+    if (MASK) g.mbits = (e < hi) ? (mrow[e >> 5] >> (e & 31)) & 0xFu : 0u;
+}
+
+// The row's finish, on one wave. `list` holds the row's best 64 keys (lane = rank).
+struct RowOut {
+    int id, greedy, status;
+    float prob, logprob;
+};
+
+__device__ RowOut finish_row(u64 list, const RowParamsDev& p, float u, bool invalid, bool nan, int count, Lse lse, float clp) {
+    RowOut o{-1, -1, GBS_ROW_OK, 0.f, __uint_as_float(0x7fc00000u)};
+    const int l = lane_id();
+    if (invalid) {
+        o.status = GBS_ROW_INVALID_PARAMS;
+        return o;
+    }
+    if (nan) {
+        o.status = GBS_ROW_NAN_LOGIT;
+        return o;
+    }
+    const u64 top = readlane64(list, 0);
+    if (top <= FLOOR_KEY) {
+        o.status = GBS_ROW_NO_CANDIDATES;
+        return o;
+    }
+    const bool valid = l < count && list > FLOOR_KEY;
+    const int kn = __popcll(ballot(valid));
+    o.greedy = (int)key_id(top);
+    const float M = okey_to_f32(key_ok(top));
+    const float lval = okey_to_f32(key_ok(list));
+    int chosen_rank = 0;
+    if (p.temperature == 0.0f) {
+        o.id = o.greedy;
+        o.prob = 1.0f;
+    } else {
+        const float c2 = temp_scale(p.temperature);
+        const u64 E = valid ? mass(lval, M, c2) : 0ull;
+        const u64 zk = wave_sum_u64(E);
+        const u64 C = wave_scan_u64(E);
+        int keep = kn;
+        if (p.top_p > 0.0f && p.top_p < 1.0f) {
+            const u64 P = mul_ceil64(p.top_p, zk);
+            const int below = __popcll(ballot(valid && C < P));
+            keep = below + 1 < kn ? below + 1 : kn;
+        }
+        if (p.min_p > 0.0f) {
+            const u64 Q = mul_ceil64(p.min_p, MASS_ONE);
+            const int cnt = __popcll(ballot(l < keep && E >= Q));
+            keep = cnt > 1 ? cnt : 1;
+        }
+        const bool kept = l < keep;
+        const u64 z = wave_sum_u64(kept ? E : 0ull);
+        const u64 t = (u64)mul_floor(u, (u128)z, nullptr);
+        // kept tokens in ascending id order: sort (id, rank) pairs
+        const u64 sk = wave_sort_asc(kept ? (((u64)key_id(list) << 32) | (u64)l) : ~0ull);
+        const bool skept = sk != ~0ull;
+        const int rank = (int)(u32)sk;
+        const u64 Es = shfl64(E, skept ? rank : 0);
+        const u64 cum = wave_scan_u64(skept ? Es : 0ull);
+        const u64 hit = ballot(skept && cum > t);
+        const int f = hit ? (int)__builtin_ctzll(hit) : 0;
+        chosen_rank = (int)(u32)readlane64(sk, f);
+        o.id = (int)(readlane64(sk, f) >> 32);
+        const u64 ec = readlane64(Es, f);
+        o.prob = (float)((double)ec / (double)z);
+    }
+    // log-softmax of the chosen token over the allowed tokens, base-2 online sums
+    const float lx = __uint_as_float(readlane32(__float_as_uint(lval), chosen_rank));
+    if (isinf(M)) o.logprob = __uint_as_float(0x7fc00000u);
+    else o.logprob = ((lx - lse.m) * clp - log2f(lse.s)) * 0.6931471805599453f;
+    return o;
+}
+
+template <int DT, bool COUNTS, bool MASK, bool LOGPROB>
+__global__ void __launch_bounds__(NT) sample_fast_k(const void* __restrict__ logits, long long stride, int vocab, int chunk,
+                                                    const int* __restrict__ counts, const u32* __restrict__ mask,
+                                                    const RowParamsDev* __restrict__ params, const float* __restrict__ uniforms,
+                                                    int kmax, bool vec, FastWs ws, int* __restrict__ out_ids,
+                                                    int* __restrict__ out_greedy, float* __restrict__ out_probs,
+                                                    float* __restrict__ out_logprobs, int* __restrict__ out_status) {
+    __shared__ u64 s_buf[NW][BUF];
+    __shared__ u64 s_list[NW][WAVE];
+    __shared__ Lse s_lse[NW];
+    __shared__ unsigned s_nan[NW];
+    __shared__ unsigned s_flag;
+    const int S = gridDim.x, sp = blockIdx.x, r = blockIdx.y;
+    const int tid = threadIdx.x, w = tid / WAVE, l = lane_id();
+    const size_t esz = DT == GBS_DTYPE_F32 ? 4 : 2;
+    const void* row = (const char*)logits + (size_t)r * (size_t)stride * esz;
+    const int* crow = COUNTS ? counts + (size_t)r * vocab : nullptr;
+    const u32* mrow = MASK ? mask + (size_t)r * ((vocab + 31) / 32) : nullptr;
+    const RowParamsDev p = params[r];
+    const float u = uniforms[r];
+    const bool invalid = params_invalid(p, u) || p.top_k < 1 || p.top_k > kmax;
+    const int count = invalid ? 1 : p.top_k;
+    const float rinv = 1.0f / p.repetition;
+    const float clp = p.temperature > 0.0f ? temp_scale(p.temperature) : 1.44269504088896340736f;
+    const int lo = sp * chunk;
+    const int hi = min(vocab, lo + chunk);
+
+    WaveTop<BUF> wt;
+    wt.init(s_buf[w], count, FLOOR_KEY);
+    bool nan = false;
+    Lse lse{-INFINITY, 0.f};
+
+    const int step = NT * 4 * GROUPS;
+    const int wave_first = lo + w * WAVE * 4;
+    const int nsteps = wave_first < hi ? (hi - lo - w * WAVE * 4 + step - 1) / step : 0;
+    Group g[GROUPS], gn[GROUPS];
+    int e = lo + tid * 4;
+#pragma unroll
+    for (int j = 0; j < GROUPS; ++j) load_group<DT, COUNTS, MASK>(row, crow, mrow, e + j * NT * 4, hi, vec, g[j]);
+    for (int s = 0; s < nsteps; ++s) {
+        const int en = e + step;
+        if (s + 1 < nsteps) {
+#pragma unroll
+            for (int j = 0; j < GROUPS; ++j) load_group<DT, COUNTS, MASK>(row, crow, mrow, en + j * NT * 4, hi, vec, gn[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < GROUPS; ++j) {
+            const int eg = e + j * NT * 4;
+            float lv[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                float v = penalize(g[j].x[q], g[j].c[q], rinv, p.repetition, p.frequency, p.presence);
+                if (!((g[j].mbits >> q) & 1u) || !g[j].in[q]) v = -INFINITY;
+                nan |= v != v;
+                lv[q] = v;
+                wt.offer(v != v ? 0ull : make_key(okey_f32(v), (u32)(eg + q)));
+            }
+            if (LOGPROB) {
+                const float gm = fmaxf(fmaxf(lv[0], lv[1]), fmaxf(lv[2], lv[3]));
+                if (gm > lse.m) {
+                    lse.s = lse.m == -INFINITY ? 0.f : lse.s * exp2f((lse.m - gm) * clp);
+                    lse.m = gm;
+                }
+                if (lse.m != -INFINITY) {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) lse.s += exp2f((lv[q] - lse.m) * clp);
+                }
+            }
+        }
+        wt.flush(false);
+#pragma unroll
+        for (int j = 0; j < GROUPS; ++j) g[j] = gn[j];
+        e = en;
+    }
+    wt.flush(true);
+
+    // block reduction: lists, LSE, NaN
+    s_list[w][l] = wt.list;
+    if (LOGPROB) {
+#pragma unroll
+        for (int m = 1; m < WAVE; m <<= 1) {
+            Lse o{__shfl_xor(lse.m, m, WAVE), __shfl_xor(lse.s, m, WAVE)};
+            lse = lse_merge(lse, o, clp);
+        }
+    }
+    const bool wnan = ballot(nan) != 0ull;
+    if (l == 0) {
+        s_lse[w] = lse;
+        s_nan[w] = wnan ? 1u : 0u;
+    }
+    __syncthreads();
+    if (w == 0) {
+        for (int o = 1; o < NW; ++o) wt.merge_sorted(s_list[o][l]);
+        const size_t slot = (size_t)r * S + sp;
+        ws.lists[slot * WAVE + l] = wt.list;
+        if (l == 0) {
+            Lse b = s_lse[0];
+            unsigned bn = s_nan[0];
+            for (int o = 1; o < NW; ++o) {
+                if (LOGPROB) b = lse_merge(b, s_lse[o], clp);
+                bn |= s_nan[o];
+            }
+            ws.lse[slot] = b;
+            ws.nan[slot] = bn;
+        }
+    }
+    if (!arrive_last(&ws.counters[r], (unsigned)S, &s_flag)) return;
+    if (w != 0) return;
+
+    u64 list = 0;
+    for (int o = 0; o < S; ++o) list = wave_merge_desc(list, ws.lists[((size_t)r * S + o) * WAVE + l]);
+    Lse rl{-INFINITY, 0.f};
+    unsigned rn = 0;
+    for (int o = l; o < S; o += WAVE) {
+        if (LOGPROB) rl = lse_merge(rl, ws.lse[(size_t)r * S + o], clp);
+        rn |= ws.nan[(size_t)r * S + o];
+    }
+    if (LOGPROB) {
+#pragma unroll
+        for (int m = 1; m < WAVE; m <<= 1) {
+            Lse o{__shfl_xor(rl.m, m, WAVE), __shfl_xor(rl.s, m, WAVE)};
+            rl = lse_merge(rl, o, clp);
+        }
+    }
+    rn = wave_or(rn);
+    const RowOut o = finish_row(list, p, u, invalid, rn != 0u, count, rl, clp);
+    if (l == 0) {
+        out_ids[r] = o.id;
+        if (out_greedy) out_greedy[r] = o.greedy;
+        if (out_probs) out_probs[r] = o.prob;
+        if (out_logprobs) out_logprobs[r] = o.status == GBS_ROW_OK ? o.logprob : __uint_as_float(0x7fc00000u);
+        if (out_status) out_status[r] = o.status;
+    }
+}
+
+template <int DT, bool COUNTS, bool MASK, bool LOGPROB>
+void launch_fast(dim3 grid, hipStream_t st, const void* logits, long long stride, int vocab, int chunk, const int* counts,
+                 const u32* mask, const RowParamsDev* params, const float* uniforms, int kmax, bool vec, FastWs ws, int* out_ids,
+                 int* out_greedy, float* out_probs, float* out_logprobs, int* out_status) {
+    hipLaunchKernelGGL((sample_fast_k<DT, COUNTS, MASK, LOGPROB>), grid, dim3(NT), 0, st, logits, stride, vocab, chunk, counts, mask,
+                       params, uniforms, kmax, vec, ws, out_ids, out_greedy, out_probs, out_logprobs, out_status);
+}
+
+template <int DT>
+void dispatch_fast(bool c, bool m, bool lp, dim3 grid, hipStream_t st, const void* logits, long long stride, int vocab, int chunk,
+                   const int* counts, const u32* mask, const RowParamsDev* params, const float* uniforms, int kmax, bool vec,
+                   FastWs ws, int* out_ids, int* out_greedy, float* out_probs, float* out_logprobs, int* out_status) {
+#define GBS_FAST(C, M, L)                                                                                                      \
+    launch_fast<DT, C, M, L>(grid, st, logits, stride, vocab, chunk, counts, mask, params, uniforms, kmax, vec, ws, out_ids,   \
+                             out_greedy, out_probs, out_logprobs, out_status)
+    if (c && m && lp) GBS_FAST(true, true, true);
+    else if (c && m) GBS_FAST(true, true, false);
+    else if (c && lp) GBS_FAST(true, false, true);
+    else if (c) GBS_FAST(true, false, false);
+    else if (m && lp) GBS_FAST(false, true, true);
+    else if (m) GBS_FAST(false, true, false);
+    else if (lp) GBS_FAST(false, false, true);
+    else GBS_FAST(false, false, false);
+#undef GBS_FAST
+}
+
+}  // namespace
+
+GBS_EXPORT size_t gbs_sample_workspace_bytes(int rows, int vocab, int kmax) {
+    if (rows <= 0 || vocab <= 0 || vocab > GBS_MAX_VOCAB || kmax < 0 || kmax > GBS_MAX_COUNT) return 0;
+    if (kmax == 0) return 0;  // the full-distribution path is not built yet
+    return fast_ws_bytes(rows, vocab, fast_splits(rows, vocab));
+}
+
+GBS_EXPORT int gbs_sample_rows(const void* logits, int dtype, int rows, int stride, int vocab, const int32_t* counts, const uint32_t* mask,
+                               const GbsRowParams* params, const float* uniforms, int kmax, int* out_ids, int* out_greedy,
+                               float* out_probs, float* out_logprobs, int* out_status, void* ws, size_t ws_bytes, void* stream) {
+    if (rows < 0 || vocab <= 0 || vocab > GBS_MAX_VOCAB || stride < vocab || kmax < 0 || kmax > GBS_MAX_COUNT) return GBS_ERR_INVALID;
+    if (dtype != GBS_DTYPE_F32 && dtype != GBS_DTYPE_BF16) return GBS_ERR_INVALID;
+    if (rows == 0) return 0;
+    if (kmax == 0) return GBS_ERR_INVALID;
+    if (rows > 65535 || !logits || !params || !uniforms || !out_ids || !ws || !aligned(ws, 256)) return GBS_ERR_INVALID;
+    const int S = fast_splits(rows, vocab);
+    if (ws_bytes < fast_ws_bytes(rows, vocab, S)) return GBS_ERR_INVALID;
+    int chunk = (vocab + S - 1) / S;
+    chunk = (chunk + 31) / 32 * 32;  // whole mask words per chunk
+    const size_t esz = dtype == GBS_DTYPE_F32 ? 4 : 2;
+    const bool vec = stride % 4 == 0 && vocab % 4 == 0 && aligned(logits, 4 * esz) && (!counts || aligned(counts, 16));
+    const dim3 grid(S, rows);
+    const FastWs w = fast_ws(ws, rows, S);
+    const hipStream_t st = to_stream(stream);
+    const RowParamsDev* p = (const RowParamsDev*)params;
+    if (dtype == GBS_DTYPE_F32)
+        dispatch_fast<GBS_DTYPE_F32>(counts != nullptr, mask != nullptr, out_logprobs != nullptr, grid, st, logits, stride, vocab, chunk,
+                                     counts, mask, p, uniforms, kmax, vec, w, out_ids, out_greedy, out_probs, out_logprobs,
+                                     out_status);
+    else
+        dispatch_fast<GBS_DTYPE_BF16>(counts != nullptr, mask != nullptr, out_logprobs != nullptr, grid, st, logits, stride, vocab,
+                                      chunk, counts, mask, p, uniforms, kmax, vec, w, out_ids, out_greedy, out_probs, out_logprobs,
+                                      out_status);
+    return launch_status();
+}

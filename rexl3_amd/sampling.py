@@ -1,0 +1,261 @@
+"""Host-side mirror of REXL3's sampler API over the MI355X library (include/gbs_sample.h).
+
+Names and argument meanings follow `gb_sampling` (crates/sampling/src/lib.rs:26-305) and `gb_spec`
+(crates/spec/src/lib.rs:30-35, crates/spec/src/tree.rs:417-438); every call runs on the GPU through the C ABI.
+PyTorch only provides device memory and the current stream.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from . import _lib
+
+MARGIN = 8  # crates/sampling/src/lib.rs:26
+TOP_K_CAP = 56  # crates/server/src/api.rs:43-44
+ROW_OK, ROW_NO_CANDIDATES, ROW_NAN_LOGIT, ROW_INVALID_PARAMS = 0, 1, 2, 3
+STATUS_NAMES = {0: "ok", 1: "NoCandidates", 2: "NanLogit", 3: "InvalidParams"}
+DTYPE_CODE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+
+KEYED_ROW_DTYPE = np.dtype([("seed", "<u8"), ("first_position", "<u8"), ("temperature", "<f8"), ("top_p", "<f8"),
+                            ("min_p", "<f8"), ("top_k", "<i4"), ("keyed", "<i4")])
+ROW_PARAMS_DTYPE = np.dtype([("temperature", "<f4"), ("top_p", "<f4"), ("min_p", "<f4"), ("repetition", "<f4"),
+                             ("presence", "<f4"), ("frequency", "<f4"), ("top_k", "<i4"), ("reserved", "<i4")])
+
+
+class SamplingError(Exception):
+    """crates/sampling/src/lib.rs:70-76."""
+
+
+@dataclass(frozen=True)
+class Sampling:
+    """crates/sampling/src/lib.rs:28-68."""
+
+    seed: int = 0
+    temperature: float = 1.0
+    top_k: int = 20
+    top_p: float = 0.95
+    min_p: float = 0.0
+
+    def candidate_count(self, vocab: int) -> int:
+        return vocab if self.top_k == 0 else min(self.top_k + MARGIN, vocab)
+
+    def validate(self) -> None:
+        if not math.isfinite(self.temperature) or self.temperature < 0.0:
+            raise SamplingError("invalid sampling parameters: temperature must be finite and >= 0")
+        if not math.isfinite(self.top_p) or not 0.0 <= self.top_p <= 1.0:
+            raise SamplingError("invalid sampling parameters: top_p must be in [0, 1]")
+        if not math.isfinite(self.min_p) or not 0.0 <= self.min_p <= 1.0:
+            raise SamplingError("invalid sampling parameters: min_p must be in [0, 1]")
+
+
+def _ptr(t):
+    return None if t is None else C.c_void_p(t.data_ptr())
+
+
+def _stream(device) -> C.c_void_p:
+    return C.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _require_cuda(t: torch.Tensor, name: str):
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a device tensor")
+
+
+class Workspace:
+    """Zero-initialised device workspaces, one per (device, purpose), grown on demand. The gbs_* entry points leave their
+    counters at zero after every call, so a workspace is cleared once when it is allocated."""
+
+    def __init__(self):
+        self._bufs = {}
+
+    def get(self, device: torch.device, purpose: str, nbytes: int) -> torch.Tensor:
+        key = (str(device), purpose)
+        buf = self._bufs.get(key)
+        if buf is None or buf.numel() < nbytes:
+            buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+            _lib.call("gbs_workspace_clear", _ptr(buf), buf.numel(), _stream(device))
+            self._bufs[key] = buf
+        return buf
+
+
+WORKSPACE = Workspace()
+
+
+# ------------------------------------------------------------------------------------------------ top-k drop-ins
+
+def topk_workspace_bytes(rows: int, valid: int, count: int, dtype: torch.dtype = torch.bfloat16, blocks: int = 1) -> int:
+    lib = _lib.load()
+    if dtype == torch.float32:
+        return rows * blocks * 8 * count * 8
+    if dtype == torch.float16:
+        return lib.gb_glm_topk_f16_workspace_bytes(rows, valid, count)
+    return lib.gb_topk_valid_workspace_bytes(rows, valid, count)
+
+
+def topk(logits: torch.Tensor, count: int, valid: int | None = None, blocks: int | None = None):
+    """Exact top-`count` per row by (value desc, id asc) (gb_topk_valid / gb_nemo_glue_topk / gb_glm_topk_f16).
+    Returns (ids int32 [rows, count], vals float32 [rows, count])."""
+    _require_cuda(logits, "logits")
+    rows, stride = logits.shape
+    valid = stride if valid is None else valid
+    dev = logits.device
+    ids = torch.empty((rows, count), dtype=torch.int32, device=dev)
+    vals = torch.empty((rows, count), dtype=torch.float32, device=dev)
+    st = _stream(dev)
+    if logits.dtype == torch.float32:
+        if valid != stride:
+            raise ValueError("the f32 top-k reads whole rows (valid == stride)")
+        if blocks is None:  # the reference's plan, crates/cuda/src/nemotron_glue.rs:172-176
+            blocks = max(1, min(48 // max(rows, 1), 16, -(-stride // 2048)))
+        wsb = rows * blocks * 8 * count * 8
+        ws = torch.empty(max(wsb, 8), dtype=torch.uint8, device=dev)
+        _lib.call("gb_nemo_glue_topk", _ptr(logits), rows, stride, count, blocks, _ptr(ws), wsb, _ptr(ids), _ptr(vals), st)
+    else:
+        lib = _lib.load()
+        f16 = logits.dtype == torch.float16
+        wsb = (lib.gb_glm_topk_f16_workspace_bytes if f16 else lib.gb_topk_valid_workspace_bytes)(rows, valid, count)
+        ws = torch.empty(max(wsb, 16), dtype=torch.uint8, device=dev)
+        name = "gb_glm_topk_f16" if f16 else "gb_topk_valid"
+        _lib.call(name, _ptr(logits), rows, stride, valid, count, _ptr(ids), _ptr(vals), _ptr(ws), wsb, st)
+    return ids, vals
+
+
+def keyed_rows(samplings, positions) -> np.ndarray:
+    """KeyedRow records (crates/cuda/csrc/glm_mtp.cu:258-264) for a list of Sampling and absolute positions."""
+    recs = np.zeros(len(samplings), dtype=KEYED_ROW_DTYPE)
+    for r, (s, p) in enumerate(zip(samplings, positions)):
+        recs[r] = (s.seed, p, s.temperature, s.top_p, s.min_p, s.top_k, 1)
+    return recs
+
+
+def keyed_pick(ids: torch.Tensor, vals: torch.Tensor, params: np.ndarray, depth: int = 0):
+    """gb_glm_keyed_pick: the keyed draw over each row's sorted candidates. Returns (ids [rows], vals [rows])."""
+    rows, count = ids.shape
+    dev = ids.device
+    p = torch.from_numpy(np.ascontiguousarray(params, dtype=KEYED_ROW_DTYPE).view(np.uint8)).to(dev)
+    oi = torch.empty(rows, dtype=torch.int32, device=dev)
+    ov = torch.empty(rows, dtype=torch.float32, device=dev)
+    _lib.call("gb_glm_keyed_pick", _ptr(ids), _ptr(vals), count, rows, _ptr(p), depth, _ptr(oi), _ptr(ov), _stream(dev))
+    return oi, ov
+
+
+def greedy_gather(ids: torch.Tensor, vals: torch.Tensor):
+    rows, count = ids.shape
+    dev = ids.device
+    oi = torch.empty(rows, dtype=torch.int32, device=dev)
+    ov = torch.empty(rows, dtype=torch.float32, device=dev)
+    _lib.call("gb_qfn_greedy_gather", _ptr(ids), _ptr(vals), count, rows, _ptr(oi), _ptr(ov), _stream(dev))
+    return oi, ov
+
+
+# ------------------------------------------------------------------------------------------------ fused keyed sampler
+
+def keyed_sample_rows(logits: torch.Tensor, params: np.ndarray | torch.Tensor, depth: int = 0, valid: int | None = None,
+                      out_vals: bool = False):
+    """gbs_keyed_sample_rows: per row, top-(top_k + 8) of the full row then `try_choose` at first_position + depth.
+    Returns (ids int32 [rows], status int32 [rows], vals float32 [rows] or None)."""
+    _require_cuda(logits, "logits")
+    rows, stride = logits.shape
+    valid = stride if valid is None else valid
+    dev = logits.device
+    if isinstance(params, np.ndarray):
+        params = torch.from_numpy(np.ascontiguousarray(params, dtype=KEYED_ROW_DTYPE).view(np.uint8)).to(dev)
+    oi = torch.empty(rows, dtype=torch.int32, device=dev)
+    os_ = torch.empty(rows, dtype=torch.int32, device=dev)
+    ov = torch.empty(rows, dtype=torch.float32, device=dev) if out_vals else None
+    wsb = _lib.load().gbs_keyed_sample_workspace_bytes(rows, valid)
+    ws = WORKSPACE.get(dev, "keyed", wsb)
+    _lib.call("gbs_keyed_sample_rows", _ptr(logits), DTYPE_CODE[logits.dtype], rows, stride, valid, _ptr(params), depth, _ptr(oi),
+              _ptr(ov), _ptr(os_), _ptr(ws), ws.numel(), _stream(dev))
+    return oi, os_, ov
+
+
+def choose_rows(logits: torch.Tensor, positions, s: Sampling, valid: int | None = None) -> list[int]:
+    """`choose_rows` (crates/sampling/src/lib.rs:269-280) over full logits rows: row r sampled at positions[r].
+    Raises SamplingError on a failed row, as `choose` panics."""
+    s.validate()
+    rows = logits.shape[0]
+    if len(positions) != rows:
+        raise SamplingError("choose_rows: values, ids and positions differ in length")
+    ids, st, _ = keyed_sample_rows(logits, keyed_rows([s] * rows, positions), 0, valid)
+    st = st.cpu().numpy()
+    bad = np.nonzero(st)[0]
+    if bad.size:
+        raise SamplingError(f"sampling failed: {STATUS_NAMES[int(st[bad[0]])]} (row {int(bad[0])})")
+    return [int(x) for x in ids.cpu().numpy()]
+
+
+# ------------------------------------------------------------------------------------------------ accept steps
+
+def accept(drafts: torch.Tensor, samples: torch.Tensor) -> torch.Tensor:
+    """Longest prefix with drafts == samples per sequence (crates/spec/src/lib.rs:30-35).
+    drafts int32 [n_seq, width], samples int32 [n_seq, width + 1] -> int32 [n_seq]."""
+    n_seq, width = drafts.shape
+    dev = samples.device
+    out = torch.empty(n_seq, dtype=torch.int32, device=dev)
+    _lib.call("gbs_accept", _ptr(drafts), _ptr(samples), n_seq, width, _ptr(out), _stream(dev))
+    return out
+
+
+def accept_tree(tokens: torch.Tensor, parents: torch.Tensor, samples: torch.Tensor):
+    """crates/spec/src/tree.rs:417-438 per tree: (path int32 [n_tree, nodes] padded with -1, path_len int32 [n_tree])."""
+    n_tree, nodes = tokens.shape
+    dev = tokens.device
+    path = torch.empty((n_tree, nodes), dtype=torch.int32, device=dev)
+    plen = torch.empty(n_tree, dtype=torch.int32, device=dev)
+    _lib.call("gbs_accept_tree", _ptr(tokens), _ptr(parents), _ptr(samples), n_tree, nodes, _ptr(path), _ptr(plen), _stream(dev))
+    return path, plen
+
+
+# ------------------------------------------------------------------------------------------------ extended pipeline
+
+def row_params(rows: int, temperature=1.0, top_p=1.0, min_p=0.0, repetition=1.0, presence=0.0, frequency=0.0,
+               top_k=0) -> np.ndarray:
+    p = np.zeros(rows, dtype=ROW_PARAMS_DTYPE)
+    p["temperature"], p["top_p"], p["min_p"] = temperature, top_p, min_p
+    p["repetition"], p["presence"], p["frequency"], p["top_k"] = repetition, presence, frequency, top_k
+    return p
+
+
+def sample_rows(logits: torch.Tensor, params: np.ndarray | torch.Tensor, uniforms: torch.Tensor, counts: torch.Tensor | None = None,
+                mask: torch.Tensor | None = None, kmax: int = 64, logprobs: bool = False, probs: bool = True):
+    """gbs_sample_rows. Returns a dict of device tensors: ids, greedy, status, and probs / logprobs when asked."""
+    _require_cuda(logits, "logits")
+    rows, stride = logits.shape
+    vocab = stride
+    dev = logits.device
+    if isinstance(params, np.ndarray):
+        params = torch.from_numpy(np.ascontiguousarray(params, dtype=ROW_PARAMS_DTYPE).view(np.uint8)).to(dev)
+    out = dict(ids=torch.empty(rows, dtype=torch.int32, device=dev), greedy=torch.empty(rows, dtype=torch.int32, device=dev),
+               status=torch.empty(rows, dtype=torch.int32, device=dev))
+    if probs:
+        out["probs"] = torch.empty(rows, dtype=torch.float32, device=dev)
+    if logprobs:
+        out["logprobs"] = torch.empty(rows, dtype=torch.float32, device=dev)
+    wsb = _lib.load().gbs_sample_workspace_bytes(rows, vocab, kmax)
+    ws = WORKSPACE.get(dev, "sample", wsb)
+    _lib.call("gbs_sample_rows", _ptr(logits), DTYPE_CODE[logits.dtype], rows, stride, vocab, _ptr(counts), _ptr(mask), _ptr(params),
+              _ptr(uniforms), kmax, _ptr(out["ids"]), _ptr(out["greedy"]), _ptr(out.get("probs")), _ptr(out.get("logprobs")),
+              _ptr(out["status"]), _ptr(ws), ws.numel(), _stream(dev))
+    return out
+
+
+def spec_verify(target: torch.Tensor, draft: torch.Tensor, draft_ids: torch.Tensor, temperatures: torch.Tensor,
+                u_accept: torch.Tensor, u_resample: torch.Tensor):
+    """gbs_spec_verify: (accepted int32 [n_seq], tokens int32 [n_seq, width + 1], status int32 [n_seq])."""
+    n_seq, width = draft_ids.shape
+    vocab = target.shape[-1]
+    dev = target.device
+    acc = torch.empty(n_seq, dtype=torch.int32, device=dev)
+    toks = torch.empty((n_seq, width + 1), dtype=torch.int32, device=dev)
+    st = torch.empty(n_seq, dtype=torch.int32, device=dev)
+    wsb = _lib.load().gbs_spec_verify_workspace_bytes(n_seq, width, vocab)
+    ws = WORKSPACE.get(dev, "spec", wsb)
+    _lib.call("gbs_spec_verify", _ptr(target), _ptr(draft), n_seq, width, vocab, _ptr(draft_ids), _ptr(temperatures), _ptr(u_accept),
+              _ptr(u_resample), _ptr(acc), _ptr(toks), _ptr(st), _ptr(ws), ws.numel(), _stream(dev))
+    return acc, toks, st

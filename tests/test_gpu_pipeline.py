@@ -1,0 +1,132 @@
+"""The extended pipeline (gbs_sample_rows) on the GPU against the oracle: token ids, greedy ids and statuses bit-exact;
+probabilities within 1e-5 relative; log-probabilities within 1e-5 relative (the oracle computes them in double)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from rexl3_amd import sampling as S
+from rexl3_amd import workloads as W
+from tests.gpu_util import dev, host, log, need_gpu
+
+pytestmark = pytest.mark.gpu
+RTOL = 1e-5
+
+
+def run_both(cfg, kmax=64, logprobs=True):
+    x = cfg["logits"]
+    is_bf16 = cfg["dtype"] == "bf16"
+    t = dev(x, torch.bfloat16) if is_bf16 else dev(x)
+    counts = None if cfg["counts"] is None else dev(cfg["counts"])
+    mask = None if cfg["mask"] is None else dev(cfg["mask"])
+    u = dev(cfg["uniforms"])
+    g = S.sample_rows(t, cfg["params"], u, counts, mask, kmax=kmax, logprobs=logprobs)
+    g = {k: host(v) for k, v in g.items()}
+    w = O.sample_rows(x, O.DTYPE_BF16 if is_bf16 else O.DTYPE_F32, cfg["counts"], cfg["mask"], cfg["params"], cfg["uniforms"],
+                      threads=8)
+    return g, w
+
+
+def compare(g, w, what):
+    assert np.array_equal(g["status"], w["status"]), f"{what}: status {np.nonzero(g['status'] != w['status'])[0][:10]}"
+    bad = np.nonzero(g["ids"] != w["ids"])[0]
+    assert bad.size == 0, f"{what}: ids differ at rows {bad[:10]} got {g['ids'][bad[:5]]} want {w['ids'][bad[:5]]}"
+    ok = w["status"] == 0
+    assert np.array_equal(g["greedy"][ok], w["greedy"][ok]), what
+    np.testing.assert_allclose(g["probs"][ok], w["probs"][ok], rtol=RTOL, atol=0, err_msg=what)
+    if "logprobs" in g:
+        fin = ok & np.isfinite(w["logprobs"])
+        np.testing.assert_allclose(g["logprobs"][fin], w["logprobs"][fin], rtol=RTOL, atol=1e-6, err_msg=what)
+
+
+def test_config1_single_row():
+    need_gpu()
+    for seed in range(1, 6):
+        cfg = W.config1(seed)
+        g, w = run_both(cfg)
+        compare(g, w, f"config1 seed {seed}")
+
+
+def test_config2_bf16_batched():
+    need_gpu()
+    cfg = W.config2()
+    g, w = run_both(cfg)
+    compare(g, w, "config2")
+    t0 = cfg["params"]["temperature"] == 0
+    assert np.array_equal(g["ids"][t0], g["greedy"][t0])
+
+
+def test_config4_grammar_masks():
+    need_gpu()
+    cfg = W.config4(rows=64)
+    g, w = run_both(cfg)
+    compare(g, w, "config4")
+    # rows that allow exactly one token return it for any uniform
+    m = cfg["mask"]
+    for r in range(8):
+        bits = np.unpackbits(m[r].view(np.uint8), bitorder="little")
+        assert g["ids"][r] == int(np.nonzero(bits)[0][0])
+        assert g["probs"][r] == 1.0
+
+
+def test_northstar_pipeline_penalties_and_mask():
+    need_gpu()
+    cfg = W.northstar(rows=32)
+    log("northstar rows=32")
+    g, w = run_both(cfg)
+    compare(g, w, "northstar")
+
+
+def test_edge_rows():
+    need_gpu()
+    rng = np.random.default_rng(9)
+    V, B = 5000, 16
+    x = rng.standard_normal((B, V)).astype(np.float32)
+    words = (V + 31) // 32
+    mask = np.full((B, words), 0xFFFFFFFF, dtype=np.uint32)
+    p = S.row_params(B, temperature=0.9, top_p=0.8, min_p=0.1, top_k=30, repetition=1.2, presence=0.2, frequency=0.1)
+    u = W.uniforms_f32(5, B)
+    counts = rng.integers(0, 3, (B, V)).astype(np.int32)
+    mask[0] = 0                       # nothing allowed
+    x[1, 77] = np.nan                 # NaN allowed -> NanLogit
+    x[2, 77] = np.nan
+    mask[2, 77 // 32] &= ~np.uint32(1 << (77 % 32))  # NaN masked out -> fine
+    p[3]["temperature"] = 0.0         # greedy
+    p[4]["top_k"] = 65                # breaks kmax
+    p[5]["temperature"] = -1.0        # invalid
+    u[6] = 1.0                        # invalid uniform
+    x[7, 100] = np.inf                # +inf maximum
+    x[7, 4000] = np.inf
+    mask[8] = 0
+    mask[8, 3] = 0b1011               # three allowed tokens < top_k
+    x[9, :] = 1.25                    # all equal
+    counts[9] = 0
+    p[10]["top_p"] = 1.0
+    p[10]["min_p"] = 0.0
+    u[11] = np.float32(0.99999994)    # largest uniform
+    u[12] = 0.0
+    x[13] = -x[13] * 1e-3             # tiny spread
+    x[14, :] = -0.0
+    x[14, 10] = 0.0
+    p[15]["top_k"] = 1
+    cfg = dict(logits=x, dtype="f32", params=p, uniforms=u, counts=counts, mask=mask)
+    g, w = run_both(cfg)
+    # row 4 breaks the kmax promise (top_k 65 > 64): the single-pass path refuses it; the oracle has no such limit
+    assert g["status"][4] == 3 and g["ids"][4] == -1 and w["status"][4] == 0
+    for k in ("status", "ids", "greedy", "probs", "logprobs"):
+        g[k] = np.delete(g[k], 4)
+        w[k] = np.delete(w[k], 4)
+    compare(g, w, "edges")
+    assert list(g["status"][:6]) == [1, 2, 0, 0, 3, 3]
+
+
+def test_kmax_and_rows_invariance():
+    need_gpu()
+    cfg = W.config4(rows=24)
+    g1, w = run_both(cfg, kmax=64)
+    compare(g1, w, "kmax 64")
+    x, u = dev(cfg["logits"]), dev(cfg["uniforms"])
+    m = dev(cfg["mask"])
+    for r in [0, 9, 23]:
+        one = S.sample_rows(x[r:r + 1].contiguous(), cfg["params"][r:r + 1], u[r:r + 1].contiguous(), None, m[r:r + 1].contiguous())
+        assert host(one["ids"])[0] == g1["ids"][r]

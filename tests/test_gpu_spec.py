@@ -1,0 +1,48 @@
+"""Speculative verification (gbs_spec_verify) on the GPU against the oracle: accepted lengths and tokens bit-exact."""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from rexl3_amd import sampling as S
+from rexl3_amd import workloads as W
+from tests.gpu_util import dev, host, log, need_gpu
+
+pytestmark = pytest.mark.gpu
+
+
+def run(cfg):
+    acc, toks, st = S.spec_verify(dev(cfg["target"]), dev(cfg["draft"]), dev(cfg["draft_ids"]), dev(cfg["temperatures"]),
+                                  dev(cfg["u_accept"]), dev(cfg["u_resample"]))
+    wa, wt, ws = O.spec_verify(cfg["target"], cfg["draft"], cfg["n_seq"], cfg["width"], cfg["draft_ids"], cfg["temperatures"],
+                               cfg["u_accept"], cfg["u_resample"], threads=8)
+    return (host(acc), host(toks), host(st)), (wa, wt, ws)
+
+
+def test_config5_small_vocab_many_sequences():
+    need_gpu()
+    cfg = W.config5(seed=21, n_seq=64, width=7, vocab=3000)
+    (a, t, s), (wa, wt, ws) = run(cfg)
+    assert np.array_equal(s, ws)
+    assert np.array_equal(a, wa)
+    assert np.array_equal(t, wt)
+    log(f"accepted lengths {np.bincount(a, minlength=8)}")
+
+
+def test_config5_full_vocab():
+    need_gpu()
+    cfg = W.config5(seed=5, n_seq=8, width=7)
+    (a, t, s), (wa, wt, ws) = run(cfg)
+    assert np.array_equal(s, ws) and np.array_equal(a, wa) and np.array_equal(t, wt)
+
+
+def test_spec_greedy_and_errors():
+    need_gpu()
+    cfg = W.config5(seed=3, n_seq=6, width=3, vocab=1000)
+    cfg["temperatures"][0:4] = 0.0        # sequence 0 greedy
+    cfg["draft_ids"][1, 1] = 1000          # invalid id
+    cfg["target"][2 * 4 + 2, 5] = np.nan   # NaN in sequence 2
+    cfg["u_resample"][3] = 1.0             # invalid
+    cfg["draft"][4 * 4 + 1, :] = -np.inf   # empty draft row
+    (a, t, s), (wa, wt, ws) = run(cfg)
+    assert list(ws) == [0, 3, 2, 3, 1, 0]
+    assert np.array_equal(s, ws) and np.array_equal(a, wa) and np.array_equal(t, wt)
