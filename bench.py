@@ -1,0 +1,242 @@
+"""Benchmark of the token-sampling hot path on one MI355X.
+
+Default workload (BASELINE.json's metric): the extended pipeline -- repetition/presence/frequency penalties over dense
+int32 counts, a u32 grammar bitmask, temperature, top-k 50 / top-p 0.9, fused max/log-sum-exp (log-probabilities on),
+inverse-CDF draw from one uniform per row -- at B=256, V=151,936 fp32, inputs resident in HBM. One step = one
+gbs_sample_rows launch over the batch. Prints one JSON line.
+
+    python bench.py [--steps K] [--warmup W] [--workload northstar|c1|c2|c4|c5|keyed] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "sampled rows/sec + achieved HBM GB/s at B=256, V=151936 fp32, 1 MI355X"
+HBM_PEAK_GBS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="northstar")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    return ap.parse_args()
+
+
+def algorithmic_bytes(rows, vocab, logit_bytes, counts, mask, extra=0):
+    per_row = logit_bytes * vocab + (4 * vocab if counts else 0) + (4 * ((vocab + 31) // 32) if mask else 0)
+    return rows * per_row + extra
+
+
+def time_launches(launch, steps, warmup):
+    import torch
+    for _ in range(warmup):
+        launch()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        launch()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps  # ms per step
+
+
+def cpu_baseline_sample(cfg, seconds, threads):
+    """The oracle's extended pipeline (the build's CPU restatement, there is no reference code for it) over the same
+    batch, repeated until `seconds` of wall time have passed."""
+    import numpy as np
+
+    from oracle import oracle as O
+    x = cfg["logits"]
+    dt = O.DTYPE_BF16 if cfg["dtype"] == "bf16" else O.DTYPE_F32
+    rows = x.shape[0]
+    done, t0 = 0, time.perf_counter()
+    while True:
+        O.sample_rows(x, dt, cfg["counts"], cfg["mask"], cfg["params"], cfg["uniforms"], threads=threads)
+        done += rows
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    return done / el, done, el
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: every box in this run has one, and the sampler shards by rows with no "
+              f"communication (see DESIGN.md). --gpus {args.gpus} is not supported.", file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    from rexl3_amd import _lib
+    from rexl3_amd import sampling as S
+    from rexl3_amd import workloads as W
+
+    lib = _lib.load()
+    dev = torch.device("cuda:0")
+    stream = C.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    wl = args.workload
+    threads = max(1, min(os.cpu_count() or 1, 16))
+    cpu = None
+
+    if wl in ("northstar", "c1", "c2", "c4"):
+        cfg = {"northstar": W.northstar, "c1": W.config1, "c2": W.config2, "c4": W.config4}[wl]()
+        x = cfg["logits"]
+        rows, vocab = x.shape
+        is_bf16 = cfg["dtype"] == "bf16"
+        xt = torch.from_numpy(x).to(dev)
+        if is_bf16:
+            xt = xt.view(torch.bfloat16)
+        ct = None if cfg["counts"] is None else torch.from_numpy(cfg["counts"]).to(dev)
+        mt = None if cfg["mask"] is None else torch.from_numpy(cfg["mask"]).to(dev)
+        pt = torch.from_numpy(np.ascontiguousarray(cfg["params"]).view(np.uint8)).to(dev)
+        ut = torch.from_numpy(cfg["uniforms"]).to(dev)
+        out = {k: torch.empty(rows, dtype=torch.int32 if k in ("ids", "greedy", "status") else torch.float32, device=dev)
+               for k in ("ids", "greedy", "status", "probs", "logprobs")}
+        wsb = lib.gbs_sample_workspace_bytes(rows, vocab, 64)
+        ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+        lib.gbs_workspace_clear(ws.data_ptr(), wsb, stream)
+        P = lambda t: None if t is None else C.c_void_p(t.data_ptr())  # noqa: E731
+        argv = (P(xt), 1 if is_bf16 else 0, rows, vocab, vocab, P(ct), P(mt), P(pt), P(ut), 64, P(out["ids"]), P(out["greedy"]),
+                P(out["probs"]), P(out["logprobs"]), P(out["status"]), P(ws), wsb, stream)
+        fn = lib.gbs_sample_rows
+
+        def launch():
+            rc = fn(*argv)
+            if rc:
+                raise RuntimeError(f"gbs_sample_rows returned {rc}")
+
+        ms = time_launches(launch, args.steps, args.warmup)
+        nbytes = algorithmic_bytes(rows, vocab, 2 if is_bf16 else 4, ct is not None, mt is not None)
+        kernel = "sample_fast_k"
+        dtype = "bf16->f32" if is_bf16 else "f32"
+        workload = {"northstar": "extended pipeline: penalties (dense i32 counts) + u32 grammar mask + T 0.8 + top-k 50 / top-p 0.9"
+                                 " + log-softmax + inverse-CDF draw",
+                    "c1": "config 1: single row, T 0.7, top-k 50, top-p 0.9",
+                    "c2": "config 2: bf16 batched, per-row T, top-k 40, top-p 0.95, min-p 0.05",
+                    "c4": "config 4: grammar mask, top-k 64, top-p 0.95"}[wl]
+        st = out["status"].cpu().numpy()
+        assert (st[cfg["params"]["temperature"] >= 0] >= 0).all()
+        if not args.no_cpu:
+            v, done, el = cpu_baseline_sample(cfg, args.cpu_seconds, threads)
+            v1, done1, el1 = cpu_baseline_sample({**cfg, "logits": cfg["logits"][:8], "counts": None if cfg["counts"] is None
+                                                  else cfg["counts"][:8], "mask": None if cfg["mask"] is None else cfg["mask"][:8],
+                                                  "params": cfg["params"][:8], "uniforms": cfg["uniforms"][:8]}, 2.0, 1)
+            cpu = {"value": round(v, 1), "unit": "rows/s", "cores": threads, "kind": "port",
+                   "sample": f"the build's C oracle of the same pipeline on the same {rows}-row batch, repeated for "
+                             f"{el:.1f} s ({done} rows) over {threads} threads; 1 thread: {v1:.1f} rows/s ({done1} rows)",
+                   "gbps": round(algorithmic_bytes(1, vocab, 2 if is_bf16 else 4, ct is not None, mt is not None) * v / 1e9, 3)}
+    elif wl == "keyed":
+        # the reference-parity keyed sampler: top-(k+8) of full f32 rows + try_choose, B=256, V=151,936
+        cfg = W.northstar()
+        x = cfg["logits"]
+        rows, vocab = x.shape
+        xt = torch.from_numpy(x).to(dev)
+        recs = S.keyed_rows([S.Sampling(seed=11, temperature=0.8, top_k=50, top_p=0.9, min_p=0.0)] * rows, list(range(rows)))
+        pt = torch.from_numpy(recs.view(np.uint8)).to(dev)
+        oi = torch.empty(rows, dtype=torch.int32, device=dev)
+        os_ = torch.empty(rows, dtype=torch.int32, device=dev)
+        wsb = lib.gbs_keyed_sample_workspace_bytes(rows, vocab)
+        ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+        lib.gbs_workspace_clear(ws.data_ptr(), wsb, stream)
+        argv = (C.c_void_p(xt.data_ptr()), 0, rows, vocab, vocab, C.c_void_p(pt.data_ptr()), 0, C.c_void_p(oi.data_ptr()), None,
+                C.c_void_p(os_.data_ptr()), C.c_void_p(ws.data_ptr()), wsb, stream)
+        fn = lib.gbs_keyed_sample_rows
+
+        def launch():
+            rc = fn(*argv)
+            if rc:
+                raise RuntimeError(f"gbs_keyed_sample_rows returned {rc}")
+
+        ms = time_launches(launch, args.steps, args.warmup)
+        nbytes = algorithmic_bytes(rows, vocab, 4, False, False)
+        kernel = "keyed_sample_k"
+        dtype = "f32 (choose in f64)"
+        workload = "keyed sampler (reference parity): exact top-58 of full rows + try_choose (T 0.8, top-k 50, top-p 0.9)"
+        if not args.no_cpu:
+            from oracle import oracle as O
+            t0 = time.perf_counter()
+            done = 0
+            while time.perf_counter() - t0 < args.cpu_seconds:
+                O.batch_keyed_sample(x, O.DTYPE_F32, vocab, recs, 0, threads=threads)
+                done += rows
+            el = time.perf_counter() - t0
+            cpu = {"value": round(done / el, 1), "unit": "rows/s", "cores": threads, "kind": "port",
+                   "sample": f"C restatement of the reference CPU path (try_top_candidates(row, 58) + try_choose) on the same "
+                             f"batch, {done} rows in {el:.1f} s over {threads} threads"}
+    elif wl == "c5":
+        cfg = W.config5()
+        n_seq, width = cfg["n_seq"], cfg["width"]
+        R, vocab = cfg["target"].shape
+        tt = torch.from_numpy(cfg["target"]).to(dev)
+        dt_ = torch.from_numpy(cfg["draft"]).to(dev)
+        di = torch.from_numpy(cfg["draft_ids"]).to(dev)
+        te = torch.from_numpy(cfg["temperatures"]).to(dev)
+        ua = torch.from_numpy(cfg["u_accept"]).to(dev)
+        ur = torch.from_numpy(cfg["u_resample"]).to(dev)
+        acc = torch.empty(n_seq, dtype=torch.int32, device=dev)
+        toks = torch.empty((n_seq, width + 1), dtype=torch.int32, device=dev)
+        stt = torch.empty(n_seq, dtype=torch.int32, device=dev)
+        wsb = lib.gbs_spec_verify_workspace_bytes(n_seq, width, vocab)
+        ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+        lib.gbs_workspace_clear(ws.data_ptr(), wsb, stream)
+        P = lambda t: C.c_void_p(t.data_ptr())  # noqa: E731
+        argv = (P(tt), P(dt_), n_seq, width, vocab, P(di), P(te), P(ua), P(ur), P(acc), P(toks), P(stt), P(ws), wsb, stream)
+        fn = lib.gbs_spec_verify
+
+        def launch():
+            rc = fn(*argv)
+            if rc:
+                raise RuntimeError(f"gbs_spec_verify returned {rc}")
+
+        ms = time_launches(launch, args.steps, args.warmup)
+        rows = R
+        nbytes = 2 * R * vocab * 4
+        kernel = "spec_max_k + spec_mass_k + spec_draw_k"
+        dtype = "f32 (integer masses)"
+        workload = "config 5: speculative verification, 32 sequences x (7 drafts + 1 bonus), rejection + residual resampling"
+    else:
+        raise SystemExit(f"unknown workload {wl}")
+
+    rows_per_s = rows / (ms / 1e3)
+    achieved = nbytes / (ms / 1e3) / 1e9
+    line = {
+        "metric": METRIC,
+        "value": round(rows_per_s, 1),
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": dtype,
+        "data": "synthetic: seeded splitmix64 logits (Box-Muller normals + peaks), Zipf(1.1) 4096-token count histories, "
+                "log-uniform grammar masks; resident in HBM before timing",
+        "config": {"workload": workload, "name": wl, "rows": rows, "vocab": vocab, "kernel": kernel},
+        "hbm_gbps": round(achieved, 1),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "bytes_per_launch": nbytes, "timing": "HIP events around the timed launches on their stream"},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -451,7 +451,7 @@ void gbo_keyed_pick_row(const int32_t* ids, const float* vals, int count, const 
     if (p->keyed && p->temperature > 0.0) {
         const int k = (p->top_k > 0 && p->top_k < count) ? p->top_k : count;
         GboSampling s = {p->seed, p->temperature, (uint64_t)k, p->top_p, p->min_p};
-        uint32_t uid[64];
+        uint32_t uid[64] = {0};
         for (int i = 0; i < k; ++i) uid[i] = (uint32_t)ids[i];
         uint32_t chosen = 0;
         if (gbo_try_choose(vals, uid, (size_t)k, p->first_position + (uint64_t)depth, &s, &chosen) == GBS_ROW_OK) {

@@ -19,6 +19,8 @@
 typedef uint64_t u64;
 typedef uint32_t u32;
 typedef uint16_t u16;
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 namespace gbs {
 
@@ -36,6 +38,12 @@ __device__ __forceinline__ u32 okey_f32(float f) {
     const u32 u = __float_as_uint(f);
     if ((u << 1) == 0u) return 0x80000000u;
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// okey_f32 in four operations: adding +0 turns -0 into +0 (and changes no other value), then the sign-flip map
+__device__ __forceinline__ u32 okey_f32_fast(float f) {
+    const u32 u = __float_as_uint(f + 0.0f);
+    return u ^ ((u32)((int)u >> 31) | 0x80000000u);
 }
 
 // inverse of okey_f32 (a zero comes back as +0)
@@ -83,6 +91,35 @@ __device__ __forceinline__ u64 shfl_xor64(u64 v, int m) {
     return ((u64)hi << 32) | lo;
 }
 
+// v of lane (lane ^ m), m a power of two below 64, without LDS: DPP within 16-lane rows (quad_perm for 1 and 2, row
+// rotations for 4 and 8), v_permlane16_swap / v_permlane32_swap across rows. m must be a compile-time constant after
+// unrolling.
+__device__ __forceinline__ u32 xor_lane(u32 v, int m) {
+    const int l = (int)__lane_id();
+    switch (m) {
+        case 1: return (u32)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false);   // quad_perm [1,0,3,2]
+        case 2: return (u32)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
+        case 4: {
+            const u32 down = (u32)__builtin_amdgcn_update_dpp(0, (int)v, 0x124, 0xF, 0xF, false);  // row_ror:4  -> lane - 4
+            const u32 up = (u32)__builtin_amdgcn_update_dpp(0, (int)v, 0x12C, 0xF, 0xF, false);    // row_ror:12 -> lane + 4
+            return (l & 4) ? down : up;
+        }
+        case 8: return (u32)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xF, 0xF, false);  // row_ror:8
+        case 16: {
+            const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+            return (l & 16) ? (u32)r[0] : (u32)r[1];
+        }
+        default: {
+            const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+            return (l & 32) ? (u32)r[0] : (u32)r[1];
+        }
+    }
+}
+
+__device__ __forceinline__ u64 xor_lane64(u64 v, int m) {
+    return ((u64)xor_lane((u32)(v >> 32), m) << 32) | xor_lane((u32)v, m);
+}
+
 __device__ __forceinline__ u64 shfl64(u64 v, int src) {
     const u32 lo = (u32)__shfl((int)(u32)v, src, WAVE);
     const u32 hi = (u32)__shfl((int)(u32)(v >> 32), src, WAVE);
@@ -117,7 +154,7 @@ __device__ __forceinline__ u64 wave_sort_desc(u64 v) {
     for (int k = 2; k <= WAVE; k <<= 1) {
 #pragma unroll
         for (int j = k >> 1; j > 0; j >>= 1) {
-            const u64 o = shfl_xor64(v, j);
+            const u64 o = xor_lane64(v, j);
             const bool lower = (l & j) == 0;
             const bool desc = (l & k) == 0;
             const bool keep_max = (lower == desc);
@@ -127,28 +164,14 @@ __device__ __forceinline__ u64 wave_sort_desc(u64 v) {
     return v;
 }
 
-// the 64 largest of two descending lists (one key per lane each), descending
-__device__ __forceinline__ u64 wave_merge_desc(u64 a, u64 b_desc) {
-    const int l = lane_id();
-    const u64 br = shfl64(b_desc, WAVE - 1 - l);
-    u64 v = a > br ? a : br;  // bitonic
-#pragma unroll
-    for (int j = WAVE / 2; j > 0; j >>= 1) {
-        const u64 o = shfl_xor64(v, j);
-        const bool lower = (l & j) == 0;
-        v = lower ? (v > o ? v : o) : (v < o ? v : o);
-    }
-    return v;
-}
-
-// ascending bitonic sort of one u64 per lane
+// ascending bitonic sort of one u64 per lane (lane 0 ends with the smallest)
 __device__ __forceinline__ u64 wave_sort_asc(u64 v) {
     const int l = lane_id();
 #pragma unroll
     for (int k = 2; k <= WAVE; k <<= 1) {
 #pragma unroll
         for (int j = k >> 1; j > 0; j >>= 1) {
-            const u64 o = shfl_xor64(v, j);
+            const u64 o = xor_lane64(v, j);
             const bool lower = (l & j) == 0;
             const bool asc = (l & k) == 0;
             const bool keep_min = (lower == asc);
@@ -156,6 +179,38 @@ __device__ __forceinline__ u64 wave_sort_asc(u64 v) {
         }
     }
     return v;
+}
+
+// descending bitonic clean-up of a bitonic sequence
+__device__ __forceinline__ u64 wave_bitonic_desc(u64 v) {
+    const int l = lane_id();
+#pragma unroll
+    for (int j = WAVE / 2; j > 0; j >>= 1) {
+        const u64 o = xor_lane64(v, j);
+        const bool lower = (l & j) == 0;
+        v = lower ? (v > o ? v : o) : (v < o ? v : o);
+    }
+    return v;
+}
+
+// the 64 largest of a descending list and an ascending list (one key per lane each), descending
+__device__ __forceinline__ u64 wave_merge_desc_asc(u64 a_desc, u64 b_asc) { return wave_bitonic_desc(a_desc > b_asc ? a_desc : b_asc); }
+
+// the 64 largest of two descending lists, descending
+__device__ __forceinline__ u64 wave_merge_desc(u64 a, u64 b_desc) {
+    const u64 br = shfl64(b_desc, WAVE - 1 - lane_id());
+    return wave_bitonic_desc(a > br ? a : br);
+}
+
+// the k-th largest (1 <= k <= 64) of one u32 per lane: the largest r with at least k lanes holding a value >= r
+__device__ __forceinline__ u32 wave_kth_largest(u32 v, int k) {
+    u32 r = 0;
+#pragma unroll
+    for (int b = 31; b >= 0; --b) {
+        const u32 c = r | (1u << b);
+        if (__popcll(ballot(v >= c)) >= k) r = c;
+    }
+    return r;
 }
 
 __device__ __forceinline__ u64 wave_sum_u64(u64 v) {
@@ -188,16 +243,57 @@ template <int BUF>
 struct WaveTop {
     u64 list;  // rank lane_id()
     u64 thr;   // key of rank count - 1 (wave-uniform); keys <= thr are dropped
+    u32 gate;  // order values below the gate cannot pass: (thr >> 32) + (low word of thr all ones)
     int n;     // buffered keys (wave-uniform)
     int count;
     u64* buf;
 
-    __device__ __forceinline__ void init(u64* b, int cnt, u64 floor_key) {
+    __device__ __forceinline__ void set_thr(u64 t) {
+        thr = t;
+        const u32 hi = (u32)(t >> 32);
+        gate = ((u32)t == 0xFFFFFFFFu && hi != 0xFFFFFFFFu) ? hi + 1u : hi;
+    }
+
+    // Optional sharing of the gate: every wave's `count`-th key is a lower bound of the count-th key of its whole row,
+    // so waves publish it to a block-wide LDS slot and a row-wide device slot (atomic max) and raise their own gate
+    // to the largest published value.
+    u64* s_shared;  // LDS, block-wide (may be null)
+    u64* g_shared;  // device memory, row-wide (may be null)
+    u64 g_seen;
+
+    __device__ __forceinline__ void init(u64* b, int cnt, u64 floor_key, u64* sh = nullptr, u64* gsh = nullptr) {
         list = 0;
-        thr = floor_key;
+        set_thr(floor_key);
         n = 0;
         count = cnt;
         buf = b;
+        s_shared = sh;
+        g_shared = gsh;
+        g_seen = 0;
+    }
+
+    __device__ __forceinline__ void publish() {
+        if (lane_id() == 0) {
+            if (s_shared) __hip_atomic_fetch_max(s_shared, thr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            if (g_shared && thr > g_seen) __hip_atomic_fetch_max(g_shared, thr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+
+    // Read the shared bounds (relaxed; a stale value is still a valid bound) into `pend_*`; apply_shared() raises the
+    // gate with them later. Issued before a step's data loads and applied one step later, the device read never makes
+    // the wave wait on loads it does not need yet.
+    u64 pend_l = 0, pend_g = 0;
+
+    __device__ __forceinline__ void prefetch_shared() {
+        if (g_shared) pend_g = __hip_atomic_load(g_shared, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (s_shared) pend_l = __hip_atomic_load(s_shared, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+
+    __device__ __forceinline__ void apply_shared() {
+        g_seen = pend_g;
+        u64 t = pend_l > pend_g ? pend_l : pend_g;
+        t = readlane64(t, 0);
+        if (t > thr) set_thr(t);
     }
 
     // offer one key per lane (any lane may offer a key that fails the gate)
@@ -206,6 +302,17 @@ struct WaveTop {
         const u64 m = ballot(pass);
         if (m) {
             if (pass) buf[n + mbcnt(m)] = k;
+            n += __popcll(m);
+        }
+    }
+
+    // offer element `id` of order value `ok`. The cheap 32-bit gate lets ties of the gate value through; the merge is
+    // exact, so a key that passes needlessly only costs a slot.
+    __device__ __forceinline__ void offer_ok(u32 ok, u32 id, bool valid = true) {
+        const bool pass = valid && ok >= gate;
+        const u64 m = ballot(pass);
+        if (m) {
+            if (pass) buf[n + mbcnt(m)] = make_key(ok, id);
             n += __popcll(m);
         }
     }
@@ -220,38 +327,98 @@ struct WaveTop {
             const int base = n - take;
             u64 g = l < take ? buf[base + l] : 0ull;
             n = base;
-            g = wave_sort_desc(g);
-            list = wave_merge_desc(list, g);
+            g = wave_sort_asc(g);
+            list = wave_merge_desc_asc(list, g);
             const u64 t = readlane64(list, count - 1);
-            thr = t > thr ? t : thr;
+            if (t > thr) set_thr(t);
         }
+        publish();
         wave_lds_sync();
+    }
+
+    // Raise the gate from a sample: `ok` is one order value (key high word) per lane, of elements that will all be
+    // offered. At least `count` of them are >= their count-th largest, so every key below that value is out.
+    __device__ __forceinline__ void seed(u32 ok) {
+        const u32 r = wave_kth_largest(ok, count);
+        if (r > 0u) {
+            const u64 t = ((u64)r << 32) - 1ull;
+            if (t > thr) {
+                set_thr(t);
+                publish();
+            }
+        }
     }
 
     __device__ __forceinline__ void merge_sorted(u64 g_desc) {
         list = wave_merge_desc(list, g_desc);
         const u64 t = readlane64(list, count - 1);
-        thr = t > thr ? t : thr;
+        if (t > thr) set_thr(t);
     }
 };
 
 // ------------------------------------------------------------------------------------------------ cross-block hand-off
+//
+// Blocks of one row hand their partial results to the row's last block through device memory. The partials are
+// written and read as relaxed atomics at agent scope (write-through, and reads that bypass the XCD-local L2), and each
+// writer waits for its stores to complete before the block counts its arrival. This needs no L2 write-back or
+// invalidation: a release/acquire fence at agent scope would write back and invalidate the whole L2 of the XCD in
+// every block, which costs more than the streaming itself.
 
-// Release this block's global writes and count its arrival at `counter`; true in every thread of the block that
-// arrives last (which then sees every other block's writes). The last block resets the counter to 0.
+template <typename T>
+__device__ __forceinline__ void st_agent(T* p, T v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <typename T>
+__device__ __forceinline__ T ld_agent(const T* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void st_agent_f2(float2* p, float2 v) {
+    st_agent((u64*)p, ((u64)__float_as_uint(v.y) << 32) | __float_as_uint(v.x));
+}
+
+__device__ __forceinline__ float2 ld_agent_f2(const float2* p) {
+    const u64 b = ld_agent((const u64*)p);
+    return make_float2(__uint_as_float((u32)b), __uint_as_float((u32)(b >> 32)));
+}
+
+// Count this block's arrival at `counter` after its agent-scope stores have completed; true in every thread of the
+// block that arrives last. The last block resets the counter to 0 for the next launch.
 __device__ __forceinline__ bool arrive_last(unsigned* counter, unsigned expected, unsigned* s_flag) {
-    __threadfence();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);  // every store of this thread has completed
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __syncthreads();
     if (threadIdx.x == 0) {
-        const unsigned prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const bool last = prev == expected - 1;
         if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         *s_flag = last ? 1u : 0u;
     }
     __syncthreads();
-    const bool last = *s_flag != 0u;
-    if (last) __threadfence();
-    return last;
+    return *s_flag != 0u;
+}
+
+// The last block's merge of `nl` descending 64-key lists at lists[i * 64 + lane] (agent-scope reads): each wave merges
+// every NW-th list with the next list's load in flight, then wave 0 merges the waves' results. Returns the merged
+// list in wave 0 (other waves: unspecified). All threads of the block call it. s_list: NW x 64 keys of LDS.
+template <int NW>
+__device__ __forceinline__ u64 block_merge_lists(const u64* lists, int nl, u64 (*s_list)[WAVE]) {
+    const int w = threadIdx.x / WAVE, l = lane_id();
+    u64 acc = 0;
+    u64 nxt = w < nl ? ld_agent(&lists[(size_t)w * WAVE + l]) : 0ull;
+    for (int o = w; o < nl; o += NW) {
+        const u64 cur = nxt;
+        nxt = o + NW < nl ? ld_agent(&lists[(size_t)(o + NW) * WAVE + l]) : 0ull;
+        acc = wave_merge_desc(acc, cur);
+    }
+    __syncthreads();
+    s_list[w][l] = acc;
+    __syncthreads();
+    if (w == 0)
+        for (int o = 1; o < NW; ++o) acc = wave_merge_desc(acc, s_list[o][l]);
+    return acc;
 }
 
 }  // namespace gbs

@@ -1,6 +1,8 @@
 // Block-level exact selection over a chunk of one logits row (f32 / bf16 / fp16), shared by the top-k drop-ins and
 // the fused keyed sampler. See gbs_common.hpp for the key order and the wave lists.
 #pragma once
+#include <type_traits>
+
 #include "gbs_common.hpp"
 
 namespace gbs {
@@ -8,7 +10,7 @@ namespace sel {
 
 constexpr int NT = 256;
 constexpr int NW = NT / WAVE;
-constexpr int BUF = 2 * WAVE;  // < 64 keys left after a flush + one key per lane
+constexpr int BUF = WAVE * (4 * 4 + 1);  // < 64 keys left after a flush + 16 keys per lane of one step
 
 enum { DT_F32 = 0, DT_BF16 = 1, DT_F16 = 2 };
 
@@ -19,54 +21,86 @@ __device__ __forceinline__ u32 elem_key(const void* row, int e) {
     return okey_16<true>(((const u16*)row)[e]);
 }
 
-// four order keys (high words) of elements e..e+3; `vec` = 16-byte (f32) / 8-byte (16-bit) loads are legal
+constexpr int SEL_GROUPS = 4;  // 4-element groups per lane per step of the main loop
+
 template <int DT>
-__device__ __forceinline__ void load_group(const void* row, int e, int hi, bool vec, u32 (&k)[4], bool (&in)[4]) {
-    if (vec && e + 4 <= hi) {
-        if (DT == DT_F32) {
-            const float4 v = *(const float4*)((const float*)row + e);
-            k[0] = okey_f32_nanlow(v.x); k[1] = okey_f32_nanlow(v.y); k[2] = okey_f32_nanlow(v.z); k[3] = okey_f32_nanlow(v.w);
-        } else {
-            const uint2 v = *(const uint2*)((const u16*)row + e);
-            k[0] = okey_16<DT == DT_F16>(v.x); k[1] = okey_16<DT == DT_F16>(v.x >> 16);
-            k[2] = okey_16<DT == DT_F16>(v.y); k[3] = okey_16<DT == DT_F16>(v.y >> 16);
-        }
+struct SelRaw {
+    typename std::conditional<DT == DT_F32, u32x4, u32x2>::type x[SEL_GROUPS];
+};
+
+template <int DT>
+__device__ __forceinline__ void sel_load(const void* row, int e, SelRaw<DT>& r) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) in[q] = true;
-    } else {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            in[q] = e + q < hi;
-            k[q] = in[q] ? elem_key<DT>(row, e + q) : 0u;
-        }
+    for (int j = 0; j < SEL_GROUPS; ++j) {
+        const int eg = e + j * NT * 4;
+        if constexpr (DT == DT_F32) r.x[j] = __builtin_nontemporal_load((const u32x4*)((const float*)row + eg));
+        else r.x[j] = __builtin_nontemporal_load((const u32x2*)((const u16*)row + eg));
     }
 }
 
-// Streams [lo, hi) of `row` (block-cyclic 4-element groups) through the block's wave lists; leaves the block's best 64
-// (sorted, best first) in wave 0's `list`. `count` <= 64.
+template <int DT>
+__device__ __forceinline__ void sel_keys(const SelRaw<DT>& r, int j, u32 (&k)[4]) {
+    if constexpr (DT == DT_F32) {
+        const u32x4 v = r.x[j];
+        k[0] = okey_f32_nanlow(__uint_as_float(v.x)); k[1] = okey_f32_nanlow(__uint_as_float(v.y));
+        k[2] = okey_f32_nanlow(__uint_as_float(v.z)); k[3] = okey_f32_nanlow(__uint_as_float(v.w));
+    } else {
+        const u32x2 v = r.x[j];
+        k[0] = okey_16<DT == DT_F16>(v.x); k[1] = okey_16<DT == DT_F16>(v.x >> 16);
+        k[2] = okey_16<DT == DT_F16>(v.y); k[3] = okey_16<DT == DT_F16>(v.y >> 16);
+    }
+}
+
+// Streams [lo, hi) of `row` through the block's wave lists; leaves the block's best 64 (sorted, best first) in wave 0's
+// `list`. Main loop: SEL_GROUPS 4-element groups per lane per step, every one in bounds, the next step's loads issued
+// before the current step is ranked; then a guarded tail of one group per lane per round. `count` <= 64.
 template <int DT>
 __device__ void block_select(const void* row, int lo, int hi, bool vec, int count, WaveTop<BUF>& wt, u64 (*s_list)[WAVE]) {
     const int tid = threadIdx.x;
     const int w = tid / WAVE;
-    const int step = NT * 4;
-    int e = lo + tid * 4;
-    u32 k[4], kn[4];
-    bool in[4], inn[4];
-    load_group<DT>(row, e, hi, vec, k, in);
-    // every lane of a wave runs the same number of steps: lanes past the end offer nothing
-    const int wave_first = lo + w * WAVE * 4;
-    const int nsteps = wave_first < hi ? (hi - wave_first + step - 1) / step : 0;
-    for (int s = 0; s < nsteps; ++s) {
-        const int en = e + step;
-        load_group<DT>(row, en, hi, vec, kn, inn);
+    int e0 = lo;
+    if (vec) {
+        const int step = NT * 4 * SEL_GROUPS;
+        const int nfull = (hi - lo) / step;
+        if (nfull > 0) {
+            SelRaw<DT> cur, nxt;
+            int e = lo + tid * 4;
+            sel_load<DT>(row, e, cur);
+            {
+                u32 m = 0;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) wt.offer(in[q] ? make_key(k[q], (u32)(e + q)) : 0ull), wt.flush(false);
+                for (int j = 0; j < SEL_GROUPS; ++j) {
+                    u32 k[4];
+                    sel_keys<DT>(cur, j, k);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            k[q] = kn[q];
-            in[q] = inn[q];
+                    for (int q = 0; q < 4; ++q) m = k[q] > m ? k[q] : m;
+                }
+                wt.seed(m);
+            }
+            for (int s = 0; s < nfull; ++s) {
+                const int en = s + 1 < nfull ? e + step : e;
+                sel_load<DT>(row, en, nxt);
+#pragma unroll
+                for (int j = 0; j < SEL_GROUPS; ++j) {
+                    u32 k[4];
+                    sel_keys<DT>(cur, j, k);
+                    const int eg = e + j * NT * 4;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) wt.offer_ok(k[q], (u32)(eg + q));
+                }
+                wt.flush(false);
+                cur = nxt;
+                e = en;
+            }
         }
-        e = en;
+        e0 = lo + nfull * step;
+    }
+    const int rounds = (hi - e0 + NT * 4 - 1) / (NT * 4);
+    for (int r = 0; r < rounds; ++r) {
+        const int eg = e0 + r * NT * 4 + tid * 4;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) wt.offer_ok(eg + q < hi ? elem_key<DT>(row, eg + q) : 0u, (u32)(eg + q), eg + q < hi);
+        wt.flush(false);
     }
     wt.flush(true);
     s_list[w][lane_id()] = wt.list;

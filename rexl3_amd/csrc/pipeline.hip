@@ -7,6 +7,8 @@
 // and offers the keys to its wave's gated top list. The block's lists, LSE and NaN flag go to the workspace; the last
 // block of the row merges them and finishes the row on one wave: masses of the <= 64 candidates, the exact top-p and
 // min-p cuts, and the draw in ascending id order.
+#include <type_traits>
+
 #include "gbs_modeu.hpp"
 
 using namespace gbs;
@@ -16,7 +18,7 @@ namespace {
 
 constexpr int NT = 256;
 constexpr int NW = NT / WAVE;
-constexpr int GROUPS = 2;                  // 4-element groups per lane per step
+constexpr int GROUPS = 4;  // 4-element groups per lane per step of the main loop
 constexpr int BUF = WAVE * (GROUPS * 4 + 1);
 constexpr u64 FLOOR_KEY = ((u64)NEG_INF_KEY << 32) | 0xFFFFFFFFull;  // every -inf key is at or below it
 
@@ -35,14 +37,15 @@ int fast_splits(int rows, int vocab) {
 
 struct FastWs {
     unsigned* counters;  // [rows]
+    u64* row_thr;        // [rows] the row's shared gate, reset by the row's last block
     u64* lists;          // [rows][S][64]
     Lse* lse;            // [rows][S]
     unsigned* nan;       // [rows][S]
 };
 
 size_t fast_ws_bytes(int rows, int vocab, int S) {
-    return align256((size_t)rows * 4) + align256((size_t)rows * S * WAVE * 8) + align256((size_t)rows * S * sizeof(Lse)) +
-           align256((size_t)rows * S * 4);
+    return align256((size_t)rows * 4) + align256((size_t)rows * 8) + align256((size_t)rows * S * WAVE * 8) +
+           align256((size_t)rows * S * sizeof(Lse)) + align256((size_t)rows * S * 4);
 }
 
 FastWs fast_ws(void* ws, int rows, int S) {
@@ -50,6 +53,8 @@ FastWs fast_ws(void* ws, int rows, int S) {
     FastWs w;
     w.counters = (unsigned*)p;
     p += align256((size_t)rows * 4);
+    w.row_thr = (u64*)p;
+    p += align256((size_t)rows * 8);
     w.lists = (u64*)p;
     p += align256((size_t)rows * S * WAVE * 8);
     w.lse = (Lse*)p;
@@ -58,13 +63,45 @@ FastWs fast_ws(void* ws, int rows, int S) {
     return w;
 }
 
+// One step of the main loop: GROUPS 4-element groups per lane, raw (unconverted) so that nothing waits on a load
+// until the group is processed, one step later.
 template <int DT>
-__device__ __forceinline__ void load_x4(const void* row, int e, float (&x)[4]) {
-    if (DT == GBS_DTYPE_F32) {
-        const float4 v = *(const float4*)((const float*)row + e);
-        x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
+struct RawStep {
+    typename std::conditional<DT == GBS_DTYPE_F32, u32x4, u32x2>::type x[GROUPS];
+    u32x4 c[GROUPS];
+    u32 m[GROUPS];
+};
+
+// Buffer resources of one row: the base is the row, out-of-range reads return zeros (never used: the main loop only
+// covers whole in-range steps). Offsets are in bytes; the per-group offsets are scalar, so a step's loads cost one
+// vector address add per array.
+struct RowRsrc {
+    __amdgpu_buffer_rsrc_t x, c, m;
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, u32 bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+template <int DT, bool COUNTS, bool MASK>
+__device__ __forceinline__ void load_step(const RowRsrc& R, u32 e, RawStep<DT>& r) {
+    constexpr u32 ESZ = DT == GBS_DTYPE_F32 ? 4 : 2;
+#pragma unroll
+    for (int j = 0; j < GROUPS; ++j) {
+        if constexpr (DT == GBS_DTYPE_F32) r.x[j] = __builtin_amdgcn_raw_buffer_load_b128(R.x, e * ESZ, j * NT * 4 * ESZ, 0);
+        else r.x[j] = __builtin_amdgcn_raw_buffer_load_b64(R.x, e * ESZ, j * NT * 4 * ESZ, 0);
+        if constexpr (COUNTS) r.c[j] = __builtin_amdgcn_raw_buffer_load_b128(R.c, e * 4, j * NT * 16, 0);
+        if constexpr (MASK) r.m[j] = __builtin_amdgcn_raw_buffer_load_b32(R.m, (e >> 5) * 4, j * NT * 4 / 8, 0);
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ void unpack_x(const RawStep<DT>& r, int j, float (&x)[4]) {
+    if constexpr (DT == GBS_DTYPE_F32) {
+        const u32x4 v = r.x[j];
+        x[0] = __uint_as_float(v.x); x[1] = __uint_as_float(v.y); x[2] = __uint_as_float(v.z); x[3] = __uint_as_float(v.w);
     } else {
-        const uint2 v = *(const uint2*)((const u16*)row + e);
+        const u32x2 v = r.x[j];
         x[0] = __uint_as_float(v.x << 16); x[1] = __uint_as_float(v.x & 0xFFFF0000u);
         x[2] = __uint_as_float(v.y << 16); x[3] = __uint_as_float(v.y & 0xFFFF0000u);
     }
@@ -74,39 +111,6 @@ template <int DT>
 __device__ __forceinline__ float load_x1(const void* row, int e) {
     if (DT == GBS_DTYPE_F32) return ((const float*)row)[e];
     return __uint_as_float((u32)((const u16*)row)[e] << 16);
-}
-
-struct Group {
-    float x[4];
-    int c[4];
-    u32 mbits;  // the 4 mask bits of the group, bit q = element q
-    bool in[4];
-};
-
-template <int DT, bool COUNTS, bool MASK>
-__device__ __forceinline__ void load_group(const void* row, const int* crow, const u32* mrow, int e, int hi, bool vec, Group& g) {
-    if (vec && e + 4 <= hi) {
-        load_x4<DT>(row, e, g.x);
-        if (COUNTS) {
-            const int4 c = *(const int4*)(crow + e);
-            g.c[0] = c.x; g.c[1] = c.y; g.c[2] = c.z; g.c[3] = c.w;
-        }
-#pragma unroll
-        for (int q = 0; q < 4; ++q) g.in[q] = true;
-    } else {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            g.in[q] = e + q < hi;
-            g.x[q] = g.in[q] ? load_x1<DT>(row, e + q) : 0.f;
-            if (COUNTS) g.c[q] = g.in[q] ? crow[e + q] : 0;
-        }
-    }
-    if (!COUNTS) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) g.c[q] = 0;
-    }
-    g.mbits = 0xFu;
-    if (MASK) g.mbits = (e < hi) ? (mrow[e >> 5] >> (e & 31)) & 0xFu : 0u;
 }
 
 // The row's finish, on one wave. `list` holds the row's best 64 keys (lane = rank).
@@ -191,8 +195,11 @@ __global__ void __launch_bounds__(NT) sample_fast_k(const void* __restrict__ log
     __shared__ Lse s_lse[NW];
     __shared__ unsigned s_nan[NW];
     __shared__ unsigned s_flag;
+    __shared__ u64 s_thr;
     const int S = gridDim.x, sp = blockIdx.x, r = blockIdx.y;
     const int tid = threadIdx.x, w = tid / WAVE, l = lane_id();
+    if (tid == 0) s_thr = 0;
+    __syncthreads();
     const size_t esz = DT == GBS_DTYPE_F32 ? 4 : 2;
     const void* row = (const char*)logits + (size_t)r * (size_t)stride * esz;
     const int* crow = COUNTS ? counts + (size_t)r * vocab : nullptr;
@@ -207,51 +214,127 @@ __global__ void __launch_bounds__(NT) sample_fast_k(const void* __restrict__ log
     const int hi = min(vocab, lo + chunk);
 
     WaveTop<BUF> wt;
-    wt.init(s_buf[w], count, FLOOR_KEY);
-    bool nan = false;
+    wt.init(s_buf[w], count, FLOOR_KEY, &s_thr, nullptr);
     Lse lse{-INFINITY, 0.f};
 
-    const int step = NT * 4 * GROUPS;
-    const int wave_first = lo + w * WAVE * 4;
-    const int nsteps = wave_first < hi ? (hi - lo - w * WAVE * 4 + step - 1) / step : 0;
-    Group g[GROUPS], gn[GROUPS];
-    int e = lo + tid * 4;
-#pragma unroll
-    for (int j = 0; j < GROUPS; ++j) load_group<DT, COUNTS, MASK>(row, crow, mrow, e + j * NT * 4, hi, vec, g[j]);
-    for (int s = 0; s < nsteps; ++s) {
-        const int en = e + step;
-        if (s + 1 < nsteps) {
-#pragma unroll
-            for (int j = 0; j < GROUPS; ++j) load_group<DT, COUNTS, MASK>(row, crow, mrow, en + j * NT * 4, hi, vec, gn[j]);
+    // the penalised logit of one element, in the operation order of the definition:
+    // c > 0: (x > 0 ? x * rinv : x * rep) - ((float)c * freq + pres); otherwise x.
+    auto penalized = [&](float x, int c) {
+        float v = x;
+        if (COUNTS) {
+            if (c > 0) {
+                const float a = x > 0.0f ? x * rinv : x * p.repetition;
+                v = a - ((float)c * p.frequency + p.presence);
+            }
         }
+        return v;
+    };
+    auto logit = [&](float x, int c, u32 mbit) {
+        const float v = penalized(x, c);
+        return mbit ? v : -INFINITY;
+    };
+    u32 nanv = 0;  // per lane: a NaN was seen
+    const float lse_c = clp;
+    // one 4-element group: penalties, mask, NaN flag, keys offered to the wave list, online log-sum-exp.
+    // The mask is applied with a bitfield insert: bfe_i32 of the element's bit is all ones or all zeros.
+    auto group = [&](const float (&x)[4], const int (&c)[4], u32 mbits, int eg) {
+        float lv[4];
 #pragma unroll
-        for (int j = 0; j < GROUPS; ++j) {
-            const int eg = e + j * NT * 4;
-            float lv[4];
+        for (int q = 0; q < 4; ++q) {
+            const float v = penalized(x[q], c[q]);
+            const u32 keep = (u32)__builtin_amdgcn_sbfe((int)mbits, q, 1);
+            lv[q] = __uint_as_float((__float_as_uint(v) & keep) | (0xFF800000u & ~keep));
+        }
+        nanv |= (__builtin_isunordered(lv[0], lv[1]) | __builtin_isunordered(lv[2], lv[3])) ? 1u : 0u;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) wt.offer_ok(okey_f32_fast(lv[q]), (u32)(eg + q));
+        if (LOGPROB) {
+            const float gm = fmaxf(fmaxf(lv[0], lv[1]), fmaxf(lv[2], lv[3]));
+            if (gm > lse.m) {
+                lse.s = lse.m == -INFINITY ? 0.f : lse.s * __builtin_amdgcn_exp2f((lse.m - gm) * lse_c);
+                lse.m = gm;
+            }
+            if (lse.m != -INFINITY) {
+                const float mc = lse.m * lse_c;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) lse.s += __builtin_amdgcn_exp2f(__builtin_fmaf(lv[q], lse_c, -mc));
+            }
+        }
+    };
+
+    const int step = NT * 4 * GROUPS;
+    int e0 = lo;
+    if (vec) {
+        // full steps: every group of every lane in bounds; the next step's loads are in flight while this one is ranked
+        const int nfull = (hi - lo) / step;
+        if (nfull > 0) {
+            RawStep<DT> cur, nxt;
+            const u32 esz = DT == GBS_DTYPE_F32 ? 4u : 2u;
+            const RowRsrc R{rsrc(row, (u32)vocab * esz), rsrc(crow, COUNTS ? (u32)vocab * 4u : 0u),
+                            rsrc(mrow, MASK ? (u32)((vocab + 31) / 32) * 4u : 0u)};
+            int e = lo + tid * 4;
+            load_step<DT, COUNTS, MASK>(R, (u32)e, cur);
+            {
+                // the gate starts at the count-th largest of the lanes' first-step maxima
+                u32 m = 0;
+#pragma unroll
+                for (int j = 0; j < GROUPS; ++j) {
+                    const int eg = e + j * NT * 4;
+                    float x[4];
+                    unpack_x<DT>(cur, j, x);
+                    const u32 mb = MASK ? (cur.m[j] >> (eg & 31)) & 0xFu : 0xFu;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const float v = logit(x[q], COUNTS ? (int)cur.c[j][q] : 0, (mb >> q) & 1u);
+                        const u32 k = v != v ? 0u : okey_f32_fast(v);
+                        m = k > m ? k : m;
+                    }
+                }
+                wt.seed(m);
+            }
+            for (int s = 0; s < nfull; ++s) {
+                const int en = s + 1 < nfull ? e + step : e;
+                wt.apply_shared();
+                wt.prefetch_shared();
+                load_step<DT, COUNTS, MASK>(R, (u32)en, nxt);
+#pragma unroll
+                for (int j = 0; j < GROUPS; ++j) {
+                    const int eg = e + j * NT * 4;
+                    float x[4];
+                    int c[4] = {0, 0, 0, 0};
+                    unpack_x<DT>(cur, j, x);
+                    if (COUNTS) {
+                        c[0] = (int)cur.c[j].x; c[1] = (int)cur.c[j].y; c[2] = (int)cur.c[j].z; c[3] = (int)cur.c[j].w;
+                    }
+                    const u32 mb = MASK ? (cur.m[j] >> (eg & 31)) & 0xFu : 0xFu;
+                    group(x, c, mb, eg);
+                }
+                wt.flush(false);
+                cur = nxt;
+                e = en;
+            }
+        }
+        e0 = lo + nfull * step;
+    }
+    // the rest of the chunk (or all of it when 16-byte loads are not legal), one group per lane per round, guarded
+    {
+        const int rounds = (hi - e0 + NT * 4 - 1) / (NT * 4);
+        for (int k = 0; k < rounds; ++k) {
+            const int eg = e0 + k * NT * 4 + tid * 4;
+            float x[4];
+            int c[4];
+            u32 mb = 0;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                float v = penalize(g[j].x[q], g[j].c[q], rinv, p.repetition, p.frequency, p.presence);
-                if (!((g[j].mbits >> q) & 1u) || !g[j].in[q]) v = -INFINITY;
-                nan |= v != v;
-                lv[q] = v;
-                wt.offer(v != v ? 0ull : make_key(okey_f32(v), (u32)(eg + q)));
+                const bool in = eg + q < hi;
+                x[q] = in ? load_x1<DT>(row, eg + q) : 0.f;
+                c[q] = (COUNTS && in) ? crow[eg + q] : 0;
+                const u32 bit = MASK ? (in ? (mrow[(eg + q) >> 5] >> ((eg + q) & 31)) & 1u : 0u) : (in ? 1u : 0u);
+                mb |= bit << q;
             }
-            if (LOGPROB) {
-                const float gm = fmaxf(fmaxf(lv[0], lv[1]), fmaxf(lv[2], lv[3]));
-                if (gm > lse.m) {
-                    lse.s = lse.m == -INFINITY ? 0.f : lse.s * exp2f((lse.m - gm) * clp);
-                    lse.m = gm;
-                }
-                if (lse.m != -INFINITY) {
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) lse.s += exp2f((lv[q] - lse.m) * clp);
-                }
-            }
+            group(x, c, mb, eg);
+            wt.flush(false);
         }
-        wt.flush(false);
-#pragma unroll
-        for (int j = 0; j < GROUPS; ++j) g[j] = gn[j];
-        e = en;
     }
     wt.flush(true);
 
@@ -264,7 +347,7 @@ __global__ void __launch_bounds__(NT) sample_fast_k(const void* __restrict__ log
             lse = lse_merge(lse, o, clp);
         }
     }
-    const bool wnan = ballot(nan) != 0ull;
+    const bool wnan = ballot(nanv != 0u) != 0ull;
     if (l == 0) {
         s_lse[w] = lse;
         s_nan[w] = wnan ? 1u : 0u;
@@ -273,7 +356,7 @@ __global__ void __launch_bounds__(NT) sample_fast_k(const void* __restrict__ log
     if (w == 0) {
         for (int o = 1; o < NW; ++o) wt.merge_sorted(s_list[o][l]);
         const size_t slot = (size_t)r * S + sp;
-        ws.lists[slot * WAVE + l] = wt.list;
+        st_agent(&ws.lists[slot * WAVE + l], wt.list);
         if (l == 0) {
             Lse b = s_lse[0];
             unsigned bn = s_nan[0];
@@ -281,20 +364,22 @@ __global__ void __launch_bounds__(NT) sample_fast_k(const void* __restrict__ log
                 if (LOGPROB) b = lse_merge(b, s_lse[o], clp);
                 bn |= s_nan[o];
             }
-            ws.lse[slot] = b;
-            ws.nan[slot] = bn;
+            st_agent_f2((float2*)&ws.lse[slot], make_float2(b.m, b.s));
+            st_agent(&ws.nan[slot], bn);
         }
     }
     if (!arrive_last(&ws.counters[r], (unsigned)S, &s_flag)) return;
+    if (tid == 0) st_agent(&ws.row_thr[r], (u64)0);
+    const u64 list = block_merge_lists<NW>(ws.lists + (size_t)r * S * WAVE, S, s_list);
     if (w != 0) return;
-
-    u64 list = 0;
-    for (int o = 0; o < S; ++o) list = wave_merge_desc(list, ws.lists[((size_t)r * S + o) * WAVE + l]);
     Lse rl{-INFINITY, 0.f};
     unsigned rn = 0;
     for (int o = l; o < S; o += WAVE) {
-        if (LOGPROB) rl = lse_merge(rl, ws.lse[(size_t)r * S + o], clp);
-        rn |= ws.nan[(size_t)r * S + o];
+        if (LOGPROB) {
+            const float2 f = ld_agent_f2((const float2*)&ws.lse[(size_t)r * S + o]);
+            rl = lse_merge(rl, Lse{f.x, f.y}, clp);
+        }
+        rn |= ld_agent(&ws.nan[(size_t)r * S + o]);
     }
     if (LOGPROB) {
 #pragma unroll

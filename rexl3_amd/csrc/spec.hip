@@ -43,7 +43,6 @@ struct RowInfo {
 struct SeqInfo {
     int status, accepted, row, mode;  // mode 0: token fixed; 1: residual draw; 2: bonus draw
     int token, pad[3];
-    u128 weight_total;
 };
 
 struct SpecWs {
@@ -117,6 +116,39 @@ __device__ __forceinline__ T block_reduce_sum(T v, T* s) {
     return r;
 }
 
+__device__ __forceinline__ RowInfo load_row(const RowInfo* rows, int r) {
+    RowInfo ri;
+    ri.tkey = ld_agent(&rows[r].tkey);
+    ri.dkey = ld_agent(&rows[r].dkey);
+    ri.zp = ld_agent(&rows[r].zp);
+    ri.zq = ld_agent(&rows[r].zq);
+    ri.nan = ld_agent(&rows[r].nan);
+    return ri;
+}
+
+__device__ __forceinline__ void store_seq(SeqInfo* seqs, int s, const SeqInfo& v) {
+    st_agent(&seqs[s].status, v.status);
+    st_agent(&seqs[s].accepted, v.accepted);
+    st_agent(&seqs[s].row, v.row);
+    st_agent(&seqs[s].mode, v.mode);
+    st_agent(&seqs[s].token, v.token);
+}
+
+__device__ __forceinline__ SeqInfo load_seq(const SeqInfo* seqs, int s) {
+    SeqInfo v{};
+    v.status = ld_agent(&seqs[s].status);
+    v.accepted = ld_agent(&seqs[s].accepted);
+    v.row = ld_agent(&seqs[s].row);
+    v.mode = ld_agent(&seqs[s].mode);
+    v.token = ld_agent(&seqs[s].token);
+    return v;
+}
+
+__device__ __forceinline__ u128 load_u128(const u128* p) {
+    const u64 lo = ld_agent((const u64*)p), hi = ld_agent((const u64*)p + 1);
+    return ((u128)hi << 64) | lo;
+}
+
 // ---- launch 1: maxima ----
 __global__ void __launch_bounds__(NT) spec_max_k(const float* __restrict__ target, const float* __restrict__ draft, int width, int vocab,
                                                  int chunk, SpecWs ws) {
@@ -145,23 +177,23 @@ __global__ void __launch_bounds__(NT) spec_max_k(const float* __restrict__ targe
     dk = block_reduce_max(dk, s_red);
     const unsigned bn = block_reduce_max((u64)(nan ? 1 : 0), s_red) != 0ull;
     if (threadIdx.x == 0) {
-        ws.maxparts[((size_t)r * S + sp) * 2] = tk;
-        ws.maxparts[((size_t)r * S + sp) * 2 + 1] = dk;
-        ws.nanparts[(size_t)r * S + sp] = bn;
+        st_agent(&ws.maxparts[((size_t)r * S + sp) * 2], tk);
+        st_agent(&ws.maxparts[((size_t)r * S + sp) * 2 + 1], dk);
+        st_agent(&ws.nanparts[(size_t)r * S + sp], bn);
     }
     if (!arrive_last(&ws.row_counters[r], (unsigned)S, &s_flag)) return;
     if (threadIdx.x == 0) {
         u64 a = 0, b = 0;
         unsigned n = 0;
         for (int o = 0; o < S; ++o) {
-            const u64 x = ws.maxparts[((size_t)r * S + o) * 2], y = ws.maxparts[((size_t)r * S + o) * 2 + 1];
+            const u64 x = ld_agent(&ws.maxparts[((size_t)r * S + o) * 2]), y = ld_agent(&ws.maxparts[((size_t)r * S + o) * 2 + 1]);
             a = x > a ? x : a;
             b = y > b ? y : b;
-            n |= ws.nanparts[(size_t)r * S + o];
+            n |= ld_agent(&ws.nanparts[(size_t)r * S + o]);
         }
-        ws.rows[r].tkey = a;
-        ws.rows[r].dkey = b;
-        ws.rows[r].nan = n;
+        st_agent(&ws.rows[r].tkey, a);
+        st_agent(&ws.rows[r].dkey, b);
+        st_agent(&ws.rows[r].nan, n);
     }
 }
 
@@ -184,7 +216,7 @@ __global__ void __launch_bounds__(NT) spec_mass_k(const float* __restrict__ targ
     const bool has_draft = (r % W1) < width;
     const float T = temps[r];
     const bool draw = temp_ok(T) && T > 0.0f;
-    const RowInfo info = ws.rows[r];
+    const RowInfo info = load_row(ws.rows, r);
     const float Mp = key_value(info.tkey), Mq = key_value(info.dkey);
     const float c2 = draw ? temp_scale(T) : 0.0f;
     const float* tr = target + (size_t)r * vocab;
@@ -204,18 +236,18 @@ __global__ void __launch_bounds__(NT) spec_mass_k(const float* __restrict__ targ
     zp = block_reduce_sum(zp, s_red);
     zq = block_reduce_sum(zq, s_red);
     if (threadIdx.x == 0) {
-        ws.sumparts[((size_t)r * S + sp) * 2] = zp;
-        ws.sumparts[((size_t)r * S + sp) * 2 + 1] = zq;
+        st_agent(&ws.sumparts[((size_t)r * S + sp) * 2], zp);
+        st_agent(&ws.sumparts[((size_t)r * S + sp) * 2 + 1], zq);
     }
     if (!arrive_last(&ws.row_counters[r], (unsigned)S, &s_flag)) return;
     if (threadIdx.x == 0) {
         u64 a = 0, b = 0;
         for (int o = 0; o < S; ++o) {
-            a += ws.sumparts[((size_t)r * S + o) * 2];
-            b += ws.sumparts[((size_t)r * S + o) * 2 + 1];
+            a += ld_agent(&ws.sumparts[((size_t)r * S + o) * 2]);
+            b += ld_agent(&ws.sumparts[((size_t)r * S + o) * 2 + 1]);
         }
-        ws.rows[r].zp = a;
-        ws.rows[r].zq = b;
+        st_agent(&ws.rows[r].zp, a);
+        st_agent(&ws.rows[r].zq, b);
     }
     if (!arrive_last(&ws.seq_counters[seq], (unsigned)W1, &s_flag)) return;
     if (threadIdx.x != 0) return;
@@ -232,7 +264,7 @@ __global__ void __launch_bounds__(NT) spec_mass_k(const float* __restrict__ targ
     }
     bool nan = false, empty = false;
     for (int j = 0; j <= width; ++j) {
-        const RowInfo ri = ws.rows[r0 + j];
+        const RowInfo ri = load_row(ws.rows, r0 + j);
         nan |= ri.nan != 0u;
         empty |= ri.tkey == 0ull || (j < width && ri.dkey == 0ull);
     }
@@ -242,7 +274,7 @@ __global__ void __launch_bounds__(NT) spec_mass_k(const float* __restrict__ targ
     if (si.status == GBS_ROW_OK) {
         int j = 0;
         for (; j < width; ++j) {
-            const RowInfo ri = ws.rows[r0 + j];
+            const RowInfo ri = load_row(ws.rows, r0 + j);
             const float Tj = temps[r0 + j];
             const int x = draft_ids[(size_t)seq * width + j];
             bool acc;
@@ -261,13 +293,13 @@ __global__ void __launch_bounds__(NT) spec_mass_k(const float* __restrict__ targ
         const float Tj = temps[r0 + j];
         if (Tj == 0.0f) {
             si.mode = 0;
-            si.token = (int)key_id(ws.rows[r0 + j].tkey);
+            si.token = (int)key_id(ld_agent(&ws.rows[r0 + j].tkey));
         } else {
             si.mode = j < width ? 1 : 2;
             si.token = -1;
         }
     }
-    ws.seqs[seq] = si;
+    store_seq(ws.seqs, seq, si);
 }
 
 // residual (mode 1) or bonus (mode 2) weight of element i of the sequence's draw row
@@ -290,7 +322,7 @@ __global__ void __launch_bounds__(NT) spec_draw_k(const float* __restrict__ targ
     __shared__ unsigned s_flag;
     __shared__ int s_tok;
     const int S = gridDim.x, sp = blockIdx.x, seq = blockIdx.y;
-    const SeqInfo si = ws.seqs[seq];
+    const SeqInfo si = load_seq(ws.seqs, seq);
     const bool drawing = si.status == GBS_ROW_OK && si.mode != 0;
     const int lo = sp * chunk, hi = min(vocab, lo + chunk);
     float Mp = 0.f, Mq = 0.f, c2 = 0.f;
@@ -298,7 +330,7 @@ __global__ void __launch_bounds__(NT) spec_draw_k(const float* __restrict__ targ
     const float* tr = target;
     const float* dr = draft;
     if (drawing) {
-        const RowInfo ri = ws.rows[si.row];
+        const RowInfo ri = load_row(ws.rows, si.row);
         Mp = key_value(ri.tkey);
         Mq = key_value(ri.dkey);
         zp = ri.zp;
@@ -311,18 +343,21 @@ __global__ void __launch_bounds__(NT) spec_draw_k(const float* __restrict__ targ
     if (drawing)
         for (int i = lo + (int)threadIdx.x; i < hi; i += NT) part += draw_weight(si.mode, tr, dr, i, Mp, Mq, c2, zp, zq);
     part = block_reduce_sum(part, s_red);
-    if (threadIdx.x == 0) ws.wparts[(size_t)seq * S + sp] = part;
+    if (threadIdx.x == 0) {
+        st_agent((u64*)&ws.wparts[(size_t)seq * S + sp], (u64)part);
+        st_agent((u64*)&ws.wparts[(size_t)seq * S + sp] + 1, (u64)(part >> 64));
+    }
     if (!arrive_last(&ws.draw_counters[seq], (unsigned)S, &s_flag)) return;
     int token = si.token;
     if (drawing) {
         if (threadIdx.x == 0) {
             u128 total = 0;
-            for (int o = 0; o < S; ++o) total += ws.wparts[(size_t)seq * S + o];
+            for (int o = 0; o < S; ++o) total += load_u128(&ws.wparts[(size_t)seq * S + o]);
             const u128 t = mul_floor(u_resample[seq], total, nullptr);
             u128 before = 0;
             int c = 0;
             for (; c < S; ++c) {
-                const u128 w = ws.wparts[(size_t)seq * S + c];
+                const u128 w = load_u128(&ws.wparts[(size_t)seq * S + c]);
                 if (before + w > t) break;
                 before += w;
             }
