@@ -507,8 +507,10 @@ int gbo_keyed_sample_row(const void* row, int dtype, int valid, const GbsKeyedRo
  *   7. top-k:       K = the first min(top_k, |A|) of A in order (all of A when top_k == 0).
  *   8. top-p:       if 0 < top_p < 1: P = ceil(top_p * Z_K) exactly; keep = min(1 + #{j : C_j < P}, |K|), where C_j is
  *                   the inclusive prefix mass in order (crates/sampling/src/lib.rs:241-251's rule, in integers).
- *   9. min-p:       if min_p > 0: Q = ceil(min_p * 2^44); keep = max(1, #{j < keep : E_j >= Q})
- *                   (crates/sampling/src/lib.rs:253-259's rule: count, then truncate).
+ *   9. min-p:       if min_p > 0: Q = ceil(min_p * 2^44); the kept set is {j < keep : E_j >= Q} (a filter on the
+ *                   top-p prefix; it holds the first token, whose mass is 2^44 >= Q). The reference's rule
+ *                   (crates/sampling/src/lib.rs:253-259) counts and truncates, which is the same set whenever the
+ *                   masses are monotone along the order.
  *  10. draw:        Z = sum of the kept masses; t = floor(u * Z) exactly; the kept tokens taken in ascending id order, the
  *                   token is the first whose running mass sum exceeds t.
  *  prob = (float)((double)E_token / (double)Z); logprob = log-softmax over A at temperature T (1 when T == 0), double
@@ -749,27 +751,25 @@ void gbo_sample_row(const void* logits, int dtype, int vocab, const int32_t* cou
             }
             keep = below + 1 < kk ? below + 1 : kk;
         }
-        if (p->min_p > 0.0f) {
-            const uint64_t Q = mul_ceil64(p->min_p, 1ULL << 44);
-            size_t cnt = 0;
-            for (size_t j = 0; j < keep; ++j)
-                if (E[j] >= Q) ++cnt;
-            keep = cnt > 1 ? cnt : 1;
-        }
+        /* min-p filters the prefix: a token stays if its mass is at least Q (the first token, of mass 2^44, always does) */
+        const uint64_t Q = p->min_p > 0.0f ? mul_ceil64(p->min_p, 1ULL << 44) : 0;
         uint64_t z = 0;
-        for (size_t j = 0; j < keep; ++j) z += E[j];
-        const uint64_t t = (uint64_t)mul_floor128(u, z, NULL);
-        /* ascending id order over the kept set: E is indexed by rank, so sort (id, rank) pairs */
+        size_t nk = 0;
         int* byid = (int*)malloc(keep * sizeof(int) * 2);
         for (size_t j = 0; j < keep; ++j) {
-            byid[2 * j] = cand[j].id;
-            byid[2 * j + 1] = (int)j;
+            if (E[j] < Q) continue;
+            z += E[j];
+            byid[2 * nk] = cand[j].id;
+            byid[2 * nk + 1] = (int)j;
+            ++nk;
         }
-        qsort(byid, keep, sizeof(int) * 2, by_id_asc);
+        const uint64_t t = (uint64_t)mul_floor128(u, z, NULL);
+        /* ascending id order over the kept set: E is indexed by rank, so sort (id, rank) pairs */
+        qsort(byid, nk, sizeof(int) * 2, by_id_asc);
         uint64_t acc = 0;
         int chosen = -1;
         uint64_t ec = 0;
-        for (size_t j = 0; j < keep; ++j) {
+        for (size_t j = 0; j < nk; ++j) {
             acc += E[byid[2 * j + 1]];
             if (acc > t) {
                 chosen = byid[2 * j];
@@ -779,7 +779,7 @@ void gbo_sample_row(const void* logits, int dtype, int vocab, const int32_t* cou
         }
         out->id = chosen;
         out->prob = (float)((double)ec / (double)z);
-        out->kept = (int32_t)keep;
+        out->kept = (int32_t)nk;
         out->z_kept = z;
         free(byid);
         free(E);

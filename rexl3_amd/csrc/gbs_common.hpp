@@ -248,10 +248,24 @@ struct WaveTop {
     int count;
     u64* buf;
 
+    float gate_f;  // the float whose order value is `gate`: for a non-NaN v, okey(v) >= gate <=> v >= gate_f
+
     __device__ __forceinline__ void set_thr(u64 t) {
         thr = t;
         const u32 hi = (u32)(t >> 32);
         gate = ((u32)t == 0xFFFFFFFFu && hi != 0xFFFFFFFFu) ? hi + 1u : hi;
+        gate_f = okey_to_f32(gate);
+    }
+
+    // offer element `id` of value `v` (f32 order, NaN never passes): one float compare per element; the order key is
+    // built only for the elements that pass
+    __device__ __forceinline__ void offer_f(float v, u32 id) {
+        const bool pass = v >= gate_f;
+        const u64 m = ballot(pass);
+        if (m) {
+            if (pass) buf[n + mbcnt(m)] = make_key(okey_f32_fast(v), id);
+            n += __popcll(m);
+        }
     }
 
     // Optional sharing of the gate: every wave's `count`-th key is a lower bound of the count-th key of its whole row,

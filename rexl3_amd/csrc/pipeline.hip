@@ -10,6 +10,7 @@
 #include <type_traits>
 
 #include "gbs_modeu.hpp"
+#include "pipeline_full.hpp"
 
 using namespace gbs;
 using namespace gbs::modeu;
@@ -18,11 +19,21 @@ namespace {
 
 constexpr int NT = 256;
 constexpr int NW = NT / WAVE;
-constexpr int GROUPS = 4;  // 4-element groups per lane per step of the main loop
-constexpr int BUF = WAVE * (GROUPS * 4 + 1);
+#ifndef GBS_FAST_GROUPS
+#define GBS_FAST_GROUPS 4
+#endif
+#ifndef GBS_FAST_BLOCKS
+#define GBS_FAST_BLOCKS 1024
+#endif
+constexpr int GROUPS = GBS_FAST_GROUPS;  // 4-element groups per lane per step of the main loop
+#ifndef GBS_FAST_FLUSH_GROUPS
+#define GBS_FAST_FLUSH_GROUPS GBS_FAST_GROUPS
+#endif
+constexpr int FLUSH_GROUPS = GBS_FAST_FLUSH_GROUPS;  // groups offered between two flushes of the wave buffer
+constexpr int BUF = WAVE * (FLUSH_GROUPS * 4 + 1);
 constexpr u64 FLOOR_KEY = ((u64)NEG_INF_KEY << 32) | 0xFFFFFFFFull;  // every -inf key is at or below it
 
-constexpr int FAST_TARGET_BLOCKS = 1024;
+constexpr int FAST_TARGET_BLOCKS = GBS_FAST_BLOCKS;
 constexpr int FAST_MIN_CHUNK = 4096;
 
 size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
@@ -155,12 +166,9 @@ __device__ RowOut finish_row(u64 list, const RowParamsDev& p, float u, bool inva
             const int below = __popcll(ballot(valid && C < P));
             keep = below + 1 < kn ? below + 1 : kn;
         }
-        if (p.min_p > 0.0f) {
-            const u64 Q = mul_ceil64(p.min_p, MASS_ONE);
-            const int cnt = __popcll(ballot(l < keep && E >= Q));
-            keep = cnt > 1 ? cnt : 1;
-        }
-        const bool kept = l < keep;
+        // min-p filters the top-p prefix (the first token, of mass 2^44 >= Q, always stays)
+        const u64 Q = p.min_p > 0.0f ? mul_ceil64(p.min_p, MASS_ONE) : 0ull;
+        const bool kept = l < keep && E >= Q;
         const u64 z = wave_sum_u64(kept ? E : 0ull);
         const u64 t = (u64)mul_floor(u, (u128)z, nullptr);
         // kept tokens in ascending id order: sort (id, rank) pairs
@@ -247,7 +255,7 @@ __global__ void __launch_bounds__(NT) sample_fast_k(const void* __restrict__ log
         }
         nanv |= (__builtin_isunordered(lv[0], lv[1]) | __builtin_isunordered(lv[2], lv[3])) ? 1u : 0u;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) wt.offer_ok(okey_f32_fast(lv[q]), (u32)(eg + q));
+        for (int q = 0; q < 4; ++q) wt.offer_f(lv[q], (u32)(eg + q));
         if (LOGPROB) {
             const float gm = fmaxf(fmaxf(lv[0], lv[1]), fmaxf(lv[2], lv[3]));
             if (gm > lse.m) {
@@ -308,8 +316,8 @@ __global__ void __launch_bounds__(NT) sample_fast_k(const void* __restrict__ log
                     }
                     const u32 mb = MASK ? (cur.m[j] >> (eg & 31)) & 0xFu : 0xFu;
                     group(x, c, mb, eg);
+                    if ((j + 1) % FLUSH_GROUPS == 0) wt.flush(false);
                 }
-                wt.flush(false);
                 cur = nxt;
                 e = en;
             }
@@ -429,7 +437,7 @@ void dispatch_fast(bool c, bool m, bool lp, dim3 grid, hipStream_t st, const voi
 
 GBS_EXPORT size_t gbs_sample_workspace_bytes(int rows, int vocab, int kmax) {
     if (rows <= 0 || vocab <= 0 || vocab > GBS_MAX_VOCAB || kmax < 0 || kmax > GBS_MAX_COUNT) return 0;
-    if (kmax == 0) return 0;  // the full-distribution path is not built yet
+    if (kmax == 0) return 256;  // the full-distribution path keeps its state in LDS
     return fast_ws_bytes(rows, vocab, fast_splits(rows, vocab));
 }
 
@@ -439,8 +447,11 @@ GBS_EXPORT int gbs_sample_rows(const void* logits, int dtype, int rows, int stri
     if (rows < 0 || vocab <= 0 || vocab > GBS_MAX_VOCAB || stride < vocab || kmax < 0 || kmax > GBS_MAX_COUNT) return GBS_ERR_INVALID;
     if (dtype != GBS_DTYPE_F32 && dtype != GBS_DTYPE_BF16) return GBS_ERR_INVALID;
     if (rows == 0) return 0;
-    if (kmax == 0) return GBS_ERR_INVALID;
-    if (rows > 65535 || !logits || !params || !uniforms || !out_ids || !ws || !aligned(ws, 256)) return GBS_ERR_INVALID;
+    if (rows > 65535 || !logits || !params || !uniforms || !out_ids) return GBS_ERR_INVALID;
+    if (kmax == 0)
+        return launch_sample_full(logits, dtype, rows, stride, vocab, counts, mask, params, uniforms, out_ids, out_greedy, out_probs,
+                                  out_logprobs, out_status, stream);
+    if (!ws || !aligned(ws, 256)) return GBS_ERR_INVALID;
     const int S = fast_splits(rows, vocab);
     if (ws_bytes < fast_ws_bytes(rows, vocab, S)) return GBS_ERR_INVALID;
     int chunk = (vocab + S - 1) / S;

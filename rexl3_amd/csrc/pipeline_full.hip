@@ -1,0 +1,427 @@
+// The extended pipeline's full-distribution path (gbs_sample_rows with kmax == 0): any top_k (0 = off), top-p over the
+// whole vocabulary, min-p and the inverse-CDF draw, exact in integer masses, with the same definition as the single-pass
+// kernel (gbs_modeu.hpp).
+//
+// One block of 1024 threads per row; every pass streams the row's logits, counts and mask words again (coalesced
+// 4-element groups). The exact cuts are radix selections over the 64-bit order keys (value, ~id), 11 bits per pass, on
+// LDS histograms of (count, mass, largest key) per digit; a pass ends early when the crossing digit holds one key.
+//   pass 0            row maximum (greedy id), NaN flag, number of allowed tokens, online log-sum-exp
+//   top-k passes      the top_k-th key by count (and the mass above it)            if 0 < top_k < allowed
+//   top-p passes      the key where the descending cumulative mass reaches P         if 0 < top_p < 1
+//   draw passes       kept-mass sums per 4096-element tile, then a scan of the one tile holding the draw
+// No radix pass sorts anything: each only counts the keys that share the prefix found so far.
+#include "gbs_modeu.hpp"
+#include "pipeline_full.hpp"
+
+using namespace gbs;
+using namespace gbs::modeu;
+
+namespace {
+
+constexpr int NTF = 1024;
+constexpr int NWF = NTF / WAVE;
+constexpr int DB = 11;
+constexpr int NB = 1 << DB;
+constexpr int TILE = NTF * 4;
+constexpr int MAX_TILES = (GBS_MAX_VOCAB + TILE - 1) / TILE;
+constexpr u32 VALID_MIN_OK = NEG_INF_KEY + 1u;  // order values above -inf
+
+template <int DT, bool COUNTS, bool MASK>
+struct Row {
+    const void* x;
+    const int* c;
+    const u32* m;
+    int vocab;
+    bool vec;
+    float rinv, rep, freq, pres;
+
+    __device__ __forceinline__ float pen(float v, int cnt) const {
+        if (COUNTS && cnt > 0) {
+            const float a = v > 0.0f ? v * rinv : v * rep;
+            return a - ((float)cnt * freq + pres);
+        }
+        return v;
+    }
+
+    // the penalised, masked logits of elements e..e+3 (out of range: -inf)
+    __device__ __forceinline__ void group(int e, float (&l)[4]) const {
+        float xv[4];
+        int cv[4] = {0, 0, 0, 0};
+        if (vec && e + 4 <= vocab) {
+            if (DT == GBS_DTYPE_F32) {
+                const float4 v = *(const float4*)((const float*)x + e);
+                xv[0] = v.x; xv[1] = v.y; xv[2] = v.z; xv[3] = v.w;
+            } else {
+                const uint2 v = *(const uint2*)((const u16*)x + e);
+                xv[0] = __uint_as_float(v.x << 16); xv[1] = __uint_as_float(v.x & 0xFFFF0000u);
+                xv[2] = __uint_as_float(v.y << 16); xv[3] = __uint_as_float(v.y & 0xFFFF0000u);
+            }
+            if (COUNTS) {
+                const int4 cc = *(const int4*)(c + e);
+                cv[0] = cc.x; cv[1] = cc.y; cv[2] = cc.z; cv[3] = cc.w;
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const bool in = e + q < vocab;
+                xv[q] = in ? (DT == GBS_DTYPE_F32 ? ((const float*)x)[e + q] : __uint_as_float((u32)((const u16*)x)[e + q] << 16)) : 0.f;
+                if (COUNTS) cv[q] = in ? c[e + q] : 0;
+            }
+        }
+        const u32 mw = MASK ? (e < vocab ? m[e >> 5] >> (e & 31) : 0u) : 0xFu;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const bool in = e + q < vocab && ((mw >> q) & 1u);
+            l[q] = in ? pen(xv[q], cv[q]) : -INFINITY;
+        }
+    }
+};
+
+__device__ __forceinline__ bool valid_l(float v) { return v > -INFINITY; }  // false for NaN and -inf
+
+template <typename T>
+__device__ __forceinline__ T block_sum(T v, T* s_red) {
+    const int w = threadIdx.x / WAVE;
+    for (int m = 1; m < WAVE; m <<= 1) {
+        if constexpr (sizeof(T) == 8) v += shfl_xor64(v, m);
+        else v += (T)__shfl_xor((int)v, m, WAVE);
+    }
+    __syncthreads();
+    if (lane_id() == 0) s_red[w] = v;
+    __syncthreads();
+    T r = 0;
+    for (int o = 0; o < NWF; ++o) r += s_red[o];
+    __syncthreads();
+    return r;
+}
+
+__device__ __forceinline__ u64 block_max_u64(u64 v, u64* s_red) {
+    const int w = threadIdx.x / WAVE;
+    for (int m = 1; m < WAVE; m <<= 1) {
+        const u64 o = shfl_xor64(v, m);
+        v = o > v ? o : v;
+    }
+    __syncthreads();
+    if (lane_id() == 0) s_red[w] = v;
+    __syncthreads();
+    u64 r = 0;
+    for (int o = 0; o < NWF; ++o) r = s_red[o] > r ? s_red[o] : r;
+    __syncthreads();
+    return r;
+}
+
+struct Shared {
+    u32 cnt[NB];
+    u64 mass[NB];
+    u64 maxk[NB];
+    u64 red[NWF];
+    u64 tile[MAX_TILES];
+    float lse_m[NWF], lse_s[NWF];
+    u64 bc[8];  // broadcast slots
+};
+
+// One radix selection over the keys >= lb of the row: the key K at which the descending cumulative weight (count when
+// by_mass is false, mass otherwise) first reaches `target` -- weight(keys > K) < target <= weight(keys >= K).
+// With frac_p > 0 the target is ceil(frac_p * total weight), the total being the first pass's sum.
+// *mass_above receives the mass of the keys > K.
+template <int DT, bool COUNTS, bool MASK>
+__device__ u64 radix_select(const Row<DT, COUNTS, MASK>& R, float M, float c2, u64 lb, bool by_mass, u64 target, float frac_p,
+                            u64* mass_above, u64* total_out, Shared& sh) {
+    u64 prefix = 0;
+    int plen = 0;
+    u64 above = 0;
+    for (;;) {
+        const int db = 64 - plen < DB ? 64 - plen : DB;
+        for (int i = threadIdx.x; i < NB; i += NTF) {
+            sh.cnt[i] = 0;
+            sh.mass[i] = 0;
+            sh.maxk[i] = 0;
+        }
+        __syncthreads();
+        const u64 pmask = plen == 0 ? 0ull : (~0ull << (64 - plen));
+        for (int base = 0; base < R.vocab; base += TILE) {
+            const int e = base + (int)threadIdx.x * 4;
+            float l[4];
+            R.group(e, l);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                if (!valid_l(l[q])) continue;
+                const u64 key = make_key(okey_f32(l[q]), (u32)(e + q));
+                if (key < lb || (key & pmask) != prefix) continue;
+                const int d = (int)((key >> (64 - plen - db)) & ((1ull << db) - 1ull));
+                atomicAdd(&sh.cnt[d], 1u);
+                atomicAdd((unsigned long long*)&sh.mass[d], (unsigned long long)mass(l[q], M, c2));
+                atomicMax((unsigned long long*)&sh.maxk[d], (unsigned long long)key);
+            }
+        }
+        __syncthreads();
+        // wave 0 finds the crossing digit, scanning digits from the largest down: lane i owns 32 digits
+        if (threadIdx.x < WAVE) {
+            const int l = lane_id();
+            constexpr int PER = NB / WAVE;
+            const int nd = 1 << db;
+            u64 wsum = 0, msum = 0;
+            for (int k = 0; k < PER; ++k) {
+                const int d = nd - 1 - (l * PER + k);
+                if (d >= 0) {
+                    wsum += by_mass ? sh.mass[d] : (u64)sh.cnt[d];
+                    msum += sh.mass[d];
+                }
+            }
+            if (plen == 0 && frac_p > 0.0f) {
+                const u64 tot = wave_sum_u64(wsum);
+                if (total_out) *total_out = tot;
+                target = mul_ceil64(frac_p, tot);
+            }
+            const u64 incl = wave_scan_u64(wsum);
+            const u64 excl = incl - wsum;
+            const u64 mincl = wave_scan_u64(msum);
+            const u64 mexcl = mincl - msum;
+            const u64 hit = ballot(incl >= target);
+            const int f = hit ? (int)__builtin_ctzll(hit) : WAVE - 1;
+            if (l == f) {
+                u64 acc = excl, macc = mexcl;
+                int dstar = 0;
+                for (int k = 0; k < PER; ++k) {
+                    const int d = nd - 1 - (l * PER + k);
+                    if (d < 0) break;
+                    const u64 w = by_mass ? sh.mass[d] : (u64)sh.cnt[d];
+                    dstar = d;
+                    if (acc + w >= target) break;
+                    acc += w;
+                    macc += sh.mass[d];
+                }
+                sh.bc[0] = (u64)dstar;
+                sh.bc[1] = target - acc;
+                sh.bc[2] = macc;
+                sh.bc[3] = sh.cnt[dstar];
+                sh.bc[4] = sh.maxk[dstar];
+            }
+        }
+        __syncthreads();
+        const int dstar = (int)sh.bc[0];
+        target = sh.bc[1];
+        above += sh.bc[2];
+        const u64 cstar = sh.bc[3], kmax = sh.bc[4];
+        __syncthreads();
+        prefix |= (u64)dstar << (64 - plen - db);
+        plen += db;
+        if (cstar <= 1 || plen >= 64) {
+            if (mass_above) *mass_above = above;
+            return cstar == 1 ? kmax : prefix;
+        }
+    }
+}
+
+template <int DT, bool COUNTS, bool MASK>
+__global__ void __launch_bounds__(NTF) sample_full_k(const void* __restrict__ logits, long long stride, int vocab,
+                                                     const int* __restrict__ counts, const u32* __restrict__ mask,
+                                                     const RowParamsDev* __restrict__ params, const float* __restrict__ uniforms, bool vec,
+                                                     int* __restrict__ out_ids, int* __restrict__ out_greedy, float* __restrict__ out_probs,
+                                                     float* __restrict__ out_logprobs, int* __restrict__ out_status) {
+    __shared__ Shared sh;
+    const int r = blockIdx.x;
+    const int tid = threadIdx.x, w = tid / WAVE, l = lane_id();
+    const RowParamsDev p = params[r];
+    const float u = uniforms[r];
+    Row<DT, COUNTS, MASK> R;
+    R.x = (const char*)logits + (size_t)r * (size_t)stride * (DT == GBS_DTYPE_F32 ? 4 : 2);
+    R.c = COUNTS ? counts + (size_t)r * vocab : nullptr;
+    R.m = MASK ? mask + (size_t)r * ((vocab + 31) / 32) : nullptr;
+    R.vocab = vocab;
+    R.vec = vec;
+    R.rinv = 1.0f / p.repetition;
+    R.rep = p.repetition;
+    R.freq = p.frequency;
+    R.pres = p.presence;
+    const float clp = p.temperature > 0.0f ? temp_scale(p.temperature) : 1.44269504088896340736f;
+
+    auto finish = [&](int id, int greedy, int status, float prob, float lp) {
+        if (tid == 0) {
+            out_ids[r] = status == GBS_ROW_OK ? id : -1;
+            if (out_greedy) out_greedy[r] = status == GBS_ROW_OK ? greedy : -1;
+            if (out_probs) out_probs[r] = status == GBS_ROW_OK ? prob : 0.f;
+            if (out_logprobs) out_logprobs[r] = status == GBS_ROW_OK ? lp : __uint_as_float(0x7fc00000u);
+            if (out_status) out_status[r] = status;
+        }
+    };
+    if (params_invalid(p, u)) {
+        finish(-1, -1, GBS_ROW_INVALID_PARAMS, 0.f, 0.f);
+        return;
+    }
+
+    // ---- pass 0: maximum, NaN, allowed count, log-sum-exp
+    u64 kmaxv = 0;
+    u32 nan = 0, nallowed = 0;
+    Lse lse{-INFINITY, 0.f};
+    for (int base = 0; base < vocab; base += TILE) {
+        const int e = base + tid * 4;
+        float lv[4];
+        R.group(e, lv);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            nan |= lv[q] != lv[q];
+            if (valid_l(lv[q])) {
+                ++nallowed;
+                const u64 k = make_key(okey_f32(lv[q]), (u32)(e + q));
+                kmaxv = k > kmaxv ? k : kmaxv;
+                if (lv[q] > lse.m) {
+                    lse.s = lse.m == -INFINITY ? 0.f : lse.s * exp2f((lse.m - lv[q]) * clp);
+                    lse.m = lv[q];
+                }
+                lse.s += exp2f((lv[q] - lse.m) * clp);
+            }
+        }
+    }
+    for (int m = 1; m < WAVE; m <<= 1) {
+        const Lse o{__shfl_xor(lse.m, m, WAVE), __shfl_xor(lse.s, m, WAVE)};
+        lse = lse_merge(lse, o, clp);
+    }
+    if (l == 0) {
+        sh.lse_m[w] = lse.m;
+        sh.lse_s[w] = lse.s;
+    }
+    const u32 nan_any = (u32)block_sum((u64)nan, sh.red);
+    const u64 n_allowed = block_sum((u64)nallowed, sh.red);
+    const u64 top = block_max_u64(kmaxv, sh.red);
+    Lse rl{-INFINITY, 0.f};
+    for (int o = 0; o < NWF; ++o) rl = lse_merge(rl, Lse{sh.lse_m[o], sh.lse_s[o]}, clp);
+    if (nan_any) {
+        finish(-1, -1, GBS_ROW_NAN_LOGIT, 0.f, 0.f);
+        return;
+    }
+    if (n_allowed == 0) {
+        finish(-1, -1, GBS_ROW_NO_CANDIDATES, 0.f, 0.f);
+        return;
+    }
+    const int greedy = (int)key_id(top);
+    const float M = okey_to_f32(key_ok(top));
+    auto logprob_of = [&](float lx) {
+        if (isinf(M)) return __uint_as_float(0x7fc00000u);
+        return ((lx - rl.m) * clp - log2f(rl.s)) * 0.6931471805599453f;
+    };
+    if (p.temperature == 0.0f) {
+        finish(greedy, greedy, GBS_ROW_OK, 1.0f, logprob_of(M));
+        return;
+    }
+    const float c2 = temp_scale(p.temperature);
+
+    // ---- top-k
+    const u64 floor_key = (u64)VALID_MIN_OK << 32;
+    u64 lb = floor_key;
+    u64 zk = 0;
+    bool have_zk = false;
+    if (p.top_k > 0 && (u64)p.top_k < n_allowed) {
+        u64 above = 0;
+        const u64 kk = radix_select(R, M, c2, floor_key, false, (u64)p.top_k, 0.0f, &above, nullptr, sh);
+        lb = kk;
+        zk = above + mass(okey_to_f32(key_ok(kk)), M, c2);
+        have_zk = true;
+    }
+    // ---- top-p
+    u64 kp = lb;
+    if (p.top_p > 0.0f && p.top_p < 1.0f) {
+        u64 tot = 0;
+        if (have_zk) kp = radix_select(R, M, c2, lb, true, mul_ceil64(p.top_p, zk), 0.0f, nullptr, nullptr, sh);
+        else kp = radix_select(R, M, c2, lb, true, 0, p.top_p, nullptr, &tot, sh);
+    }
+    // ---- draw: kept = key >= kp and mass >= Q, in ascending id order
+    const u64 Q = p.min_p > 0.0f ? mul_ceil64(p.min_p, MASS_ONE) : 0ull;
+    auto kept_mass = [&](float v, int i) -> u64 {
+        if (!valid_l(v)) return 0ull;
+        if (make_key(okey_f32(v), (u32)i) < kp) return 0ull;
+        const u64 E = mass(v, M, c2);
+        return E >= Q ? E : 0ull;
+    };
+    const int ntiles = (vocab + TILE - 1) / TILE;
+    u64 z = 0;
+    for (int t = 0; t < ntiles; ++t) {
+        const int e = t * TILE + tid * 4;
+        float lv[4];
+        R.group(e, lv);
+        u64 s = 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) s += kept_mass(lv[q], e + q);
+        s = block_sum(s, sh.red);
+        if (tid == 0) sh.tile[t] = s;
+        z += s;
+    }
+    __syncthreads();
+    const u64 target = (u64)mul_floor(u, (u128)z, nullptr);
+    int tsel = ntiles - 1;
+    u64 before = 0;
+    for (int t = 0; t < ntiles; ++t) {
+        if (before + sh.tile[t] > target) {
+            tsel = t;
+            break;
+        }
+        before += sh.tile[t];
+    }
+    // the tile: thread sums, a block exclusive scan, the owning thread scans its 4 elements
+    const int e = tsel * TILE + tid * 4;
+    float lv[4];
+    R.group(e, lv);
+    u64 em[4], mine = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        em[q] = kept_mass(lv[q], e + q);
+        mine += em[q];
+    }
+    const u64 incl = wave_scan_u64(mine);
+    __syncthreads();
+    if (l == WAVE - 1) sh.red[w] = incl;
+    __syncthreads();
+    u64 wbase = before;
+    for (int o = 0; o < w; ++o) wbase += sh.red[o];
+    const u64 excl = wbase + incl - mine;
+    if (excl <= target && target < excl + mine) {
+        u64 acc = excl;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            acc += em[q];
+            if (acc > target) {
+                sh.bc[5] = (u64)(e + q);
+                sh.bc[6] = em[q];
+                sh.bc[7] = __float_as_uint(lv[q]);
+                break;
+            }
+        }
+    }
+    __syncthreads();
+    const int id = (int)sh.bc[5];
+    const u64 ec = sh.bc[6];
+    const float lx = __uint_as_float((u32)sh.bc[7]);
+    finish(id, greedy, GBS_ROW_OK, (float)((double)ec / (double)z), logprob_of(lx));
+}
+
+}  // namespace
+
+namespace gbs {
+
+int launch_sample_full(const void* logits, int dtype, int rows, int stride, int vocab, const int32_t* counts, const uint32_t* mask,
+                       const void* params, const float* uniforms, int* out_ids, int* out_greedy, float* out_probs, float* out_logprobs,
+                       int* out_status, void* stream) {
+    const size_t esz = dtype == GBS_DTYPE_F32 ? 4 : 2;
+    const bool vec = stride % 4 == 0 && aligned(logits, 4 * esz) && (!counts || (vocab % 4 == 0 && aligned(counts, 16)));
+    const hipStream_t st = to_stream(stream);
+    const RowParamsDev* p = (const RowParamsDev*)params;
+#define GBS_FULL(D, C, Mk)                                                                                                        \
+    hipLaunchKernelGGL((sample_full_k<D, C, Mk>), dim3(rows), dim3(NTF), 0, st, logits, (long long)stride, vocab, counts, mask, p, \
+                       uniforms, vec, out_ids, out_greedy, out_probs, out_logprobs, out_status)
+    const bool c = counts != nullptr, m = mask != nullptr;
+    if (dtype == GBS_DTYPE_F32) {
+        if (c && m) GBS_FULL(GBS_DTYPE_F32, true, true);
+        else if (c) GBS_FULL(GBS_DTYPE_F32, true, false);
+        else if (m) GBS_FULL(GBS_DTYPE_F32, false, true);
+        else GBS_FULL(GBS_DTYPE_F32, false, false);
+    } else {
+        if (c && m) GBS_FULL(GBS_DTYPE_BF16, true, true);
+        else if (c) GBS_FULL(GBS_DTYPE_BF16, true, false);
+        else if (m) GBS_FULL(GBS_DTYPE_BF16, false, true);
+        else GBS_FULL(GBS_DTYPE_BF16, false, false);
+    }
+#undef GBS_FULL
+    return launch_status();
+}
+
+}  // namespace gbs

@@ -130,3 +130,41 @@ def test_kmax_and_rows_invariance():
     for r in [0, 9, 23]:
         one = S.sample_rows(x[r:r + 1].contiguous(), cfg["params"][r:r + 1], u[r:r + 1].contiguous(), None, m[r:r + 1].contiguous())
         assert host(one["ids"])[0] == g1["ids"][r]
+
+
+# ---------------------------------------------------------------- the full-distribution path (kmax == 0)
+
+def test_full_path_config3_penalties_top_p_over_the_whole_vocabulary():
+    need_gpu()
+    cfg = W.config3(rows=16)
+    log("config3 rows=16 full path")
+    g, w = run_both(cfg, kmax=0)
+    compare(g, w, "config3")
+
+
+def test_full_path_equals_fast_path_and_oracle():
+    need_gpu()
+    for cfg, what in [(W.config1(3), "c1"), (W.config2(), "c2"), (W.config4(rows=32), "c4"), (W.northstar(rows=16), "ns")]:
+        g0, w = run_both(cfg, kmax=0)
+        compare(g0, w, what + " full")
+        g1, _ = run_both(cfg, kmax=64)
+        assert np.array_equal(g0["ids"], g1["ids"]), what
+
+
+def test_full_path_large_top_k_ties_and_min_p():
+    need_gpu()
+    rng = np.random.default_rng(17)
+    B, V = 24, 70001
+    x = (rng.integers(0, 12, (B, V)) * 0.25).astype(np.float32)  # massive exact ties
+    x[3] = 1.0                                                      # one value everywhere
+    x[4] = rng.standard_normal(V).astype(np.float32) * 4
+    x[5, ::7] = -np.inf
+    p = S.row_params(B, temperature=0.9, top_p=0.7, min_p=0.0, top_k=0)
+    p["top_k"][:8] = [100, 1000, 5000, 70001, 70000, 3, 65, 256]
+    p["min_p"][8:12] = [0.1, 0.5, 1.0, 0.01]
+    p["top_p"][12:16] = [1.0, 0.0, 0.999, 0.01]
+    p["temperature"][16:18] = [0.05, 3.0]
+    u = W.uniforms_f32(77, B)
+    cfg = dict(logits=x, dtype="f32", params=p, uniforms=u, counts=None, mask=None)
+    g, w = run_both(cfg, kmax=0)
+    compare(g, w, "ties")
