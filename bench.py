@@ -31,12 +31,25 @@ def parse():
     ap.add_argument("--workload", default="northstar")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only copy 316,026,880 bytes device to device (the plain copy that scales rocprofv3 FETCH_SIZE)")
     return ap.parse_args()
 
 
 def algorithmic_bytes(rows, vocab, logit_bytes, counts, mask, extra=0):
     per_row = logit_bytes * vocab + (4 * vocab if counts else 0) + (4 * ((vocab + 31) // 32) if mask else 0)
     return rows * per_row + extra
+
+
+def profiled_traffic(workload):
+    """HBM bytes per launch measured with rocprofv3 FETCH_SIZE + WRITE_SIZE (scaled by a plain copy of known size), as
+    recorded in profiles/; None when no measurement of this workload is recorded."""
+    import re
+    path = os.path.join(ROOT, "profiles", {"northstar": "sample_fast_k_northstar.md"}.get(workload, ""))
+    if not os.path.isfile(path):
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*(\d+)", open(path).read())
+    return int(m.group(1)) if m else None
 
 
 def time_launches(launch, steps, warmup):
@@ -86,15 +99,24 @@ def main():
     from rexl3_amd import sampling as S
     from rexl3_amd import workloads as W
 
-    lib = _lib.load()
     dev = torch.device("cuda:0")
+    if args.copy_calibration:
+        src = torch.ones(316_026_880 // 4, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": src.numel() * 4, "launches": 3}))
+        return
+    lib = _lib.load()
     stream = C.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
     wl = args.workload
     threads = max(1, min(os.cpu_count() or 1, 16))
     cpu = None
 
-    if wl in ("northstar", "c1", "c2", "c4"):
-        cfg = {"northstar": W.northstar, "c1": W.config1, "c2": W.config2, "c4": W.config4}[wl]()
+    if wl in ("northstar", "c1", "c2", "c3", "c4"):
+        cfg = {"northstar": W.northstar, "c1": W.config1, "c2": W.config2, "c3": W.config3, "c4": W.config4}[wl]()
+        kmax = 0 if wl == "c3" else 64
         x = cfg["logits"]
         rows, vocab = x.shape
         is_bf16 = cfg["dtype"] == "bf16"
@@ -107,11 +129,11 @@ def main():
         ut = torch.from_numpy(cfg["uniforms"]).to(dev)
         out = {k: torch.empty(rows, dtype=torch.int32 if k in ("ids", "greedy", "status") else torch.float32, device=dev)
                for k in ("ids", "greedy", "status", "probs", "logprobs")}
-        wsb = lib.gbs_sample_workspace_bytes(rows, vocab, 64)
+        wsb = lib.gbs_sample_workspace_bytes(rows, vocab, kmax)
         ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
         lib.gbs_workspace_clear(ws.data_ptr(), wsb, stream)
         P = lambda t: None if t is None else C.c_void_p(t.data_ptr())  # noqa: E731
-        argv = (P(xt), 1 if is_bf16 else 0, rows, vocab, vocab, P(ct), P(mt), P(pt), P(ut), 64, P(out["ids"]), P(out["greedy"]),
+        argv = (P(xt), 1 if is_bf16 else 0, rows, vocab, vocab, P(ct), P(mt), P(pt), P(ut), kmax, P(out["ids"]), P(out["greedy"]),
                 P(out["probs"]), P(out["logprobs"]), P(out["status"]), P(ws), wsb, stream)
         fn = lib.gbs_sample_rows
 
@@ -122,12 +144,13 @@ def main():
 
         ms = time_launches(launch, args.steps, args.warmup)
         nbytes = algorithmic_bytes(rows, vocab, 2 if is_bf16 else 4, ct is not None, mt is not None)
-        kernel = "sample_fast_k"
+        kernel = "sample_full_k" if kmax == 0 else "sample_fast_k"
         dtype = "bf16->f32" if is_bf16 else "f32"
         workload = {"northstar": "extended pipeline: penalties (dense i32 counts) + u32 grammar mask + T 0.8 + top-k 50 / top-p 0.9"
                                  " + log-softmax + inverse-CDF draw",
                     "c1": "config 1: single row, T 0.7, top-k 50, top-p 0.9",
                     "c2": "config 2: bf16 batched, per-row T, top-k 40, top-p 0.95, min-p 0.05",
+                    "c3": "config 3: penalties over dense counts, T 0.8, top-p 0.9 over the whole vocabulary (no top-k)",
                     "c4": "config 4: grammar mask, top-k 64, top-p 0.95"}[wl]
         st = out["status"].cpu().numpy()
         assert (st[cfg["params"]["temperature"] >= 0] >= 0).all()
@@ -231,7 +254,7 @@ def main():
         "config": {"workload": workload, "name": wl, "rows": rows, "vocab": vocab, "kernel": kernel},
         "hbm_gbps": round(achieved, 1),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(wl),
                      "bytes_per_launch": nbytes, "timing": "HIP events around the timed launches on their stream"},
         "cpu_baseline": cpu,
     }
