@@ -196,9 +196,21 @@ __device__ __forceinline__ u64 wave_bitonic_desc(u64 v) {
 // the 64 largest of a descending list and an ascending list (one key per lane each), descending
 __device__ __forceinline__ u64 wave_merge_desc_asc(u64 a_desc, u64 b_asc) { return wave_bitonic_desc(a_desc > b_asc ? a_desc : b_asc); }
 
+// v of lane 63 - lane: mirror within each 16-lane row (DPP), then swap row halves and neighbouring rows (permlanes)
+__device__ __forceinline__ u32 reverse_lane(u32 v) {
+    const int l = (int)__lane_id();
+    u32 m = (u32)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false);  // row_mirror
+    const auto a = __builtin_amdgcn_permlane32_swap(m, m, false, false);
+    m = (l & 32) ? (u32)a[0] : (u32)a[1];
+    const auto b = __builtin_amdgcn_permlane16_swap(m, m, false, false);
+    return (l & 16) ? (u32)b[0] : (u32)b[1];
+}
+
+__device__ __forceinline__ u64 reverse_lane64(u64 v) { return ((u64)reverse_lane((u32)(v >> 32)) << 32) | reverse_lane((u32)v); }
+
 // the 64 largest of two descending lists, descending
 __device__ __forceinline__ u64 wave_merge_desc(u64 a, u64 b_desc) {
-    const u64 br = shfl64(b_desc, WAVE - 1 - lane_id());
+    const u64 br = reverse_lane64(b_desc);
     return wave_bitonic_desc(a > br ? a : br);
 }
 
@@ -215,18 +227,33 @@ __device__ __forceinline__ u32 wave_kth_largest(u32 v, int k) {
 
 __device__ __forceinline__ u64 wave_sum_u64(u64 v) {
 #pragma unroll
-    for (int m = 1; m < WAVE; m <<= 1) v += shfl_xor64(v, m);
+    for (int m = 1; m < WAVE; m <<= 1) v += xor_lane64(v, m);
     return v;
 }
 
-// inclusive prefix sum over lanes
-__device__ __forceinline__ u64 wave_scan_u64(u64 v) {
-    const int l = lane_id();
-#pragma unroll
-    for (int d = 1; d < WAVE; d <<= 1) {
-        const u64 o = shfl64(v, l >= d ? l - d : l);
-        if (l >= d) v += o;
+// u64 of the DPP-shifted lane (0 where the control selects no lane or the row is masked off)
+__device__ __forceinline__ u64 dpp64(u64 v, int ctrl, int row_mask) {
+    u32 lo, hi;
+    switch (ctrl) {  // the control must be a constant: one case per use
+        case 0x111: lo = __builtin_amdgcn_update_dpp(0, (int)(u32)v, 0x111, 0xF, 0xF, true); hi = __builtin_amdgcn_update_dpp(0, (int)(u32)(v >> 32), 0x111, 0xF, 0xF, true); break;
+        case 0x112: lo = __builtin_amdgcn_update_dpp(0, (int)(u32)v, 0x112, 0xF, 0xF, true); hi = __builtin_amdgcn_update_dpp(0, (int)(u32)(v >> 32), 0x112, 0xF, 0xF, true); break;
+        case 0x114: lo = __builtin_amdgcn_update_dpp(0, (int)(u32)v, 0x114, 0xF, 0xF, true); hi = __builtin_amdgcn_update_dpp(0, (int)(u32)(v >> 32), 0x114, 0xF, 0xF, true); break;
+        case 0x118: lo = __builtin_amdgcn_update_dpp(0, (int)(u32)v, 0x118, 0xF, 0xF, true); hi = __builtin_amdgcn_update_dpp(0, (int)(u32)(v >> 32), 0x118, 0xF, 0xF, true); break;
+        case 0x142: lo = __builtin_amdgcn_update_dpp(0, (int)(u32)v, 0x142, 0xA, 0xF, false); hi = __builtin_amdgcn_update_dpp(0, (int)(u32)(v >> 32), 0x142, 0xA, 0xF, false); break;
+        default: lo = __builtin_amdgcn_update_dpp(0, (int)(u32)v, 0x143, 0xC, 0xF, false); hi = __builtin_amdgcn_update_dpp(0, (int)(u32)(v >> 32), 0x143, 0xC, 0xF, false); break;
     }
+    (void)row_mask;
+    return ((u64)hi << 32) | lo;
+}
+
+// inclusive prefix sum over lanes: DPP row shifts within 16-lane rows, then row broadcasts across rows
+__device__ __forceinline__ u64 wave_scan_u64(u64 v) {
+    v += dpp64(v, 0x111, 0xF);  // row_shr:1
+    v += dpp64(v, 0x112, 0xF);  // row_shr:2
+    v += dpp64(v, 0x114, 0xF);  // row_shr:4
+    v += dpp64(v, 0x118, 0xF);  // row_shr:8
+    v += dpp64(v, 0x142, 0xA);  // row_bcast:15 into rows 1 and 3
+    v += dpp64(v, 0x143, 0xC);  // row_bcast:31 into rows 2 and 3
     return v;
 }
 
@@ -274,6 +301,33 @@ struct WaveTop {
     u64* s_shared;  // LDS, block-wide (may be null)
     u64* g_shared;  // device memory, row-wide (may be null)
     u64 g_seen;
+    // Union bound: every wave of the block also publishes its m-th key, m = count / nslots + 1, into its own LDS slot;
+    // the smallest of the nslots slots has at least nslots * m - 1 >= count keys of the block above it (each wave's
+    // m best, one of them possibly equal to it), so it bounds the block's count-th key like a list of the whole block
+    // would, without merging the waves' candidates.
+    u64* s_slots;   // LDS, nslots entries (may be null)
+    int slot_w, nslots, mth;
+
+    __device__ __forceinline__ void set_slots(u64* slots, int w, int n) {
+        s_slots = slots;
+        slot_w = w;
+        nslots = n;
+        mth = count / n + 1;
+        if (mth > WAVE) s_slots = nullptr;
+    }
+
+    __device__ __forceinline__ void publish_slot(u64 v) {
+        if (!s_slots || v == 0ull) return;
+        if (lane_id() == 0) s_slots[slot_w] = v;
+        wave_lds_sync();
+        u64 mn = lane_id() < nslots ? s_slots[lane_id()] : ~0ull;
+#pragma unroll
+        for (int m = 1; m < WAVE; m <<= 1) {
+            const u64 o = xor_lane64(mn, m);
+            mn = o < mn ? o : mn;
+        }
+        if (lane_id() == 0 && mn > 0ull && s_shared) __hip_atomic_fetch_max(s_shared, mn, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
 
     __device__ __forceinline__ void init(u64* b, int cnt, u64 floor_key, u64* sh = nullptr, u64* gsh = nullptr) {
         list = 0;
@@ -284,6 +338,10 @@ struct WaveTop {
         s_shared = sh;
         g_shared = gsh;
         g_seen = 0;
+        s_slots = nullptr;
+        slot_w = 0;
+        nslots = 0;
+        mth = 0;
     }
 
     __device__ __forceinline__ void publish() {
@@ -347,6 +405,7 @@ struct WaveTop {
             if (t > thr) set_thr(t);
         }
         publish();
+        if (s_slots) publish_slot(readlane64(list, mth - 1));
         wave_lds_sync();
     }
 
@@ -360,6 +419,10 @@ struct WaveTop {
                 set_thr(t);
                 publish();
             }
+        }
+        if (s_slots) {
+            const u32 rm = wave_kth_largest(ok, mth);
+            if (rm > 0u) publish_slot(((u64)rm << 32) - 1ull);
         }
     }
 
@@ -414,6 +477,25 @@ __device__ __forceinline__ bool arrive_last(unsigned* counter, unsigned expected
     return *s_flag != 0u;
 }
 
+// The top 64 of the NW waves' descending lists, in wave 0 (other waves: unspecified), by a pairwise tree in LDS:
+// log2(NW) merge levels instead of NW - 1 merges on one wave. All threads of the block call it; s_list must not be in
+// use by another wave when it is called.
+template <int NW>
+__device__ __forceinline__ u64 block_tree_merge(u64 acc, u64 (*s_list)[WAVE]) {
+    const int w = threadIdx.x / WAVE, l = lane_id();
+    s_list[w][l] = acc;
+    __syncthreads();
+#pragma unroll
+    for (int h = NW / 2; h >= 1; h >>= 1) {
+        if (w < h) {
+            acc = wave_merge_desc(acc, s_list[w + h][l]);
+            if (h > 1) s_list[w][l] = acc;
+        }
+        if (h > 1) __syncthreads();
+    }
+    return acc;
+}
+
 // The last block's merge of `nl` descending 64-key lists at lists[i * 64 + lane] (agent-scope reads): each wave merges
 // every NW-th list with the next list's load in flight, then wave 0 merges the waves' results. Returns the merged
 // list in wave 0 (other waves: unspecified). All threads of the block call it. s_list: NW x 64 keys of LDS.
@@ -428,11 +510,7 @@ __device__ __forceinline__ u64 block_merge_lists(const u64* lists, int nl, u64 (
         acc = wave_merge_desc(acc, cur);
     }
     __syncthreads();
-    s_list[w][l] = acc;
-    __syncthreads();
-    if (w == 0)
-        for (int o = 1; o < NW; ++o) acc = wave_merge_desc(acc, s_list[o][l]);
-    return acc;
+    return block_tree_merge<NW>(acc, s_list);
 }
 
 }  // namespace gbs

@@ -10,7 +10,7 @@ namespace sel {
 
 constexpr int NT = 256;
 constexpr int NW = NT / WAVE;
-constexpr int BUF = WAVE * (4 * 4 + 1);  // < 64 keys left after a flush + 16 keys per lane of one step
+constexpr int BUF = WAVE * (4 + 1);  // < 64 keys left after a flush + 4 keys per lane of one group
 
 enum { DT_F32 = 0, DT_BF16 = 1, DT_F16 = 2 };
 
@@ -63,34 +63,52 @@ __device__ void block_select(const void* row, int lo, int hi, bool vec, int coun
         const int step = NT * 4 * SEL_GROUPS;
         const int nfull = (hi - lo) / step;
         if (nfull > 0) {
-            SelRaw<DT> cur, nxt;
+            SelRaw<DT> b0, b1;
             int e = lo + tid * 4;
-            sel_load<DT>(row, e, cur);
+            sel_load<DT>(row, e, b0);
             {
                 u32 m = 0;
 #pragma unroll
                 for (int j = 0; j < SEL_GROUPS; ++j) {
                     u32 k[4];
-                    sel_keys<DT>(cur, j, k);
+                    sel_keys<DT>(b0, j, k);
 #pragma unroll
                     for (int q = 0; q < 4; ++q) m = k[q] > m ? k[q] : m;
                 }
                 wt.seed(m);
             }
-            for (int s = 0; s < nfull; ++s) {
-                const int en = s + 1 < nfull ? e + step : e;
-                sel_load<DT>(row, en, nxt);
+            // one step: every key of the step, one gate test per key folded into one scalar mask, one branch into
+            // the (rare) offer path
+            auto step_fn = [&](const SelRaw<DT>& B, int e) {
+                u32 k[SEL_GROUPS * 4];
 #pragma unroll
                 for (int j = 0; j < SEL_GROUPS; ++j) {
-                    u32 k[4];
-                    sel_keys<DT>(cur, j, k);
-                    const int eg = e + j * NT * 4;
+                    u32 kj[4];
+                    sel_keys<DT>(B, j, kj);
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) wt.offer_ok(k[q], (u32)(eg + q));
+                    for (int q = 0; q < 4; ++q) k[j * 4 + q] = kj[q];
                 }
-                wt.flush(false);
-                cur = nxt;
-                e = en;
+                const u32 g = wt.gate;
+                u64 anyp = 0;
+#pragma unroll
+                for (int i = 0; i < SEL_GROUPS * 4; ++i) anyp |= ballot(k[i] >= g);
+                if (anyp) {
+#pragma unroll
+                    for (int j = 0; j < SEL_GROUPS; ++j) {
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) wt.offer_ok(k[j * 4 + q], (u32)(e + j * NT * 4 + q));
+                        wt.flush(false);
+                    }
+                }
+            };
+            // two register buffers in turn: no buffer copy forces its loads to complete early
+            for (int s = 0; s < nfull; s += 2) {
+                sel_load<DT>(row, s + 1 < nfull ? e + step : e, b1);
+                step_fn(b0, e);
+                if (s + 1 >= nfull) break;
+                sel_load<DT>(row, s + 2 < nfull ? e + 2 * step : e, b0);
+                step_fn(b1, e + step);
+                e += 2 * step;
             }
         }
         e0 = lo + nfull * step;
@@ -103,11 +121,7 @@ __device__ void block_select(const void* row, int lo, int hi, bool vec, int coun
         wt.flush(false);
     }
     wt.flush(true);
-    s_list[w][lane_id()] = wt.list;
-    __syncthreads();
-    if (w == 0) {
-        for (int o = 1; o < NW; ++o) wt.merge_sorted(s_list[o][lane_id()]);
-    }
+    wt.list = block_tree_merge<NW>(wt.list, s_list);
 }
 
 }  // namespace sel

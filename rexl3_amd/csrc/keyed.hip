@@ -227,9 +227,12 @@ __global__ void __launch_bounds__(NT) keyed_sample_k(const void* logits, long lo
     WaveTop<BUF> wt;
     wt.init(s_buf[threadIdx.x / WAVE], count, 0ull);
     block_select<DT>(row, lo, hi, vec, count, wt, s_list);
-    if (threadIdx.x < WAVE) st_agent(&parts[((size_t)r * S + sp) * WAVE + threadIdx.x], wt.list);
-    if (!arrive_last(&counters[r], (unsigned)S, &s_flag)) return;
-    const u64 list = block_merge_lists<NW>(parts + (size_t)r * S * WAVE, S, s_list);
+    u64 list = wt.list;
+    if (S > 1) {
+        if (threadIdx.x < WAVE) st_agent(&parts[((size_t)r * S + sp) * WAVE + threadIdx.x], wt.list);
+        if (!arrive_last(&counters[r], (unsigned)S, &s_flag)) return;
+        list = block_merge_lists<NW>(parts + (size_t)r * S * WAVE, S, s_list);
+    }
     if (threadIdx.x >= WAVE) return;
     const int l = lane_id();
     int status = ok ? GBS_ROW_OK : GBS_ROW_INVALID_PARAMS;

@@ -17,17 +17,35 @@ using namespace gbs::modeu;
 
 namespace {
 
-constexpr int NT = 256;
+#ifndef GBS_FAST_MINBLOCKS
+#define GBS_FAST_MINBLOCKS 1
+#endif
+#ifndef GBS_FAST_THREADS
+#define GBS_FAST_THREADS 1024
+#endif
+constexpr int NT = GBS_FAST_THREADS;
 constexpr int NW = NT / WAVE;
+#ifndef GBS_EXP_NOPEN
+#define GBS_EXP_NOPEN 0
+#endif
+#ifndef GBS_EXP_NOSEL
+#define GBS_EXP_NOSEL 0
+#endif
+#ifndef GBS_EXP_NOFINISH
+#define GBS_EXP_NOFINISH 0
+#endif
+#ifndef GBS_EXP_NOLSE
+#define GBS_EXP_NOLSE 0
+#endif
 #ifndef GBS_FAST_GROUPS
 #define GBS_FAST_GROUPS 4
 #endif
 #ifndef GBS_FAST_BLOCKS
-#define GBS_FAST_BLOCKS 1024
+#define GBS_FAST_BLOCKS 256
 #endif
 constexpr int GROUPS = GBS_FAST_GROUPS;  // 4-element groups per lane per step of the main loop
 #ifndef GBS_FAST_FLUSH_GROUPS
-#define GBS_FAST_FLUSH_GROUPS GBS_FAST_GROUPS
+#define GBS_FAST_FLUSH_GROUPS 1
 #endif
 constexpr int FLUSH_GROUPS = GBS_FAST_FLUSH_GROUPS;  // groups offered between two flushes of the wave buffer
 constexpr int BUF = WAVE * (FLUSH_GROUPS * 4 + 1);
@@ -192,7 +210,7 @@ __device__ RowOut finish_row(u64 list, const RowParamsDev& p, float u, bool inva
 }
 
 template <int DT, bool COUNTS, bool MASK, bool LOGPROB>
-__global__ void __launch_bounds__(NT) sample_fast_k(const void* __restrict__ logits, long long stride, int vocab, int chunk,
+__global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const void* __restrict__ logits, long long stride, int vocab, int chunk,
                                                     const int* __restrict__ counts, const u32* __restrict__ mask,
                                                     const RowParamsDev* __restrict__ params, const float* __restrict__ uniforms,
                                                     int kmax, bool vec, FastWs ws, int* __restrict__ out_ids,
@@ -204,9 +222,11 @@ __global__ void __launch_bounds__(NT) sample_fast_k(const void* __restrict__ log
     __shared__ unsigned s_nan[NW];
     __shared__ unsigned s_flag;
     __shared__ u64 s_thr;
+    __shared__ u64 s_slots[NW];
     const int S = gridDim.x, sp = blockIdx.x, r = blockIdx.y;
     const int tid = threadIdx.x, w = tid / WAVE, l = lane_id();
     if (tid == 0) s_thr = 0;
+    if (tid < NW) s_slots[tid] = 0;
     __syncthreads();
     const size_t esz = DT == GBS_DTYPE_F32 ? 4 : 2;
     const void* row = (const char*)logits + (size_t)r * (size_t)stride * esz;
@@ -223,17 +243,18 @@ __global__ void __launch_bounds__(NT) sample_fast_k(const void* __restrict__ log
 
     WaveTop<BUF> wt;
     wt.init(s_buf[w], count, FLOOR_KEY, &s_thr, nullptr);
+    wt.set_slots(s_slots, w, NW);
     Lse lse{-INFINITY, 0.f};
 
     // the penalised logit of one element, in the operation order of the definition:
     // c > 0: (x > 0 ? x * rinv : x * rep) - ((float)c * freq + pres); otherwise x.
     auto penalized = [&](float x, int c) {
         float v = x;
-        if (COUNTS) {
-            if (c > 0) {
-                const float a = x > 0.0f ? x * rinv : x * p.repetition;
-                v = a - ((float)c * p.frequency + p.presence);
-            }
+        if (COUNTS && !GBS_EXP_NOPEN) {
+            // branch-free: most counts are zero, but a divergent branch per element costs more than the arithmetic
+            const float a = x * (x > 0.0f ? rinv : p.repetition);
+            const float b = (float)c * p.frequency + p.presence;
+            v = c > 0 ? a - b : x;
         }
         return v;
     };
@@ -254,9 +275,11 @@ __global__ void __launch_bounds__(NT) sample_fast_k(const void* __restrict__ log
             lv[q] = __uint_as_float((__float_as_uint(v) & keep) | (0xFF800000u & ~keep));
         }
         nanv |= (__builtin_isunordered(lv[0], lv[1]) | __builtin_isunordered(lv[2], lv[3])) ? 1u : 0u;
+        if (!GBS_EXP_NOSEL) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) wt.offer_f(lv[q], (u32)(eg + q));
-        if (LOGPROB) {
+            for (int q = 0; q < 4; ++q) wt.offer_f(lv[q], (u32)(eg + q));
+        }
+        if (LOGPROB && !GBS_EXP_NOLSE) {
             const float gm = fmaxf(fmaxf(lv[0], lv[1]), fmaxf(lv[2], lv[3]));
             if (gm > lse.m) {
                 lse.s = lse.m == -INFINITY ? 0.f : lse.s * __builtin_amdgcn_exp2f((lse.m - gm) * lse_c);
@@ -300,26 +323,74 @@ __global__ void __launch_bounds__(NT) sample_fast_k(const void* __restrict__ log
                 }
                 wt.seed(m);
             }
-            for (int s = 0; s < nfull; ++s) {
-                const int en = s + 1 < nfull ? e + step : e;
-                wt.apply_shared();
-                wt.prefetch_shared();
-                load_step<DT, COUNTS, MASK>(R, (u32)en, nxt);
+            // every wave has published its seeds: start from the block's bound
+            __syncthreads();
+            wt.prefetch_shared();
+            wt.apply_shared();
+            // Two register buffers in turn, so that no copy of a buffer forces its loads to complete early: the loads
+            // of step s + 1 stay in flight while step s is ranked.
+            auto step_fn = [&](const RawStep<DT>& B, int e) {
+                // the whole step straight-line: 16 logits, one gate test per element folded into one scalar mask,
+                // one branch per step into the (rare) offer path
+                constexpr int NE = GROUPS * 4;
+                float lv[NE];
 #pragma unroll
                 for (int j = 0; j < GROUPS; ++j) {
                     const int eg = e + j * NT * 4;
                     float x[4];
-                    int c[4] = {0, 0, 0, 0};
-                    unpack_x<DT>(cur, j, x);
-                    if (COUNTS) {
-                        c[0] = (int)cur.c[j].x; c[1] = (int)cur.c[j].y; c[2] = (int)cur.c[j].z; c[3] = (int)cur.c[j].w;
+                    unpack_x<DT>(B, j, x);
+                    const u32 mb = MASK ? (B.m[j] >> (eg & 31)) : 0xFu;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const float v = penalized(x[q], COUNTS ? (int)B.c[j][q] : 0);
+                        const u32 keep = MASK ? (u32)__builtin_amdgcn_sbfe((int)mb, q, 1) : 0xFFFFFFFFu;
+                        lv[j * 4 + q] = __uint_as_float((__float_as_uint(v) & keep) | (0xFF800000u & ~keep));
                     }
-                    const u32 mb = MASK ? (cur.m[j] >> (eg & 31)) & 0xFu : 0xFu;
-                    group(x, c, mb, eg);
-                    if ((j + 1) % FLUSH_GROUPS == 0) wt.flush(false);
                 }
-                cur = nxt;
-                e = en;
+                bool nan_step = false;
+#pragma unroll
+                for (int i = 0; i < NE; i += 2) nan_step |= __builtin_isunordered(lv[i], lv[i + 1]);
+                nanv |= nan_step ? 1u : 0u;
+                if (!GBS_EXP_NOSEL) {
+                    const float g = wt.gate_f;
+                    u64 anyp = 0;
+#pragma unroll
+                    for (int i = 0; i < NE; ++i) anyp |= ballot(lv[i] >= g);
+                    if (anyp) {
+#pragma unroll
+                        for (int j = 0; j < GROUPS; ++j) {
+#pragma unroll
+                            for (int q = 0; q < 4; ++q) wt.offer_f(lv[j * 4 + q], (u32)(e + j * NT * 4 + q));
+                            wt.flush(false);
+                        }
+                    }
+                }
+                if (LOGPROB && !GBS_EXP_NOLSE) {
+                    float gm = lv[0];
+#pragma unroll
+                    for (int i = 1; i < NE; ++i) gm = fmaxf(gm, lv[i]);
+                    if (gm > lse.m) {
+                        lse.s = lse.m == -INFINITY ? 0.f : lse.s * __builtin_amdgcn_exp2f((lse.m - gm) * lse_c);
+                        lse.m = gm;
+                    }
+                    if (lse.m != -INFINITY) {
+                        const float mc = lse.m * lse_c;
+#pragma unroll
+                        for (int i = 0; i < NE; ++i) lse.s += __builtin_amdgcn_exp2f(__builtin_fmaf(lv[i], lse_c, -mc));
+                    }
+                }
+            };
+            for (int s = 0; s < nfull; s += 2) {
+                wt.apply_shared();
+                wt.prefetch_shared();
+                load_step<DT, COUNTS, MASK>(R, (u32)(s + 1 < nfull ? e + step : e), nxt);
+                step_fn(cur, e);
+                if (s + 1 >= nfull) break;
+                wt.apply_shared();
+                wt.prefetch_shared();
+                load_step<DT, COUNTS, MASK>(R, (u32)(s + 2 < nfull ? e + 2 * step : e), cur);
+                step_fn(nxt, e + step);
+                e += 2 * step;
             }
         }
         e0 = lo + nfull * step;
@@ -346,8 +417,11 @@ __global__ void __launch_bounds__(NT) sample_fast_k(const void* __restrict__ log
     }
     wt.flush(true);
 
+    if (GBS_EXP_NOFINISH) {
+        if (l == 0) out_ids[r] = (int)(wt.list >> 40);
+        return;
+    }
     // block reduction: lists, LSE, NaN
-    s_list[w][l] = wt.list;
     if (LOGPROB) {
 #pragma unroll
         for (int m = 1; m < WAVE; m <<= 1) {
@@ -360,34 +434,44 @@ __global__ void __launch_bounds__(NT) sample_fast_k(const void* __restrict__ log
         s_lse[w] = lse;
         s_nan[w] = wnan ? 1u : 0u;
     }
-    __syncthreads();
-    if (w == 0) {
-        for (int o = 1; o < NW; ++o) wt.merge_sorted(s_list[o][l]);
-        const size_t slot = (size_t)r * S + sp;
-        st_agent(&ws.lists[slot * WAVE + l], wt.list);
-        if (l == 0) {
-            Lse b = s_lse[0];
-            unsigned bn = s_nan[0];
-            for (int o = 1; o < NW; ++o) {
-                if (LOGPROB) b = lse_merge(b, s_lse[o], clp);
-                bn |= s_nan[o];
-            }
-            st_agent_f2((float2*)&ws.lse[slot], make_float2(b.m, b.s));
-            st_agent(&ws.nan[slot], bn);
-        }
-    }
-    if (!arrive_last(&ws.counters[r], (unsigned)S, &s_flag)) return;
-    if (tid == 0) st_agent(&ws.row_thr[r], (u64)0);
-    const u64 list = block_merge_lists<NW>(ws.lists + (size_t)r * S * WAVE, S, s_list);
-    if (w != 0) return;
+    wt.list = block_tree_merge<NW>(wt.list, s_list);  // also orders s_lse / s_nan before the reads below
     Lse rl{-INFINITY, 0.f};
     unsigned rn = 0;
-    for (int o = l; o < S; o += WAVE) {
-        if (LOGPROB) {
-            const float2 f = ld_agent_f2((const float2*)&ws.lse[(size_t)r * S + o]);
-            rl = lse_merge(rl, Lse{f.x, f.y}, clp);
+    u64 list;
+    if (S == 1) {
+        // the whole row in this block: no hand-off through device memory
+        if (w != 0) return;
+        if (l < NW) {
+            rl = s_lse[l];
+            rn = s_nan[l];
         }
-        rn |= ld_agent(&ws.nan[(size_t)r * S + o]);
+        list = wt.list;
+    } else {
+        if (w == 0) {
+            const size_t slot = (size_t)r * S + sp;
+            st_agent(&ws.lists[slot * WAVE + l], wt.list);
+            if (l == 0) {
+                Lse b = s_lse[0];
+                unsigned bn = s_nan[0];
+                for (int o = 1; o < NW; ++o) {
+                    if (LOGPROB) b = lse_merge(b, s_lse[o], clp);
+                    bn |= s_nan[o];
+                }
+                st_agent_f2((float2*)&ws.lse[slot], make_float2(b.m, b.s));
+                st_agent(&ws.nan[slot], bn);
+            }
+        }
+        if (!arrive_last(&ws.counters[r], (unsigned)S, &s_flag)) return;
+        if (tid == 0) st_agent(&ws.row_thr[r], (u64)0);
+        list = block_merge_lists<NW>(ws.lists + (size_t)r * S * WAVE, S, s_list);
+        if (w != 0) return;
+        for (int o = l; o < S; o += WAVE) {
+            if (LOGPROB) {
+                const float2 f = ld_agent_f2((const float2*)&ws.lse[(size_t)r * S + o]);
+                rl = lse_merge(rl, Lse{f.x, f.y}, clp);
+            }
+            rn |= ld_agent(&ws.nan[(size_t)r * S + o]);
+        }
     }
     if (LOGPROB) {
 #pragma unroll

@@ -47,10 +47,8 @@ __global__ void __launch_bounds__(NT) topk_stage2_k(const void* logits, long lon
         const u64 g = l < pitch ? lists[(size_t)c * pitch + l] : 0ull;
         list = wave_merge_desc(list, g);
     }
-    s_list[w][l] = list;
-    __syncthreads();
+    list = block_tree_merge<NW>(list, s_list);
     if (w == 0) {
-        for (int o = 1; o < NW; ++o) list = wave_merge_desc(list, s_list[o][l]);
         if (l < count) {
             int id = -1;
             float v = -INFINITY;
