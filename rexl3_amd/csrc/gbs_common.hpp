@@ -22,6 +22,9 @@ typedef uint16_t u16;
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
+#ifndef GBS_EXP_STATS
+#define GBS_EXP_STATS 0
+#endif
 namespace gbs {
 
 constexpr int WAVE = 64;
@@ -277,6 +280,9 @@ struct WaveTop {
 
     float gate_f;  // the float whose order value is `gate`: for a non-NaN v, okey(v) >= gate <=> v >= gate_f
 
+#if GBS_EXP_STATS
+    int merges = 0;
+#endif
     __device__ __forceinline__ void set_thr(u64 t) {
         thr = t;
         const u32 hi = (u32)(t >> 32);
@@ -296,75 +302,76 @@ struct WaveTop {
     }
 
     // Optional sharing of the gate: every wave's `count`-th key is a lower bound of the count-th key of its whole row,
-    // so waves publish it to a block-wide LDS slot and a row-wide device slot (atomic max) and raise their own gate
-    // to the largest published value.
+    // so waves publish it to a block-wide LDS slot (atomic max) and raise their own gate to the largest published value.
     u64* s_shared;  // LDS, block-wide (may be null)
-    u64* g_shared;  // device memory, row-wide (may be null)
-    u64 g_seen;
-    // Union bound: every wave of the block also publishes its m-th key, m = count / nslots + 1, into its own LDS slot;
-    // the smallest of the nslots slots has at least nslots * m - 1 >= count keys of the block above it (each wave's
-    // m best, one of them possibly equal to it), so it bounds the block's count-th key like a list of the whole block
-    // would, without merging the waves' candidates.
-    u64* s_slots;   // LDS, nslots entries (may be null)
-    int slot_w, nslots, mth;
+    // Block bound: every wave publishes the order values of its TOPN best keys into its own LDS row. These are
+    // distinct elements of the block (each wave sees its own elements), so the count-th largest of all published
+    // values has at least `count` elements of the row at or above it: a lower bound of the row's count-th key that
+    // tracks the block as a whole, however unevenly its best elements fall on the waves.
+    static constexpr int TOPN = 8;
+    u32* s_top;  // LDS, nw * TOPN entries, zero at start (may be null)
+    int top_w, top_n;
 
-    __device__ __forceinline__ void set_slots(u64* slots, int w, int n) {
-        s_slots = slots;
-        slot_w = w;
-        nslots = n;
-        mth = count / n + 1;
-        if (mth > WAVE) s_slots = nullptr;
+    __device__ __forceinline__ void set_top(u32* t, int w, int nw) {
+        s_top = t;
+        top_w = w;
+        top_n = nw * TOPN;
+        if (top_n > 2 * WAVE) s_top = nullptr;
     }
 
-    __device__ __forceinline__ void publish_slot(u64 v) {
-        if (!s_slots || v == 0ull) return;
-        if (lane_id() == 0) s_slots[slot_w] = v;
-        wave_lds_sync();
-        u64 mn = lane_id() < nslots ? s_slots[lane_id()] : ~0ull;
+    // raise the gate to the block bound of the published values (all lanes of the wave call it)
+    __device__ __forceinline__ void block_bound() {
+        const int l = lane_id();
+        const u32 v0 = l < top_n ? s_top[l] : 0u;
+        const u32 v1 = l + WAVE < top_n ? s_top[l + WAVE] : 0u;
+        u32 r = 0;
 #pragma unroll
-        for (int m = 1; m < WAVE; m <<= 1) {
-            const u64 o = xor_lane64(mn, m);
-            mn = o < mn ? o : mn;
+        for (int b = 31; b >= 0; --b) {
+            const u32 c = r | (1u << b);
+            if (__popcll(ballot(v0 >= c)) + __popcll(ballot(v1 >= c)) >= count) r = c;
         }
-        if (lane_id() == 0 && mn > 0ull && s_shared) __hip_atomic_fetch_max(s_shared, mn, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        if (r > 0u) {
+            const u64 t = ((u64)r << 32) - 1ull;
+            if (t > thr) {
+                set_thr(t);
+                if (l == 0 && s_shared) __hip_atomic_fetch_max(s_shared, t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            }
+        }
     }
 
-    __device__ __forceinline__ void init(u64* b, int cnt, u64 floor_key, u64* sh = nullptr, u64* gsh = nullptr) {
+    __device__ __forceinline__ void publish_top() {
+        if (!s_top) return;
+        if (lane_id() < TOPN) s_top[top_w * TOPN + lane_id()] = (u32)(list >> 32);
+        wave_lds_sync();
+        block_bound();
+    }
+
+    __device__ __forceinline__ void init(u64* b, int cnt, u64 floor_key, u64* sh = nullptr) {
         list = 0;
         set_thr(floor_key);
         n = 0;
         count = cnt;
         buf = b;
         s_shared = sh;
-        g_shared = gsh;
-        g_seen = 0;
-        s_slots = nullptr;
-        slot_w = 0;
-        nslots = 0;
-        mth = 0;
+        s_top = nullptr;
+        top_w = 0;
+        top_n = 0;
     }
 
     __device__ __forceinline__ void publish() {
-        if (lane_id() == 0) {
-            if (s_shared) __hip_atomic_fetch_max(s_shared, thr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-            if (g_shared && thr > g_seen) __hip_atomic_fetch_max(g_shared, thr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
+        if (lane_id() == 0 && s_shared) __hip_atomic_fetch_max(s_shared, thr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
 
-    // Read the shared bounds (relaxed; a stale value is still a valid bound) into `pend_*`; apply_shared() raises the
-    // gate with them later. Issued before a step's data loads and applied one step later, the device read never makes
-    // the wave wait on loads it does not need yet.
-    u64 pend_l = 0, pend_g = 0;
+    // Read the shared bound (relaxed; a stale value is still a valid bound) into `pend_l`; apply_shared() raises the
+    // gate with it one step later, so the LDS read never makes the wave wait.
+    u64 pend_l = 0;
 
     __device__ __forceinline__ void prefetch_shared() {
-        if (g_shared) pend_g = __hip_atomic_load(g_shared, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (s_shared) pend_l = __hip_atomic_load(s_shared, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
 
     __device__ __forceinline__ void apply_shared() {
-        g_seen = pend_g;
-        u64 t = pend_l > pend_g ? pend_l : pend_g;
-        t = readlane64(t, 0);
+        const u64 t = readlane64(pend_l, 0);
         if (t > thr) set_thr(t);
     }
 
@@ -401,12 +408,24 @@ struct WaveTop {
             n = base;
             g = wave_sort_asc(g);
             list = wave_merge_desc_asc(list, g);
+#if GBS_EXP_STATS
+            ++merges;
+#endif
             const u64 t = readlane64(list, count - 1);
             if (t > thr) set_thr(t);
         }
         publish();
-        if (s_slots) publish_slot(readlane64(list, mth - 1));
+        if (!all) publish_top();
         wave_lds_sync();
+    }
+
+    // offer element `id` of value `v` whose gate test `v >= gate_f` was already taken: `pass` is this lane's result,
+    // `m` the wave's ballot of it
+    __device__ __forceinline__ void offer_tested(u64 m, bool pass, float v, u32 id) {
+        if (m) {
+            if (pass) buf[n + mbcnt(m)] = make_key(okey_f32_fast(v), id);
+            n += __popcll(m);
+        }
     }
 
     // Raise the gate from a sample: `ok` is one order value (key high word) per lane, of elements that will all be
@@ -420,9 +439,10 @@ struct WaveTop {
                 publish();
             }
         }
-        if (s_slots) {
-            const u32 rm = wave_kth_largest(ok, mth);
-            if (rm > 0u) publish_slot(((u64)rm << 32) - 1ull);
+        if (s_top) {
+            // the TOPN largest sample values are TOPN distinct elements of this wave
+            const u64 sv = wave_sort_desc(((u64)ok << 32) | (u64)lane_id());
+            if (lane_id() < TOPN) s_top[top_w * TOPN + lane_id()] = (u32)(sv >> 32);
         }
     }
 

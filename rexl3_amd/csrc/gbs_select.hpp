@@ -57,7 +57,6 @@ __device__ __forceinline__ void sel_keys(const SelRaw<DT>& r, int j, u32 (&k)[4]
 template <int DT>
 __device__ void block_select(const void* row, int lo, int hi, bool vec, int count, WaveTop<BUF>& wt, u64 (*s_list)[WAVE]) {
     const int tid = threadIdx.x;
-    const int w = tid / WAVE;
     int e0 = lo;
     if (vec) {
         const int step = NT * 4 * SEL_GROUPS;

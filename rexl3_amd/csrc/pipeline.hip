@@ -37,13 +37,19 @@ constexpr int NW = NT / WAVE;
 #ifndef GBS_EXP_NOLSE
 #define GBS_EXP_NOLSE 0
 #endif
+#ifndef GBS_EXP_TIMES
+#define GBS_EXP_TIMES 0
+#endif
 #ifndef GBS_FAST_GROUPS
-#define GBS_FAST_GROUPS 4
+#define GBS_FAST_GROUPS 8
 #endif
 #ifndef GBS_FAST_BLOCKS
 #define GBS_FAST_BLOCKS 256
 #endif
 constexpr int GROUPS = GBS_FAST_GROUPS;  // 4-element groups per lane per step of the main loop
+constexpr int HALF = 4;                  // groups ranked together
+constexpr int GS = WAVE * 4;             // elements between a lane's groups: a wave-step is WAVE * 4 * GROUPS contiguous
+constexpr int WSTEP = GS * GROUPS;       // elements of one wave-step
 #ifndef GBS_FAST_FLUSH_GROUPS
 #define GBS_FAST_FLUSH_GROUPS 1
 #endif
@@ -117,10 +123,11 @@ __device__ __forceinline__ void load_step(const RowRsrc& R, u32 e, RawStep<DT>& 
     constexpr u32 ESZ = DT == GBS_DTYPE_F32 ? 4 : 2;
 #pragma unroll
     for (int j = 0; j < GROUPS; ++j) {
-        if constexpr (DT == GBS_DTYPE_F32) r.x[j] = __builtin_amdgcn_raw_buffer_load_b128(R.x, e * ESZ, j * NT * 4 * ESZ, 0);
-        else r.x[j] = __builtin_amdgcn_raw_buffer_load_b64(R.x, e * ESZ, j * NT * 4 * ESZ, 0);
-        if constexpr (COUNTS) r.c[j] = __builtin_amdgcn_raw_buffer_load_b128(R.c, e * 4, j * NT * 16, 0);
-        if constexpr (MASK) r.m[j] = __builtin_amdgcn_raw_buffer_load_b32(R.m, (e >> 5) * 4, j * NT * 4 / 8, 0);
+        // logits and counts are read once: non-temporal loads (cache policy bit 1)
+        if constexpr (DT == GBS_DTYPE_F32) r.x[j] = __builtin_amdgcn_raw_buffer_load_b128(R.x, e * ESZ, j * GS * ESZ, 2);
+        else r.x[j] = __builtin_amdgcn_raw_buffer_load_b64(R.x, e * ESZ, j * GS * ESZ, 2);
+        if constexpr (COUNTS) r.c[j] = __builtin_amdgcn_raw_buffer_load_b128(R.c, e * 4, j * GS * 4, 2);
+        if constexpr (MASK) r.m[j] = __builtin_amdgcn_raw_buffer_load_b32(R.m, (e >> 5) * 4, j * GS / 8, 0);
     }
 }
 
@@ -222,11 +229,19 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
     __shared__ unsigned s_nan[NW];
     __shared__ unsigned s_flag;
     __shared__ u64 s_thr;
-    __shared__ u64 s_slots[NW];
+    __shared__ u32 s_top[NW * WaveTop<BUF>::TOPN];
     const int S = gridDim.x, sp = blockIdx.x, r = blockIdx.y;
     const int tid = threadIdx.x, w = tid / WAVE, l = lane_id();
-    if (tid == 0) s_thr = 0;
-    if (tid < NW) s_slots[tid] = 0;
+#if GBS_EXP_TIMES
+    const u64 t_start = wall_clock64();
+    u64 t_stream = 0;
+#endif
+    __shared__ int s_next;
+    if (tid == 0) {
+        s_thr = 0;
+        s_next = NW;
+    }
+    if (tid < NW * WaveTop<BUF>::TOPN) s_top[tid] = 0;
     __syncthreads();
     const size_t esz = DT == GBS_DTYPE_F32 ? 4 : 2;
     const void* row = (const char*)logits + (size_t)r * (size_t)stride * esz;
@@ -242,8 +257,8 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
     const int hi = min(vocab, lo + chunk);
 
     WaveTop<BUF> wt;
-    wt.init(s_buf[w], count, FLOOR_KEY, &s_thr, nullptr);
-    wt.set_slots(s_slots, w, NW);
+    wt.init(s_buf[w], count, FLOOR_KEY, &s_thr);
+    wt.set_top(s_top, w, NW);
     Lse lse{-INFINITY, 0.f};
 
     // the penalised logit of one element, in the operation order of the definition:
@@ -251,18 +266,16 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
     auto penalized = [&](float x, int c) {
         float v = x;
         if (COUNTS && !GBS_EXP_NOPEN) {
-            // branch-free: most counts are zero, but a divergent branch per element costs more than the arithmetic
             const float a = x * (x > 0.0f ? rinv : p.repetition);
             const float b = (float)c * p.frequency + p.presence;
             v = c > 0 ? a - b : x;
         }
         return v;
     };
-    auto logit = [&](float x, int c, u32 mbit) {
-        const float v = penalized(x, c);
-        return mbit ? v : -INFINITY;
-    };
     u32 nanv = 0;  // per lane: a NaN was seen
+#if GBS_EXP_STATS
+    int st_any = 0;
+#endif
     const float lse_c = clp;
     // one 4-element group: penalties, mask, NaN flag, keys offered to the wave list, online log-sum-exp.
     // The mask is applied with a bitfield insert: bfe_i32 of the element's bit is all ones or all zeros.
@@ -293,107 +306,122 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
         }
     };
 
-    const int step = NT * 4 * GROUPS;
     int e0 = lo;
     if (vec) {
-        // full steps: every group of every lane in bounds; the next step's loads are in flight while this one is ranked
-        const int nfull = (hi - lo) / step;
-        if (nfull > 0) {
-            RawStep<DT> cur, nxt;
-            const u32 esz = DT == GBS_DTYPE_F32 ? 4u : 2u;
-            const RowRsrc R{rsrc(row, (u32)vocab * esz), rsrc(crow, COUNTS ? (u32)vocab * 4u : 0u),
-                            rsrc(mrow, MASK ? (u32)((vocab + 31) / 32) * 4u : 0u)};
-            int e = lo + tid * 4;
-            load_step<DT, COUNTS, MASK>(R, (u32)e, cur);
-            {
-                // the gate starts at the count-th largest of the lanes' first-step maxima
-                u32 m = 0;
+        // Wave-steps of WSTEP contiguous elements (GROUPS 4-element groups per lane, GS apart): all of a wave-step's
+        // loads are issued together, then it is ranked in halves of HALF groups. Wave w takes wave-step w first (the
+        // gate is seeded from it); later wave-steps go to whichever wave asks first (an LDS counter), so that waves
+        // the memory system serves late do not hold the block. The last wave-step may run past the chunk: its loads
+        // stay inside the row (the buffer resource returns zeros past the row's end) and its out-of-chunk groups are
+        // masked to -inf.
+        const int nws = (hi - lo + WSTEP - 1) / WSTEP;
+        const u32 esz = DT == GBS_DTYPE_F32 ? 4u : 2u;
+        const RowRsrc R{rsrc(row, (u32)vocab * esz), rsrc(crow, COUNTS ? (u32)vocab * 4u : 0u),
+                        rsrc(mrow, MASK ? (u32)((vocab + 31) / 32) * 4u : 0u)};
+        constexpr int NE = HALF * 4;
+        auto penal_fn = [&](const RawStep<DT>& B, int h, int e, bool guard, float (&lv)[NE]) __attribute__((always_inline)) {
 #pragma unroll
-                for (int j = 0; j < GROUPS; ++j) {
-                    const int eg = e + j * NT * 4;
-                    float x[4];
-                    unpack_x<DT>(cur, j, x);
-                    const u32 mb = MASK ? (cur.m[j] >> (eg & 31)) & 0xFu : 0xFu;
+            for (int jj = 0; jj < HALF; ++jj) {
+                const int j = h * HALF + jj;
+                const int eg = e + j * GS;
+                float x[4];
+                unpack_x<DT>(B, j, x);
+                u32 mb = MASK ? (B.m[j] >> (eg & 31)) : 0xFu;
+                if (guard && eg >= hi) mb = 0u;
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const float v = logit(x[q], COUNTS ? (int)cur.c[j][q] : 0, (mb >> q) & 1u);
-                        const u32 k = v != v ? 0u : okey_f32_fast(v);
+                for (int q = 0; q < 4; ++q) {
+                    const u32 keep = (MASK || guard) ? (u32)__builtin_amdgcn_sbfe((int)mb, q, 1) : 0xFFFFFFFFu;
+                    float v = x[q];
+                    if (COUNTS && !GBS_EXP_NOPEN) {
+                        const int c = (int)B.c[j][q];
+                        if (ballot(c > 0 && keep != 0u)) v = penalized(x[q], c);
+                    }
+                    lv[jj * 4 + q] = __uint_as_float((__float_as_uint(v) & keep) | (0xFF800000u & ~keep));
+                }
+            }
+        };
+        // NaN flag, gate test and offers, online log-sum-exp of one half (element i of lane group jj: id e + jj*GS + q)
+        auto rank_fn = [&](const float (&lv)[NE], int e) __attribute__((always_inline)) {
+            bool nan_step = false;
+#pragma unroll
+            for (int i = 0; i < NE; i += 2) nan_step |= __builtin_isunordered(lv[i], lv[i + 1]);
+            nanv |= nan_step ? 1u : 0u;
+            float gm = lv[0];
+#pragma unroll
+            for (int i = 1; i < NE; ++i) gm = fmaxf(gm, lv[i]);
+            // the half's maximum against the gate first: most halves offer nothing (a NaN lane also tests its
+            // elements, whose NaN never passes)
+            if (!GBS_EXP_NOSEL && ballot(!(gm < wt.gate_f))) {
+#if GBS_EXP_STATS
+                ++st_any;
+#endif
+#pragma unroll
+                for (int jj = 0; jj < HALF; ++jj) {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) wt.offer_f(lv[jj * 4 + q], (u32)(e + jj * GS + q));
+                    wt.flush(false);
+                }
+            }
+            if (LOGPROB && !GBS_EXP_NOLSE) {
+                if (gm > lse.m) {
+                    lse.s = lse.m == -INFINITY ? 0.f : lse.s * __builtin_amdgcn_exp2f((lse.m - gm) * lse_c);
+                    lse.m = gm;
+                }
+                if (lse.m != -INFINITY) {
+                    const float mc = lse.m * lse_c;
+#pragma unroll
+                    for (int i = 0; i < NE; ++i)
+                        if (ballot(lv[i] != -INFINITY)) lse.s += __builtin_amdgcn_exp2f(__builtin_fmaf(lv[i], lse_c, -mc));
+                }
+            }
+        };
+        // rank one loaded wave-step (idx: its index; the last one is guarded; the first of each wave seeds the gate)
+        auto step_fn = [&](const RawStep<DT>& B, int e, int idx, bool first) __attribute__((always_inline)) {
+            const bool guard = idx == nws - 1;
+#pragma unroll
+            for (int h = 0; h < GROUPS / HALF; ++h) {
+                wt.apply_shared();
+                wt.prefetch_shared();
+                float lv[NE];
+                if (guard) penal_fn(B, h, e, true, lv);
+                else penal_fn(B, h, e, false, lv);
+                if (h == 0 && first) {
+                    // the gate starts from the lanes' maxima of the first half-step: the wave's count-th largest of
+                    // them, then the block bound of every wave's best ones
+                    u32 m = 0;
+#pragma unroll
+                    for (int i = 0; i < NE; ++i) {
+                        const u32 k = lv[i] != lv[i] ? 0u : okey_f32_fast(lv[i]);
                         m = k > m ? k : m;
                     }
+                    wt.seed(m);
+                    __syncthreads();
+                    wt.block_bound();
                 }
-                wt.seed(m);
+                rank_fn(lv, e + h * HALF * GS);
             }
-            // every wave has published its seeds: start from the block's bound
-            __syncthreads();
-            wt.prefetch_shared();
-            wt.apply_shared();
-            // Two register buffers in turn, so that no copy of a buffer forces its loads to complete early: the loads
-            // of step s + 1 stay in flight while step s is ranked.
-            auto step_fn = [&](const RawStep<DT>& B, int e) {
-                // the whole step straight-line: 16 logits, one gate test per element folded into one scalar mask,
-                // one branch per step into the (rare) offer path
-                constexpr int NE = GROUPS * 4;
-                float lv[NE];
-#pragma unroll
-                for (int j = 0; j < GROUPS; ++j) {
-                    const int eg = e + j * NT * 4;
-                    float x[4];
-                    unpack_x<DT>(B, j, x);
-                    const u32 mb = MASK ? (B.m[j] >> (eg & 31)) : 0xFu;
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const float v = penalized(x[q], COUNTS ? (int)B.c[j][q] : 0);
-                        const u32 keep = MASK ? (u32)__builtin_amdgcn_sbfe((int)mb, q, 1) : 0xFFFFFFFFu;
-                        lv[j * 4 + q] = __uint_as_float((__float_as_uint(v) & keep) | (0xFF800000u & ~keep));
-                    }
-                }
-                bool nan_step = false;
-#pragma unroll
-                for (int i = 0; i < NE; i += 2) nan_step |= __builtin_isunordered(lv[i], lv[i + 1]);
-                nanv |= nan_step ? 1u : 0u;
-                if (!GBS_EXP_NOSEL) {
-                    const float g = wt.gate_f;
-                    u64 anyp = 0;
-#pragma unroll
-                    for (int i = 0; i < NE; ++i) anyp |= ballot(lv[i] >= g);
-                    if (anyp) {
-#pragma unroll
-                        for (int j = 0; j < GROUPS; ++j) {
-#pragma unroll
-                            for (int q = 0; q < 4; ++q) wt.offer_f(lv[j * 4 + q], (u32)(e + j * NT * 4 + q));
-                            wt.flush(false);
-                        }
-                    }
-                }
-                if (LOGPROB && !GBS_EXP_NOLSE) {
-                    float gm = lv[0];
-#pragma unroll
-                    for (int i = 1; i < NE; ++i) gm = fmaxf(gm, lv[i]);
-                    if (gm > lse.m) {
-                        lse.s = lse.m == -INFINITY ? 0.f : lse.s * __builtin_amdgcn_exp2f((lse.m - gm) * lse_c);
-                        lse.m = gm;
-                    }
-                    if (lse.m != -INFINITY) {
-                        const float mc = lse.m * lse_c;
-#pragma unroll
-                        for (int i = 0; i < NE; ++i) lse.s += __builtin_amdgcn_exp2f(__builtin_fmaf(lv[i], lse_c, -mc));
-                    }
-                }
-            };
-            for (int s = 0; s < nfull; s += 2) {
-                wt.apply_shared();
-                wt.prefetch_shared();
-                load_step<DT, COUNTS, MASK>(R, (u32)(s + 1 < nfull ? e + step : e), nxt);
-                step_fn(cur, e);
-                if (s + 1 >= nfull) break;
-                wt.apply_shared();
-                wt.prefetch_shared();
-                load_step<DT, COUNTS, MASK>(R, (u32)(s + 2 < nfull ? e + 2 * step : e), cur);
-                step_fn(nxt, e + step);
-                e += 2 * step;
+        };
+        auto wstep_e = [&](int idx) { return lo + idx * WSTEP + l * 4; };
+        int idx = w;
+        for (bool first = true;; first = false) {
+            if (!first) {
+                int t = 0;
+                if (l == 0) t = __hip_atomic_fetch_add(&s_next, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                idx = __builtin_amdgcn_readfirstlane(t);
             }
+            if (idx >= nws) {
+                if (!first) break;
+                // no wave-step of its own: take part in the block's seeding barrier
+                wt.seed(0u);
+                __syncthreads();
+                wt.block_bound();
+                continue;
+            }
+            RawStep<DT> B;
+            load_step<DT, COUNTS, MASK>(R, (u32)wstep_e(idx), B);
+            step_fn(B, wstep_e(idx), idx, first);
         }
-        e0 = lo + nfull * step;
+        e0 = hi;
     }
     // the rest of the chunk (or all of it when 16-byte loads are not legal), one group per lane per round, guarded
     {
@@ -417,8 +445,20 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
     }
     wt.flush(true);
 
+#if GBS_EXP_TIMES
+    t_stream = wall_clock64();
+    __shared__ u64 s_tw[NW];
+    if (l == 0) s_tw[w] = t_stream;
+#endif
+#if GBS_EXP_STATS
+    if (l == 0) {
+        atomicAdd(out_greedy + r, st_any);
+        atomicAdd(out_status + r, wt.merges);
+    }
+#endif
     if (GBS_EXP_NOFINISH) {
-        if (l == 0) out_ids[r] = (int)(wt.list >> 40);
+        if (l == 0) out_ids[r] = (int)(wt.list >> 40) + (int)nanv;
+        if (l == 0 && out_probs) out_probs[r] = lse.s;
         return;
     }
     // block reduction: lists, LSE, NaN
@@ -488,6 +528,15 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
         if (out_probs) out_probs[r] = o.prob;
         if (out_logprobs) out_logprobs[r] = o.status == GBS_ROW_OK ? o.logprob : __uint_as_float(0x7fc00000u);
         if (out_status) out_status[r] = o.status;
+#if GBS_EXP_TIMES
+        const u64 t_end = wall_clock64();
+        u64 mn = ~0ull, mx = 0;
+        for (int o = 0; o < NW; ++o) { mn = s_tw[o] < mn ? s_tw[o] : mn; mx = s_tw[o] > mx ? s_tw[o] : mx; }
+        out_greedy[r] = (int)(t_start & 0x7fffffffu);
+        out_ids[r] = (int)(mn - t_start);
+        out_probs[r] = (float)(mx - t_start);
+        out_logprobs[r] = (float)(t_end - t_start);
+#endif
     }
 }
 
