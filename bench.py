@@ -90,7 +90,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: every box in this run has one, and the sampler shards by rows with no "
-              f"communication (see DESIGN.md). --gpus {args.gpus} is not supported.", file=sys.stderr)
+              f"communication. --gpus {args.gpus} is not supported.", file=sys.stderr)
         sys.exit(2)
     import numpy as np
     import torch

@@ -2,11 +2,13 @@
 // one caller uniform per row), exact in integer masses. The definition of every step is in gbs_modeu.hpp and in the
 // comment of sample_fast_k.
 //
-// Single-pass kernel (kmax in [1, 64]): grid (splits, rows) x 256 threads, one read of the row's logits, counts and
-// mask words. Per 4-element group a lane computes the penalised, masked logits, the order keys and the online log-sum-exp,
-// and offers the keys to its wave's gated top list. The block's lists, LSE and NaN flag go to the workspace; the last
-// block of the row merges them and finishes the row on one wave: masses of the <= 64 candidates, the exact top-p and
-// min-p cuts, and the draw in ascending id order.
+// Single-pass kernel (kmax in [1, 64]): grid (splits, rows) x 1024 threads; at 256 rows and more one block per row.
+// One read of the row's logits, counts and mask words, in wave-steps of 2048 contiguous elements handed out through an
+// LDS counter. Per element a lane computes the penalised, masked logit, the NaN flag and the online log-sum-exp, and
+// offers the order key to its wave's gated top-64 list. The waves' lists are merged by a tree in LDS; with one block per
+// row wave 0 then finishes the row (masses of the <= 64 candidates, the exact top-p cut and min-p filter, the draw in
+// ascending id order, the log-probability). With several blocks per row the blocks hand their lists, LSE and NaN flag
+// to the row's last block through the workspace.
 #include <type_traits>
 
 #include "gbs_modeu.hpp"
