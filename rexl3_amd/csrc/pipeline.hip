@@ -23,7 +23,7 @@ namespace {
 #define GBS_FAST_MINBLOCKS 1
 #endif
 #ifndef GBS_FAST_THREADS
-#define GBS_FAST_THREADS 1024
+#define GBS_FAST_THREADS 512
 #endif
 constexpr int NT = GBS_FAST_THREADS;
 constexpr int NW = NT / WAVE;
@@ -42,8 +42,11 @@ constexpr int NW = NT / WAVE;
 #ifndef GBS_EXP_TIMES
 #define GBS_EXP_TIMES 0
 #endif
+#ifndef GBS_EXP_ORACLE_GATE
+#define GBS_EXP_ORACLE_GATE 0
+#endif
 #ifndef GBS_FAST_GROUPS
-#define GBS_FAST_GROUPS 8
+#define GBS_FAST_GROUPS 4
 #endif
 #ifndef GBS_FAST_BLOCKS
 #define GBS_FAST_BLOCKS 256
@@ -109,9 +112,9 @@ struct RawStep {
     u32 m[GROUPS];
 };
 
-// Buffer resources of one row: the base is the row, out-of-range reads return zeros (never used: the main loop only
-// covers whole in-range steps). Offsets are in bytes; the per-group offsets are scalar, so a step's loads cost one
-// vector address add per array.
+// Buffer resources of one row (base, no stride, `bytes` records): a load at or past the row's end returns zeros and
+// touches no memory. Every offset, the per-group ones included, goes into the per-lane offset, which the range check
+// covers.
 struct RowRsrc {
     __amdgpu_buffer_rsrc_t x, c, m;
 };
@@ -120,16 +123,17 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, u32 byt
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
 
+// Issue one wave-step's loads (e: the lane's first element).
 template <int DT, bool COUNTS, bool MASK>
 __device__ __forceinline__ void load_step(const RowRsrc& R, u32 e, RawStep<DT>& r) {
     constexpr u32 ESZ = DT == GBS_DTYPE_F32 ? 4 : 2;
 #pragma unroll
     for (int j = 0; j < GROUPS; ++j) {
         // logits and counts are read once: non-temporal loads (cache policy bit 1)
-        if constexpr (DT == GBS_DTYPE_F32) r.x[j] = __builtin_amdgcn_raw_buffer_load_b128(R.x, e * ESZ, j * GS * ESZ, 2);
-        else r.x[j] = __builtin_amdgcn_raw_buffer_load_b64(R.x, e * ESZ, j * GS * ESZ, 2);
-        if constexpr (COUNTS) r.c[j] = __builtin_amdgcn_raw_buffer_load_b128(R.c, e * 4, j * GS * 4, 2);
-        if constexpr (MASK) r.m[j] = __builtin_amdgcn_raw_buffer_load_b32(R.m, (e >> 5) * 4, j * GS / 8, 0);
+        if constexpr (DT == GBS_DTYPE_F32) r.x[j] = __builtin_amdgcn_raw_buffer_load_b128(R.x, (e + j * GS) * ESZ, 0, 2);
+        else r.x[j] = __builtin_amdgcn_raw_buffer_load_b64(R.x, (e + j * GS) * ESZ, 0, 2);
+        if constexpr (COUNTS) r.c[j] = __builtin_amdgcn_raw_buffer_load_b128(R.c, (e + j * GS) * 4u, 0, 2);
+        if constexpr (MASK) r.m[j] = __builtin_amdgcn_raw_buffer_load_b32(R.m, ((e >> 5) + j * (GS / 32)) * 4u, 0, 0);
     }
 }
 
@@ -237,6 +241,7 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
 #if GBS_EXP_TIMES
     const u64 t_start = wall_clock64();
     u64 t_stream = 0;
+    __shared__ u64 s_tseed;
 #endif
     __shared__ int s_next;
     if (tid == 0) {
@@ -254,6 +259,7 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
     const bool invalid = params_invalid(p, u) || p.top_k < 1 || p.top_k > kmax;
     const int count = invalid ? 1 : p.top_k;
     const float rinv = 1.0f / p.repetition;
+    const float rep = p.repetition, freq = p.frequency, pres = p.presence;  // plain scalars for the element loop
     const float clp = p.temperature > 0.0f ? temp_scale(p.temperature) : 1.44269504088896340736f;
     const int lo = sp * chunk;
     const int hi = min(vocab, lo + chunk);
@@ -268,8 +274,8 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
     auto penalized = [&](float x, int c) {
         float v = x;
         if (COUNTS && !GBS_EXP_NOPEN) {
-            const float a = x * (x > 0.0f ? rinv : p.repetition);
-            const float b = (float)c * p.frequency + p.presence;
+            const float a = x * (x > 0.0f ? rinv : rep);
+            const float b = (float)c * freq + pres;
             v = c > 0 ? a - b : x;
         }
         return v;
@@ -321,7 +327,7 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
         const RowRsrc R{rsrc(row, (u32)vocab * esz), rsrc(crow, COUNTS ? (u32)vocab * 4u : 0u),
                         rsrc(mrow, MASK ? (u32)((vocab + 31) / 32) * 4u : 0u)};
         constexpr int NE = HALF * 4;
-        auto penal_fn = [&](const RawStep<DT>& B, int h, int e, bool guard, float (&lv)[NE]) __attribute__((always_inline)) {
+        auto penal_fn = [&](RawStep<DT>& B, int h, int e, bool guard, float (&lv)[NE]) __attribute__((always_inline)) {
 #pragma unroll
             for (int jj = 0; jj < HALF; ++jj) {
                 const int j = h * HALF + jj;
@@ -378,7 +384,7 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
             }
         };
         // rank one loaded wave-step (idx: its index; the last one is guarded; the first of each wave seeds the gate)
-        auto step_fn = [&](const RawStep<DT>& B, int e, int idx, bool first) __attribute__((always_inline)) {
+        auto step_fn = [&](RawStep<DT>& B, int e, int idx, bool first) __attribute__((always_inline)) {
             const bool guard = idx == nws - 1;
 #pragma unroll
             for (int h = 0; h < GROUPS / HALF; ++h) {
@@ -398,30 +404,49 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
                     }
                     wt.seed(m);
                     __syncthreads();
+#if GBS_EXP_TIMES
+                    if (tid == 0) s_tseed = wall_clock64();
+#endif
                     wt.block_bound();
+#if GBS_EXP_ORACLE_GATE
+                    if (p.reserved != 0) {
+                        const u64 t = ((u64)(u32)p.reserved << 32) - 1ull;
+                        if (t > wt.thr) wt.set_thr(t);
+                    }
+#endif
                 }
                 rank_fn(lv, e + h * HALF * GS);
             }
         };
         auto wstep_e = [&](int idx) { return lo + idx * WSTEP + l * 4; };
-        int idx = w;
-        for (bool first = true;; first = false) {
-            if (!first) {
-                int t = 0;
-                if (l == 0) t = __hip_atomic_fetch_add(&s_next, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-                idx = __builtin_amdgcn_readfirstlane(t);
+        // Two wave-steps in flight per wave: A and B alternate; a buffer is reloaded with the next wave-step as soon
+        // as it is ranked. A wave-step index at or past nws loads nothing and ends the loop.
+        auto grab = [&]() {
+            int t = 0;
+            if (l == 0) t = __hip_atomic_fetch_add(&s_next, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            return __builtin_amdgcn_readfirstlane(t);
+        };
+        RawStep<DT> A, B;
+        int ia = w;
+        int ib = grab();
+        if (ia < nws) load_step<DT, COUNTS, MASK>(R, (u32)wstep_e(ia), A);
+        if (ib < nws) load_step<DT, COUNTS, MASK>(R, (u32)wstep_e(ib), B);
+        if (ia >= nws) {
+            // no wave-step of its own: take part in the block's seeding barrier
+            wt.seed(0u);
+            __syncthreads();
+            wt.block_bound();
+        } else {
+            for (bool first = true;; first = false) {
+                step_fn(A, wstep_e(ia), ia, first);
+                ia = grab();
+                if (ia < nws) load_step<DT, COUNTS, MASK>(R, (u32)wstep_e(ia), A);
+                if (ib >= nws) break;
+                step_fn(B, wstep_e(ib), ib, false);
+                ib = grab();
+                if (ib < nws) load_step<DT, COUNTS, MASK>(R, (u32)wstep_e(ib), B);
+                if (ia >= nws) break;
             }
-            if (idx >= nws) {
-                if (!first) break;
-                // no wave-step of its own: take part in the block's seeding barrier
-                wt.seed(0u);
-                __syncthreads();
-                wt.block_bound();
-                continue;
-            }
-            RawStep<DT> B;
-            load_step<DT, COUNTS, MASK>(R, (u32)wstep_e(idx), B);
-            step_fn(B, wstep_e(idx), idx, first);
         }
         e0 = hi;
     }
@@ -535,7 +560,7 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
         u64 mn = ~0ull, mx = 0;
         for (int o = 0; o < NW; ++o) { mn = s_tw[o] < mn ? s_tw[o] : mn; mx = s_tw[o] > mx ? s_tw[o] : mx; }
         out_greedy[r] = (int)(t_start & 0x7fffffffu);
-        out_ids[r] = (int)(mn - t_start);
+        out_ids[r] = (int)(mn - t_start) | ((int)(s_tseed - t_start) << 16);
         out_probs[r] = (float)(mx - t_start);
         out_logprobs[r] = (float)(t_end - t_start);
 #endif
