@@ -283,6 +283,7 @@ struct WaveTop {
 #if GBS_EXP_STATS
     int merges = 0;
 #endif
+    static constexpr int INSERT_MAX = 6;  // survivors of a flush inserted one by one rather than sorted
     __device__ __forceinline__ void set_thr(u64 t) {
         thr = t;
         const u32 hi = (u32)(t >> 32);
@@ -397,6 +398,19 @@ struct WaveTop {
     }
 
     // merge buffered keys, 64 at a time; `all` also merges a partial group
+    // Insert one key (wave-uniform, above thr) into the descending list: its rank is the number of entries above it;
+    // the entries from that rank on move down one lane (the last one drops out).
+    __device__ __forceinline__ void insert(u64 k) {
+        const int l = lane_id();
+        const int pos = __popcll(ballot(list > k));
+        const u32 lo = (u32)__builtin_amdgcn_update_dpp(0, (int)(u32)list, 0x138, 0xF, 0xF, false);  // wave_shr:1
+        const u32 hi = (u32)__builtin_amdgcn_update_dpp(0, (int)(u32)(list >> 32), 0x138, 0xF, 0xF, false);
+        const u64 below = ((u64)hi << 32) | lo;
+        list = l < pos ? list : (l == pos ? k : below);
+    }
+
+    // merge buffered keys, 64 at a time; `all` also merges a partial group. Keys the gate has passed by since they
+    // were buffered are dropped first; a few survivors are inserted one by one, more are sorted and merged.
     __device__ __forceinline__ void flush(bool all) {
         if (n < WAVE && !(all && n > 0)) return;
         wave_lds_sync();
@@ -406,13 +420,28 @@ struct WaveTop {
             const int base = n - take;
             u64 g = l < take ? buf[base + l] : 0ull;
             n = base;
-            g = wave_sort_asc(g);
-            list = wave_merge_desc_asc(list, g);
+            u64 km = ballot(g > thr);
+            if (km == 0ull) continue;
 #if GBS_EXP_STATS
             ++merges;
 #endif
-            const u64 t = readlane64(list, count - 1);
-            if (t > thr) set_thr(t);
+            if (__popcll(km) <= INSERT_MAX) {
+                do {
+                    const int src = (int)__builtin_ctzll(km);
+                    km &= km - 1ull;
+                    const u64 k = readlane64(g, src);
+                    if (k > thr) {
+                        insert(k);
+                        const u64 t = readlane64(list, count - 1);
+                        if (t > thr) set_thr(t);
+                    }
+                } while (km);
+            } else {
+                g = wave_sort_asc(g > thr ? g : 0ull);
+                list = wave_merge_desc_asc(list, g);
+                const u64 t = readlane64(list, count - 1);
+                if (t > thr) set_thr(t);
+            }
         }
         publish();
         if (!all) publish_top();
@@ -498,16 +527,17 @@ __device__ __forceinline__ bool arrive_last(unsigned* counter, unsigned expected
 }
 
 // The top 64 of the NW waves' descending lists, in wave 0 (other waves: unspecified), by a pairwise tree in LDS:
-// log2(NW) merge levels instead of NW - 1 merges on one wave. All threads of the block call it; s_list must not be in
-// use by another wave when it is called.
+// ceil(log2(NW)) merge levels instead of NW - 1 merges on one wave. All threads of the block call it; s_list must not be
+// in use by another wave when it is called.
 template <int NW>
 __device__ __forceinline__ u64 block_tree_merge(u64 acc, u64 (*s_list)[WAVE]) {
     const int w = threadIdx.x / WAVE, l = lane_id();
     s_list[w][l] = acc;
     __syncthreads();
 #pragma unroll
-    for (int h = NW / 2; h >= 1; h >>= 1) {
-        if (w < h) {
+    for (int a = NW; a > 1; a = (a + 1) / 2) {
+        const int h = (a + 1) / 2;  // waves [0, a - h) take the list of wave w + h
+        if (w < a - h) {
             acc = wave_merge_desc(acc, s_list[w + h][l]);
             if (h > 1) s_list[w][l] = acc;
         }

@@ -25,6 +25,9 @@ namespace {
 #ifndef GBS_FAST_THREADS
 #define GBS_FAST_THREADS 512
 #endif
+#ifndef GBS_FAST_BUFS
+#define GBS_FAST_BUFS 2  // wave-steps in flight per wave
+#endif
 constexpr int NT = GBS_FAST_THREADS;
 constexpr int NW = NT / WAVE;
 #ifndef GBS_EXP_NOPEN
@@ -41,6 +44,9 @@ constexpr int NW = NT / WAVE;
 #endif
 #ifndef GBS_EXP_TIMES
 #define GBS_EXP_TIMES 0
+#endif
+#ifndef GBS_EXP_BARE
+#define GBS_EXP_BARE 0
 #endif
 #ifndef GBS_EXP_ORACLE_GATE
 #define GBS_EXP_ORACLE_GATE 0
@@ -334,6 +340,11 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
                 const int eg = e + j * GS;
                 float x[4];
                 unpack_x<DT>(B, j, x);
+#if GBS_EXP_BARE
+                for (int q = 0; q < 4; ++q)
+                    lv[jj * 4 + q] = __uint_as_float(__float_as_uint(x[q]) ^ (COUNTS ? (u32)B.c[j][q] : 0u) ^ (MASK ? B.m[j] : 0u));
+                continue;
+#endif
                 u32 mb = MASK ? (B.m[j] >> (eg & 31)) : 0xFu;
                 if (guard && eg >= hi) mb = 0u;
 #pragma unroll
@@ -350,24 +361,35 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
         };
         // NaN flag, gate test and offers, online log-sum-exp of one half (element i of lane group jj: id e + jj*GS + q)
         auto rank_fn = [&](const float (&lv)[NE], int e) __attribute__((always_inline)) {
+#if GBS_EXP_BARE
+            for (int i = 0; i < NE; ++i) nanv ^= __float_as_uint(lv[i]);
+            return;
+#endif
             bool nan_step = false;
 #pragma unroll
             for (int i = 0; i < NE; i += 2) nan_step |= __builtin_isunordered(lv[i], lv[i + 1]);
             nanv |= nan_step ? 1u : 0u;
-            float gm = lv[0];
+            // group maxima, then the half's maximum (a NaN element never raises either, and never passes the gate)
+            float gmax[HALF];
 #pragma unroll
-            for (int i = 1; i < NE; ++i) gm = fmaxf(gm, lv[i]);
-            // the half's maximum against the gate first: most halves offer nothing (a NaN lane also tests its
-            // elements, whose NaN never passes)
+            for (int jj = 0; jj < HALF; ++jj)
+                gmax[jj] = fmaxf(fmaxf(lv[jj * 4], lv[jj * 4 + 1]), fmaxf(lv[jj * 4 + 2], lv[jj * 4 + 3]));
+            float gm = gmax[0];
+#pragma unroll
+            for (int jj = 1; jj < HALF; ++jj) gm = fmaxf(gm, gmax[jj]);
+            // the gate in two levels: the half's maximum, then each group's; only a group with a candidate tests its
+            // elements (a lane whose values are all NaN also tests its elements, which never pass)
             if (!GBS_EXP_NOSEL && ballot(!(gm < wt.gate_f))) {
 #if GBS_EXP_STATS
                 ++st_any;
 #endif
 #pragma unroll
                 for (int jj = 0; jj < HALF; ++jj) {
+                    if (ballot(!(gmax[jj] < wt.gate_f))) {
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) wt.offer_f(lv[jj * 4 + q], (u32)(e + jj * GS + q));
-                    wt.flush(false);
+                        for (int q = 0; q < 4; ++q) wt.offer_f(lv[jj * 4 + q], (u32)(e + jj * GS + q));
+                        wt.flush(false);
+                    }
                 }
             }
             if (LOGPROB && !GBS_EXP_NOLSE) {
@@ -375,48 +397,50 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
                     lse.s = lse.m == -INFINITY ? 0.f : lse.s * __builtin_amdgcn_exp2f((lse.m - gm) * lse_c);
                     lse.m = gm;
                 }
-                if (lse.m != -INFINITY) {
+                // a half that is -inf on every lane adds exactly 0
+                if (lse.m != -INFINITY && ballot(gm != -INFINITY)) {
                     const float mc = lse.m * lse_c;
 #pragma unroll
-                    for (int i = 0; i < NE; ++i)
-                        if (ballot(lv[i] != -INFINITY)) lse.s += __builtin_amdgcn_exp2f(__builtin_fmaf(lv[i], lse_c, -mc));
+                    for (int i = 0; i < NE; ++i) lse.s += __builtin_amdgcn_exp2f(__builtin_fmaf(lv[i], lse_c, -mc));
                 }
             }
         };
         // rank one loaded wave-step (idx: its index; the last one is guarded; the first of each wave seeds the gate)
-        auto step_fn = [&](RawStep<DT>& B, int e, int idx, bool first) __attribute__((always_inline)) {
+        // rank one loaded wave-step (idx: its index; the last one is guarded; the first of each wave seeds the gate).
+        // `reload` runs as soon as the step's logits are computed: the buffer's registers are free from there on, so
+        // the next load is in flight while this step is ranked.
+        static_assert(GROUPS == HALF, "one half per wave-step");
+        auto step_fn = [&](RawStep<DT>& B, int e, int idx, bool first, auto&& reload) __attribute__((always_inline)) {
             const bool guard = idx == nws - 1;
+            wt.apply_shared();
+            wt.prefetch_shared();
+            float lv[NE];
+            if (guard) penal_fn(B, 0, e, true, lv);
+            else penal_fn(B, 0, e, false, lv);
+            if (first) {
+                // the gate starts from the lanes' maxima of the first wave-step: the wave's count-th largest of
+                // them, then the block bound of every wave's best ones
+                u32 m = 0;
 #pragma unroll
-            for (int h = 0; h < GROUPS / HALF; ++h) {
-                wt.apply_shared();
-                wt.prefetch_shared();
-                float lv[NE];
-                if (guard) penal_fn(B, h, e, true, lv);
-                else penal_fn(B, h, e, false, lv);
-                if (h == 0 && first) {
-                    // the gate starts from the lanes' maxima of the first half-step: the wave's count-th largest of
-                    // them, then the block bound of every wave's best ones
-                    u32 m = 0;
-#pragma unroll
-                    for (int i = 0; i < NE; ++i) {
-                        const u32 k = lv[i] != lv[i] ? 0u : okey_f32_fast(lv[i]);
-                        m = k > m ? k : m;
-                    }
-                    wt.seed(m);
-                    __syncthreads();
-#if GBS_EXP_TIMES
-                    if (tid == 0) s_tseed = wall_clock64();
-#endif
-                    wt.block_bound();
-#if GBS_EXP_ORACLE_GATE
-                    if (p.reserved != 0) {
-                        const u64 t = ((u64)(u32)p.reserved << 32) - 1ull;
-                        if (t > wt.thr) wt.set_thr(t);
-                    }
-#endif
+                for (int i = 0; i < NE; ++i) {
+                    const u32 k = lv[i] != lv[i] ? 0u : okey_f32_fast(lv[i]);
+                    m = k > m ? k : m;
                 }
-                rank_fn(lv, e + h * HALF * GS);
+                wt.seed(m);
+                __syncthreads();
+#if GBS_EXP_TIMES
+                if (tid == 0) s_tseed = wall_clock64();
+#endif
+                wt.block_bound();
+#if GBS_EXP_ORACLE_GATE
+                if (p.reserved != 0) {
+                    const u64 t = ((u64)(u32)p.reserved << 32) - 1ull;
+                    if (t > wt.thr) wt.set_thr(t);
+                }
+#endif
             }
+            reload();
+            rank_fn(lv, e);
         };
         auto wstep_e = [&](int idx) { return lo + idx * WSTEP + l * 4; };
         // Two wave-steps in flight per wave: A and B alternate; a buffer is reloaded with the next wave-step as soon
@@ -426,25 +450,45 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
             if (l == 0) t = __hip_atomic_fetch_add(&s_next, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             return __builtin_amdgcn_readfirstlane(t);
         };
+#if GBS_FAST_BUFS == 3
+        RawStep<DT> A, B, C;
+        int ia = w;
+        int ib = grab();
+        int ic = grab();
+        if (ia < nws) load_step<DT, COUNTS, MASK>(R, (u32)wstep_e(ia), A);
+        if (ib < nws) load_step<DT, COUNTS, MASK>(R, (u32)wstep_e(ib), B);
+        if (ic < nws) load_step<DT, COUNTS, MASK>(R, (u32)wstep_e(ic), C);
+#else
         RawStep<DT> A, B;
         int ia = w;
         int ib = grab();
         if (ia < nws) load_step<DT, COUNTS, MASK>(R, (u32)wstep_e(ia), A);
         if (ib < nws) load_step<DT, COUNTS, MASK>(R, (u32)wstep_e(ib), B);
+#endif
         if (ia >= nws) {
             // no wave-step of its own: take part in the block's seeding barrier
             wt.seed(0u);
             __syncthreads();
             wt.block_bound();
         } else {
+            // the buffers in turn; each is refilled with the next wave-step as soon as its logits are computed
+            auto refill = [&](RawStep<DT>& X, int& nx) {
+                nx = grab();
+                if (nx < nws) load_step<DT, COUNTS, MASK>(R, (u32)wstep_e(nx), X);
+            };
             for (bool first = true;; first = false) {
-                step_fn(A, wstep_e(ia), ia, first);
-                ia = grab();
-                if (ia < nws) load_step<DT, COUNTS, MASK>(R, (u32)wstep_e(ia), A);
+                int na = 0, nb = 0;
+                step_fn(A, wstep_e(ia), ia, first, [&]() { refill(A, na); });
+                ia = na;
                 if (ib >= nws) break;
-                step_fn(B, wstep_e(ib), ib, false);
-                ib = grab();
-                if (ib < nws) load_step<DT, COUNTS, MASK>(R, (u32)wstep_e(ib), B);
+                step_fn(B, wstep_e(ib), ib, false, [&]() { refill(B, nb); });
+                ib = nb;
+#if GBS_FAST_BUFS == 3
+                if (ic >= nws) break;
+                int nc = 0;
+                step_fn(C, wstep_e(ic), ic, false, [&]() { refill(C, nc); });
+                ic = nc;
+#endif
                 if (ia >= nws) break;
             }
         }
@@ -470,6 +514,9 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
             wt.flush(false);
         }
     }
+    // the latest block bound first: the last partial buffer is filtered against it
+    wt.prefetch_shared();
+    wt.apply_shared();
     wt.flush(true);
 
 #if GBS_EXP_TIMES
