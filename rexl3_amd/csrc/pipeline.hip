@@ -45,6 +45,9 @@ constexpr int NW = NT / WAVE;
 #ifndef GBS_EXP_TIMES
 #define GBS_EXP_TIMES 0
 #endif
+#ifndef GBS_EXP_NOFINISH2
+#define GBS_EXP_NOFINISH2 0
+#endif
 #ifndef GBS_EXP_BARE
 #define GBS_EXP_BARE 0
 #endif
@@ -167,6 +170,8 @@ struct RowOut {
     float prob, logprob;
 };
 
+constexpr int SMALL_KEPT = 16;  // kept sets up to this size skip the sort by id
+
 __device__ RowOut finish_row(u64 list, const RowParamsDev& p, float u, bool invalid, bool nan, int count, Lse lse, float clp) {
     RowOut o{-1, -1, GBS_ROW_OK, 0.f, __uint_as_float(0x7fc00000u)};
     const int l = lane_id();
@@ -195,8 +200,8 @@ __device__ RowOut finish_row(u64 list, const RowParamsDev& p, float u, bool inva
     } else {
         const float c2 = temp_scale(p.temperature);
         const u64 E = valid ? mass(lval, M, c2) : 0ull;
-        const u64 zk = wave_sum_u64(E);
         const u64 C = wave_scan_u64(E);
+        const u64 zk = readlane64(C, WAVE - 1);
         int keep = kn;
         if (p.top_p > 0.0f && p.top_p < 1.0f) {
             const u64 P = mul_ceil64(p.top_p, zk);
@@ -206,20 +211,48 @@ __device__ RowOut finish_row(u64 list, const RowParamsDev& p, float u, bool inva
         // min-p filters the top-p prefix (the first token, of mass 2^44 >= Q, always stays)
         const u64 Q = p.min_p > 0.0f ? mul_ceil64(p.min_p, MASS_ONE) : 0ull;
         const bool kept = l < keep && E >= Q;
+        const u64 km = ballot(kept);
         const u64 z = wave_sum_u64(kept ? E : 0ull);
         const u64 t = (u64)mul_floor(u, (u128)z, nullptr);
-        // kept tokens in ascending id order: sort (id, rank) pairs
-        const u64 sk = wave_sort_asc(kept ? (((u64)key_id(list) << 32) | (u64)l) : ~0ull);
-        const bool skept = sk != ~0ull;
-        const int rank = (int)(u32)sk;
-        const u64 Es = shfl64(E, skept ? rank : 0);
-        const u64 cum = wave_scan_u64(skept ? Es : 0ull);
-        const u64 hit = ballot(skept && cum > t);
-        const int f = hit ? (int)__builtin_ctzll(hit) : 0;
-        chosen_rank = (int)(u32)readlane64(sk, f);
-        o.id = (int)(readlane64(sk, f) >> 32);
-        const u64 ec = readlane64(Es, f);
-        o.prob = (float)((double)ec / (double)z);
+        if (__popcll(km) <= SMALL_KEPT) {
+            // few kept tokens: each one's running mass in ascending id order by a scalar loop over the others, then
+            // the smallest id whose running mass exceeds t
+            const u32 idj = key_id(list);
+            u64 cum = 0;
+            for (u64 mm = km; mm; mm &= mm - 1ull) {
+                const int i = (int)__builtin_ctzll(mm);
+                const u64 Ei = readlane64(E, i);
+                const u32 idi = (u32)__builtin_amdgcn_readlane((int)idj, i);
+                cum += idi <= idj ? Ei : 0ull;
+            }
+            u64 hit = ballot(kept && cum > t);
+            int f = (int)__builtin_ctzll(hit | (1ull << 63));
+            u32 best = 0xFFFFFFFFu;
+            for (; hit; hit &= hit - 1ull) {
+                const int i = (int)__builtin_ctzll(hit);
+                const u32 idi = (u32)__builtin_amdgcn_readlane((int)idj, i);
+                if (idi < best) {
+                    best = idi;
+                    f = i;
+                }
+            }
+            chosen_rank = f;
+            o.id = (int)best;
+            o.prob = (float)((double)readlane64(E, f) / (double)z);
+        } else {
+            // kept tokens in ascending id order: sort (id, rank) pairs
+            const u64 sk = wave_sort_asc(kept ? (((u64)key_id(list) << 32) | (u64)l) : ~0ull);
+            const bool skept = sk != ~0ull;
+            const int rank = (int)(u32)sk;
+            const u64 Es = shfl64(E, skept ? rank : 0);
+            const u64 cum = wave_scan_u64(skept ? Es : 0ull);
+            const u64 hit = ballot(skept && cum > t);
+            const int f = hit ? (int)__builtin_ctzll(hit) : 0;
+            chosen_rank = (int)(u32)readlane64(sk, f);
+            o.id = (int)(readlane64(sk, f) >> 32);
+            const u64 ec = readlane64(Es, f);
+            o.prob = (float)((double)ec / (double)z);
+        }
     }
     // log-softmax of the chosen token over the allowed tokens, base-2 online sums
     const float lx = __uint_as_float(readlane32(__float_as_uint(lval), chosen_rank));
@@ -588,13 +621,18 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
         }
     }
     if (LOGPROB) {
-#pragma unroll
-        for (int m = 1; m < WAVE; m <<= 1) {
+        // only the first `span` lanes hold partial sums: a butterfly over them leaves the total in lane 0
+        const int span = S == 1 ? NW : (S < WAVE ? S : WAVE);
+        for (int m = 1; m < span; m <<= 1) {
             Lse o{__shfl_xor(rl.m, m, WAVE), __shfl_xor(rl.s, m, WAVE)};
             rl = lse_merge(rl, o, clp);
         }
     }
     rn = wave_or(rn);
+#if GBS_EXP_NOFINISH2
+    if (l == 0) out_ids[r] = (int)(list >> 40) + (int)rn + (int)rl.s;
+    return;
+#endif
     const RowOut o = finish_row(list, p, u, invalid, rn != 0u, count, rl, clp);
     if (l == 0) {
         out_ids[r] = o.id;
