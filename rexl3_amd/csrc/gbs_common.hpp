@@ -260,6 +260,15 @@ __device__ __forceinline__ u64 wave_scan_u64(u64 v) {
     return v;
 }
 
+__device__ __forceinline__ u64 wave_max_u64(u64 v) {
+#pragma unroll
+    for (int m = 1; m < WAVE; m <<= 1) {
+        const u64 o = xor_lane64(v, m);
+        v = o > v ? o : v;
+    }
+    return v;
+}
+
 __device__ __forceinline__ u32 wave_or(u32 v) {
 #pragma unroll
     for (int m = 1; m < WAVE; m <<= 1) v |= (u32)__shfl_xor((int)v, m, WAVE);

@@ -192,10 +192,15 @@ int keyed_splits(int rows, int valid) {
 
 size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
+// The per-row arrival counters (zero between launches) sit at fixed offsets in the first KEYED_CTL_BYTES, room for
+// 65535 rows whatever this launch's row count; the partial lists after them are written before they are read. So a
+// workspace cleared once serves launches of any shape.
+constexpr size_t KEYED_CTL_BYTES = (size_t)65536 * 4;
+
 size_t keyed_ws_bytes(int rows, int valid) {
     if (rows <= 0 || valid <= 0) return 0;
     const int s = keyed_splits(rows, valid);
-    return align256((size_t)rows * 4) + (size_t)rows * s * WAVE * sizeof(u64);
+    return KEYED_CTL_BYTES + (size_t)rows * s * WAVE * sizeof(u64);
 }
 
 __device__ __forceinline__ bool keyed_params_ok(const KeyedRowDev& p) {
@@ -350,7 +355,7 @@ GBS_EXPORT int gbs_keyed_sample_rows(const void* logits, int dtype, int rows, in
     int chunk = (valid + S - 1) / S;
     chunk = (chunk + 3) / 4 * 4;
     unsigned* counters = (unsigned*)ws;
-    u64* parts = (u64*)((char*)ws + align256((size_t)rows * 4));
+    u64* parts = (u64*)((char*)ws + KEYED_CTL_BYTES);
     const dim3 grid(S, rows);
     const KeyedRowDev* p = (const KeyedRowDev*)params;
     if (dtype == GBS_DTYPE_F32)

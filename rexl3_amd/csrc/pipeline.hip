@@ -84,26 +84,27 @@ int fast_splits(int rows, int vocab) {
     return s;
 }
 
+// Workspace. Its first CTL_BYTES hold the per-row arrival counters, which must be zero between launches, at offsets that
+// depend only on the row (room for 65535 rows whatever this launch's row count); every launch leaves them zero. The
+// partial results after them are written before they are read. So a workspace cleared once serves launches of any
+// shape.
+constexpr size_t CTL_BYTES = (size_t)65536 * 4;
+
 struct FastWs {
-    unsigned* counters;  // [rows]
-    u64* row_thr;        // [rows] the row's shared gate, reset by the row's last block
-    u64* lists;          // [rows][S][64]
-    Lse* lse;            // [rows][S]
-    unsigned* nan;       // [rows][S]
+    unsigned* arrive;  // [rows] the row's blocks that have handed over their partials
+    u64* lists;     // [rows][S][64]
+    Lse* lse;       // [rows][S]
+    unsigned* nan;  // [rows][S]
 };
 
-size_t fast_ws_bytes(int rows, int vocab, int S) {
-    return align256((size_t)rows * 4) + align256((size_t)rows * 8) + align256((size_t)rows * S * WAVE * 8) +
-           align256((size_t)rows * S * sizeof(Lse)) + align256((size_t)rows * S * 4);
+size_t fast_part_bytes(int rows, int S) {
+    return align256((size_t)rows * S * WAVE * 8) + align256((size_t)rows * S * sizeof(Lse)) + align256((size_t)rows * S * 4);
 }
 
 FastWs fast_ws(void* ws, int rows, int S) {
-    char* p = (char*)ws;
+    char* p = (char*)ws + CTL_BYTES;
     FastWs w;
-    w.counters = (unsigned*)p;
-    p += align256((size_t)rows * 4);
-    w.row_thr = (u64*)p;
-    p += align256((size_t)rows * 8);
+    w.arrive = (unsigned*)ws;
     w.lists = (u64*)p;
     p += align256((size_t)rows * S * WAVE * 8);
     w.lse = (Lse*)p;
@@ -259,6 +260,15 @@ __device__ RowOut finish_row(u64 list, const RowParamsDev& p, float u, bool inva
     if (isinf(M)) o.logprob = __uint_as_float(0x7fc00000u);
     else o.logprob = ((lx - lse.m) * clp - log2f(lse.s)) * 0.6931471805599453f;
     return o;
+}
+
+__device__ __forceinline__ void write_row(int r, const RowOut& o, int* out_ids, int* out_greedy, float* out_probs,
+                                          float* out_logprobs, int* out_status) {
+    out_ids[r] = o.id;
+    if (out_greedy) out_greedy[r] = o.greedy;
+    if (out_probs) out_probs[r] = o.prob;
+    if (out_logprobs) out_logprobs[r] = o.status == GBS_ROW_OK ? o.logprob : __uint_as_float(0x7fc00000u);
+    if (out_status) out_status[r] = o.status;
 }
 
 template <int DT, bool COUNTS, bool MASK, bool LOGPROB>
@@ -608,8 +618,7 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
                 st_agent(&ws.nan[slot], bn);
             }
         }
-        if (!arrive_last(&ws.counters[r], (unsigned)S, &s_flag)) return;
-        if (tid == 0) st_agent(&ws.row_thr[r], (u64)0);
+        if (!arrive_last(&ws.arrive[r], (unsigned)S, &s_flag)) return;
         list = block_merge_lists<NW>(ws.lists + (size_t)r * S * WAVE, S, s_list);
         if (w != 0) return;
         for (int o = l; o < S; o += WAVE) {
@@ -652,30 +661,17 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
     }
 }
 
-template <int DT, bool COUNTS, bool MASK, bool LOGPROB>
-void launch_fast(dim3 grid, hipStream_t st, const void* logits, long long stride, int vocab, int chunk, const int* counts,
-                 const u32* mask, const RowParamsDev* params, const float* uniforms, int kmax, bool vec, FastWs ws, int* out_ids,
-                 int* out_greedy, float* out_probs, float* out_logprobs, int* out_status) {
-    hipLaunchKernelGGL((sample_fast_k<DT, COUNTS, MASK, LOGPROB>), grid, dim3(NT), 0, st, logits, stride, vocab, chunk, counts, mask,
-                       params, uniforms, kmax, vec, ws, out_ids, out_greedy, out_probs, out_logprobs, out_status);
-}
-
-template <int DT>
-void dispatch_fast(bool c, bool m, bool lp, dim3 grid, hipStream_t st, const void* logits, long long stride, int vocab, int chunk,
-                   const int* counts, const u32* mask, const RowParamsDev* params, const float* uniforms, int kmax, bool vec,
-                   FastWs ws, int* out_ids, int* out_greedy, float* out_probs, float* out_logprobs, int* out_status) {
-#define GBS_FAST(C, M, L)                                                                                                      \
-    launch_fast<DT, C, M, L>(grid, st, logits, stride, vocab, chunk, counts, mask, params, uniforms, kmax, vec, ws, out_ids,   \
-                             out_greedy, out_probs, out_logprobs, out_status)
-    if (c && m && lp) GBS_FAST(true, true, true);
-    else if (c && m) GBS_FAST(true, true, false);
-    else if (c && lp) GBS_FAST(true, false, true);
-    else if (c) GBS_FAST(true, false, false);
-    else if (m && lp) GBS_FAST(false, true, true);
-    else if (m) GBS_FAST(false, true, false);
-    else if (lp) GBS_FAST(false, false, true);
-    else GBS_FAST(false, false, false);
-#undef GBS_FAST
+// calls f.template operator()<COUNTS, MASK, LOGPROB>() for the run-time flags
+template <class F>
+void dispatch_flags(bool c, bool m, bool lp, F&& f) {
+    if (c && m && lp) f.template operator()<true, true, true>();
+    else if (c && m) f.template operator()<true, true, false>();
+    else if (c && lp) f.template operator()<true, false, true>();
+    else if (c) f.template operator()<true, false, false>();
+    else if (m && lp) f.template operator()<false, true, true>();
+    else if (m) f.template operator()<false, true, false>();
+    else if (lp) f.template operator()<false, false, true>();
+    else f.template operator()<false, false, false>();
 }
 
 }  // namespace
@@ -683,7 +679,7 @@ void dispatch_fast(bool c, bool m, bool lp, dim3 grid, hipStream_t st, const voi
 GBS_EXPORT size_t gbs_sample_workspace_bytes(int rows, int vocab, int kmax) {
     if (rows <= 0 || vocab <= 0 || vocab > GBS_MAX_VOCAB || kmax < 0 || kmax > GBS_MAX_COUNT) return 0;
     if (kmax == 0) return 256;  // the full-distribution path keeps its state in LDS
-    return fast_ws_bytes(rows, vocab, fast_splits(rows, vocab));
+    return CTL_BYTES + fast_part_bytes(rows, fast_splits(rows, vocab));
 }
 
 GBS_EXPORT int gbs_sample_rows(const void* logits, int dtype, int rows, int stride, int vocab, const int32_t* counts, const uint32_t* mask,
@@ -698,22 +694,21 @@ GBS_EXPORT int gbs_sample_rows(const void* logits, int dtype, int rows, int stri
                                   out_logprobs, out_status, stream);
     if (!ws || !aligned(ws, 256)) return GBS_ERR_INVALID;
     const int S = fast_splits(rows, vocab);
-    if (ws_bytes < fast_ws_bytes(rows, vocab, S)) return GBS_ERR_INVALID;
+    if (ws_bytes < gbs_sample_workspace_bytes(rows, vocab, kmax)) return GBS_ERR_INVALID;
     int chunk = (vocab + S - 1) / S;
     chunk = (chunk + 31) / 32 * 32;  // whole mask words per chunk
     const size_t esz = dtype == GBS_DTYPE_F32 ? 4 : 2;
     const bool vec = stride % 4 == 0 && vocab % 4 == 0 && aligned(logits, 4 * esz) && (!counts || aligned(counts, 16));
-    const dim3 grid(S, rows);
-    const FastWs w = fast_ws(ws, rows, S);
     const hipStream_t st = to_stream(stream);
     const RowParamsDev* p = (const RowParamsDev*)params;
-    if (dtype == GBS_DTYPE_F32)
-        dispatch_fast<GBS_DTYPE_F32>(counts != nullptr, mask != nullptr, out_logprobs != nullptr, grid, st, logits, stride, vocab, chunk,
-                                     counts, mask, p, uniforms, kmax, vec, w, out_ids, out_greedy, out_probs, out_logprobs,
-                                     out_status);
-    else
-        dispatch_fast<GBS_DTYPE_BF16>(counts != nullptr, mask != nullptr, out_logprobs != nullptr, grid, st, logits, stride, vocab,
-                                      chunk, counts, mask, p, uniforms, kmax, vec, w, out_ids, out_greedy, out_probs, out_logprobs,
-                                      out_status);
+    const FastWs w = fast_ws(ws, rows, S);
+    auto run = [&]<int DT>() {
+        dispatch_flags(counts != nullptr, mask != nullptr, out_logprobs != nullptr, [&]<bool C, bool M, bool L>() {
+            hipLaunchKernelGGL((sample_fast_k<DT, C, M, L>), dim3(S, rows), dim3(NT), 0, st, logits, (long long)stride, vocab, chunk,
+                               counts, mask, p, uniforms, kmax, vec, w, out_ids, out_greedy, out_probs, out_logprobs, out_status);
+        });
+    };
+    if (dtype == GBS_DTYPE_F32) run.template operator()<GBS_DTYPE_F32>();
+    else run.template operator()<GBS_DTYPE_BF16>();
     return launch_status();
 }

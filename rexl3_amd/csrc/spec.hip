@@ -57,6 +57,11 @@ struct SpecWs {
     u128* wparts;            // [n_seq][S3]
 };
 
+// The counters that must be zero between launches sit at fixed offsets in the first SPEC_CTL_BYTES (room for 65535
+// rows and sequences, whatever this launch's shape); every launch leaves them zero. The rest is written before it is
+// read, so a workspace cleared once serves launches of any shape.
+constexpr size_t SPEC_CTL_BYTES = 3 * (size_t)65536 * 4;
+
 struct Plan {
     int R, S, S3;
     size_t bytes;
@@ -67,18 +72,18 @@ Plan plan(int n_seq, int width, int vocab) {
     p.R = n_seq * (width + 1);
     p.S = splits_for(p.R, vocab);
     p.S3 = splits_for(n_seq, vocab);
-    p.bytes = align256((size_t)p.R * 4) + 2 * align256((size_t)n_seq * 4) + align256((size_t)p.R * p.S * 16) +
-              align256((size_t)p.R * p.S * 4) + align256((size_t)p.R * p.S * 16) + align256((size_t)p.R * sizeof(RowInfo)) +
-              align256((size_t)n_seq * sizeof(SeqInfo)) + align256((size_t)n_seq * p.S3 * 16);
+    p.bytes = SPEC_CTL_BYTES + align256((size_t)p.R * p.S * 16) + align256((size_t)p.R * p.S * 4) + align256((size_t)p.R * p.S * 16) +
+              align256((size_t)p.R * sizeof(RowInfo)) + align256((size_t)n_seq * sizeof(SeqInfo)) +
+              align256((size_t)n_seq * p.S3 * 16);
     return p;
 }
 
 SpecWs carve(void* ws, int n_seq, const Plan& p) {
     char* c = (char*)ws;
     SpecWs w;
-    w.row_counters = (unsigned*)c; c += align256((size_t)p.R * 4);
-    w.seq_counters = (unsigned*)c; c += align256((size_t)n_seq * 4);
-    w.draw_counters = (unsigned*)c; c += align256((size_t)n_seq * 4);
+    w.row_counters = (unsigned*)c; c += (size_t)65536 * 4;
+    w.seq_counters = (unsigned*)c; c += (size_t)65536 * 4;
+    w.draw_counters = (unsigned*)c; c += (size_t)65536 * 4;
     w.maxparts = (u64*)c; c += align256((size_t)p.R * p.S * 16);
     w.nanparts = (unsigned*)c; c += align256((size_t)p.R * p.S * 4);
     w.sumparts = (u64*)c; c += align256((size_t)p.R * p.S * 16);

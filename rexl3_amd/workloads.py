@@ -132,11 +132,11 @@ def config1(seed: int = 1):
     return dict(logits=x, dtype="f32", params=p, uniforms=uniforms_f32(seed + 2, 1), counts=None, mask=None)
 
 
-def config2(seed: int = 2):
-    B, V = 64, 151_936
+def config2(seed: int = 2, rows: int = 64):
+    B, V = rows, 151_936
     x = peaked_logits(seed, B, V, 1.0, (4, 16), 6.0, 14.0)
     t = (0.5 + 0.7 * unit(seed + 3, B)).astype(np.float32)
-    t[[5, 17, 33, 60]] = 0.0
+    t[[i for i in (5, 17, 33, 60) if i < B]] = 0.0
     p = row_params(B, temperature=t, top_p=0.95, min_p=0.05, top_k=40)
     return dict(logits=to_bf16_bits(x), dtype="bf16", params=p, uniforms=uniforms_f32(seed + 4, B), counts=None, mask=None)
 

@@ -204,3 +204,17 @@ def test_greedy_gather_and_accept_steps():
         want = O.accept_tree(toks[t], parents[t], smp[t])
         assert list(path[t, :plen[t]]) == want
         assert (path[t, plen[t]:] == -1).all()
+
+
+def test_fused_keyed_workspace_reused_across_row_counts():
+    """One workspace serves launches of different row counts (the arrival counters sit at fixed per-row offsets)."""
+    need_gpu()
+    vocab = 20_000
+    shapes = [300, 2, 300, 64, 300]
+    for i, rows in enumerate(shapes):
+        x = W.peaked_logits(500 + i, rows, vocab, 2.0, (4, 16), 6.0, 14.0)
+        recs = S.keyed_rows([S.Sampling(seed=5 + i, temperature=0.9, top_k=40, top_p=0.9, min_p=0.0)] * rows, list(range(rows)))
+        log(f"keyed workspace reuse rows={rows}")
+        gi, gs, _ = S.keyed_sample_rows(dev(x), recs, 0)
+        wi, _, ws = O.keyed_sample_rows(x, O.DTYPE_F32, vocab, recs, 0)
+        assert np.array_equal(host(gs), ws) and np.array_equal(host(gi), wi), rows

@@ -1,5 +1,6 @@
 """The extended pipeline (gbs_sample_rows) on the GPU against the oracle: token ids, greedy ids and statuses bit-exact;
-probabilities within 1e-5 relative; log-probabilities within 1e-5 relative (the oracle computes them in double)."""
+probabilities within 1e-5 relative; log-probabilities within 1e-5 absolute, i.e. the probability they stand for within 1e-5
+relative (the oracle computes them in double, the device sums the softmax denominator in f32)."""
 import numpy as np
 import pytest
 import torch
@@ -11,6 +12,7 @@ from tests.gpu_util import dev, host, log, need_gpu
 
 pytestmark = pytest.mark.gpu
 RTOL = 1e-5
+LOGPROB_ATOL = 1e-5
 
 
 def run_both(cfg, kmax=64, logprobs=True):
@@ -36,7 +38,8 @@ def compare(g, w, what):
     np.testing.assert_allclose(g["probs"][ok], w["probs"][ok], rtol=RTOL, atol=0, err_msg=what)
     if "logprobs" in g:
         fin = ok & np.isfinite(w["logprobs"])
-        np.testing.assert_allclose(g["logprobs"][fin], w["logprobs"][fin], rtol=RTOL, atol=1e-6, err_msg=what)
+        # an absolute error of 1e-5 in a log-probability is a relative error of 1e-5 in the probability it stands for
+        np.testing.assert_allclose(g["logprobs"][fin], w["logprobs"][fin], rtol=0, atol=LOGPROB_ATOL, err_msg=what)
 
 
 def test_config1_single_row():
@@ -168,3 +171,88 @@ def test_full_path_large_top_k_ties_and_min_p():
     cfg = dict(logits=x, dtype="f32", params=p, uniforms=u, counts=None, mask=None)
     g, w = run_both(cfg, kmax=0)
     compare(g, w, "ties")
+
+
+# ---------------------------------------------------------------- full batches (one block per row)
+
+def test_northstar_full_size_and_repeated_launches():
+    """The north star at its full size (256 rows x 151,936); every launch leaves the workspace's counters at zero, so
+    repeated launches give the same results."""
+    need_gpu()
+    cfg = W.northstar()
+    log("northstar 256 x 151936")
+    g, w = run_both(cfg)
+    compare(g, w, "northstar full")
+    t = dev(cfg["logits"])
+    c, m, u = dev(cfg["counts"]), dev(cfg["mask"]), dev(cfg["uniforms"])
+    for rep in range(3):
+        again = S.sample_rows(t, cfg["params"], u, c, m, kmax=64, logprobs=True)
+        assert np.array_equal(host(again["ids"]), g["ids"]), rep
+        assert np.array_equal(host(again["status"]), g["status"]), rep
+        np.testing.assert_allclose(host(again["probs"]), g["probs"], rtol=0, atol=0)
+
+
+def test_more_rows_than_cus_and_short_rows():
+    """More rows than CUs, and rows of few wave-steps (fewer than a block has waves, a ragged last wave-step)."""
+    need_gpu()
+    for rows, vocab in [(300, 151_936), (600, 40_000), (512, 5_000), (257, 36_868)]:
+        cfg = W.northstar(seed=rows, rows=rows, vocab=vocab)
+        log(f"northstar rows={rows} vocab={vocab}")
+        g, w = run_both(cfg)
+        compare(g, w, f"rows {rows} vocab {vocab}")
+
+
+def test_full_batches_bf16_masks_and_edge_rows():
+    """bf16 logits and the grammar-mask workload at full batch sizes, plus the edge rows of test_edge_rows placed inside a
+    full batch."""
+    need_gpu()
+    cfg = W.config2(rows=320)
+    log("config2 bf16 rows=320")
+    g, w = run_both(cfg)
+    compare(g, w, "config2 320 rows")
+    cfg = W.config4(rows=256)
+    log("config4 rows=256")
+    g, w = run_both(cfg)
+    compare(g, w, "config4 256 rows")
+    # edge rows: nothing allowed, NaN, T=0, invalid parameters, +inf, ties, extreme uniforms, among ordinary rows
+    rng = np.random.default_rng(19)
+    B, V = 272, 20_000
+    x = rng.standard_normal((B, V)).astype(np.float32)
+    mask = np.full((B, (V + 31) // 32), 0xFFFFFFFF, dtype=np.uint32)
+    counts = rng.integers(0, 3, (B, V)).astype(np.int32)
+    p = S.row_params(B, temperature=0.9, top_p=0.8, min_p=0.1, top_k=30, repetition=1.2, presence=0.2, frequency=0.1)
+    u = W.uniforms_f32(7, B)
+    mask[0] = 0
+    x[1, 77] = np.nan
+    x[2, 19_999] = np.nan
+    mask[2, 19_999 // 32] &= ~np.uint32(1 << (19_999 % 32))
+    p[3]["temperature"] = 0.0
+    p[5]["temperature"] = -1.0
+    u[6] = 1.0
+    x[7, 100] = np.inf
+    x[7, 15_000] = np.inf
+    x[9, :] = 1.25
+    counts[9] = 0
+    u[11] = np.float32(0.99999994)
+    u[12] = 0.0
+    x[14, :] = -0.0
+    x[14, 10] = 0.0
+    p[15]["top_k"] = 1
+    p[200]["top_k"] = 64
+    cfg = dict(logits=x, dtype="f32", params=p, uniforms=u, counts=counts, mask=mask)
+    g, w = run_both(cfg)
+    compare(g, w, "edge rows in a full batch")
+    assert list(g["status"][:3]) == [1, 2, 0] and g["status"][5] == 3 and g["status"][6] == 3
+
+
+def test_workspace_reused_across_row_counts():
+    """One workspace serves launches of different row counts: the counters that must be zero between launches sit at
+    fixed per-row offsets, so partial lists written by one shape never land where another shape counts."""
+    need_gpu()
+    big = W.northstar(seed=31, rows=300, vocab=30_000)
+    small = W.northstar(seed=32, rows=8, vocab=30_000)
+    for cfg, what in [(big, "300 rows"), (small, "8 rows (split kernel)"), (big, "300 rows again"),
+                      (W.config4(rows=3), "3 rows"), (big, "300 rows a third time")]:
+        log(what)
+        g, w = run_both(cfg)
+        compare(g, w, what)

@@ -46,3 +46,13 @@ def test_spec_greedy_and_errors():
     (a, t, s), (wa, wt, ws) = run(cfg)
     assert list(ws) == [0, 3, 2, 3, 1, 0]
     assert np.array_equal(s, ws) and np.array_equal(a, wa) and np.array_equal(t, wt)
+
+
+def test_spec_workspace_reused_across_shapes():
+    """One workspace serves launches of different shapes (the counters sit at fixed per-row and per-sequence offsets)."""
+    need_gpu()
+    for i, (n_seq, width) in enumerate([(40, 7), (2, 1), (40, 7), (9, 3), (40, 7)]):
+        cfg = W.config5(seed=60 + i, n_seq=n_seq, width=width, vocab=3000)
+        log(f"spec workspace reuse n_seq={n_seq} width={width}")
+        (a, t, s), (wa, wt, ws) = run(cfg)
+        assert np.array_equal(s, ws) and np.array_equal(a, wa) and np.array_equal(t, wt), (n_seq, width)
