@@ -229,7 +229,7 @@ def main():
         ms = time_launches(launch, args.steps, args.warmup)
         rows = R
         nbytes = 2 * R * vocab * 4
-        kernel = "spec_max_k + spec_mass_k + spec_draw_k"
+        kernel = "spec_rows_k + spec_draw_k" if R >= 192 else "spec_max_k + spec_mass_k + spec_draw_k"
         dtype = "f32 (integer masses)"
         workload = "config 5: speculative verification, 32 sequences x (7 drafts + 1 bonus), rejection + residual resampling"
     else:

@@ -40,7 +40,7 @@ __device__ __forceinline__ float penalize(float x, int c, float rinv, float rep,
 }
 
 // 2^f, f in [-0.5, 0.5]: degree-7 Taylor series of exp(f ln 2), Horner form in fused multiply-adds
-__device__ __forceinline__ float pow2_frac(float f) {
+__host__ __device__ __forceinline__ float pow2_frac(float f) {
     float p = 1.52527338e-05f;
     p = fmaf(p, f, 1.54035304e-04f);
     p = fmaf(p, f, 1.33335581e-03f);
@@ -69,6 +69,39 @@ __device__ __forceinline__ u64 mass(float l, float M, float c2) {
     if (sh <= -32) return 0ull;
     return (u64)(m >> (-sh));
 }
+
+// 2^24 * pow2_frac(f), bit for bit: every coefficient of the Horner form scaled by 2^24 (a power of two, so each fused
+// multiply-add rounds to exactly 2^24 times the unscaled one; no value comes near the subnormal or overflow range).
+__host__ __device__ __forceinline__ float pow2_frac_2p24(float f) {
+    float p = 1.52527338e-05f * 16777216.0f;
+    p = fmaf(p, f, 1.54035304e-04f * 16777216.0f);
+    p = fmaf(p, f, 1.33335581e-03f * 16777216.0f);
+    p = fmaf(p, f, 9.61812911e-03f * 16777216.0f);
+    p = fmaf(p, f, 5.55041087e-02f * 16777216.0f);
+    p = fmaf(p, f, 2.40226507e-01f * 16777216.0f);
+    p = fmaf(p, f, 6.93147181e-01f * 16777216.0f);
+    p = fmaf(p, f, 16777216.0f);
+    return p;
+}
+
+// mass() without branches or selections, for streaming sums. Preconditions: c2 and M finite, and l <= M or l = -inf
+// (M is the maximum of the values it is applied to). Bit-identical to mass() there:
+//  - y = (l - M) * c2 <= 0 is clamped at -51 (a NaN y cannot occur: l - M is never inf - inf). Every y < -25.5 has
+//    mass 0 under mass() (n <= -26, and m < 2^25 is shifted right by >= 26 bits, or y < -64), and so has the clamped
+//    y = -51: m = 2^24 shifted right by 31 bits.
+//  - Otherwise n = rint(y) in [-51, 0], m = (u32)(2^24 * 2^f) < 2^25, and (m * 2^32) >> (12 - n) with a shift in
+//    [12, 63] is m << (n + 20) for n + 20 >= 0 and m >> -(n + 20) below, as mass() computes.
+//  - l == M gives y = 0 (c2 finite): n = 0, f = 0, m = 2^24 exactly, and 2^56 >> 12 = 2^44 = MASS_ONE.
+__host__ __device__ __forceinline__ u64 mass_fast(float l, float M, float c2) {
+    const float y = fmaxf((l - M) * c2, -51.0f);
+    const float n = rintf(y);
+    const u32 m = (u32)pow2_frac_2p24(y - n);
+    const u32 s = (u32)(12 - (int)n);
+    return ((u64)m << 32) >> s;
+}
+
+// whether mass_fast may stand for mass() over a row of maximum M at c2 (one test per row)
+__host__ __device__ __forceinline__ bool mass_fast_ok(float M, float c2) { return __builtin_isfinite(M) && __builtin_isfinite(c2); }
 
 __device__ __forceinline__ float temp_scale(float t) { return 1.44269504088896340736f / t; }
 

@@ -20,9 +20,53 @@ using namespace gbs::modeu;
 
 namespace {
 
-constexpr int NT = 256;
-constexpr int TARGET_BLOCKS = 1024;
+#ifndef GBS_SPEC_NT
+#define GBS_SPEC_NT 256
+#endif
+#ifndef GBS_SPEC_BLOCKS
+#define GBS_SPEC_BLOCKS 1024
+#endif
+#ifndef GBS_SPEC_U
+#define GBS_SPEC_U 4
+#endif
+#ifndef GBS_EXP_DRAW_NOCOMPUTE
+#define GBS_EXP_DRAW_NOCOMPUTE 0
+#endif
+#ifndef GBS_EXP_DRAW_NOTAIL
+#define GBS_EXP_DRAW_NOTAIL 0
+#endif
+#ifndef GBS_SPEC_AUX_FWD
+#define GBS_SPEC_AUX_FWD 2  // cache policy of the forward sweeps' loads (2: non-temporal)
+#endif
+#ifndef GBS_SPEC_AUX_REV
+#define GBS_SPEC_AUX_REV 2
+#endif
+#ifndef GBS_EXP_DRAWT
+#define GBS_EXP_DRAWT 0
+#endif
+#if GBS_EXP_DRAWT
+__device__ u64 g_dbg[65536];
+#define DBGT(k) do { if (threadIdx.x == 0) g_dbg[(size_t)seq * 8 + (k)] = wall_clock64(); } while (0)
+#else
+#define DBGT(k) do { } while (0)
+#endif
+#ifndef GBS_SPEC_PIPE
+#define GBS_SPEC_PIPE 1
+#endif
+constexpr int NT = GBS_SPEC_NT;
+constexpr int TARGET_BLOCKS = GBS_SPEC_BLOCKS;
 constexpr int MIN_CHUNK = 2048;
+constexpr int U = GBS_SPEC_U;        // 4-element groups per thread in flight, per row
+constexpr int GSTEP = NT * 4;        // elements between a thread's groups (the draw)
+constexpr int DU = 4;                // the draw: 4-element groups per thread per tile
+constexpr int TILE = NT * 4 * DU;    // the draw: elements per tile
+constexpr int PER = TILE / NT;       // the draw: elements per thread in the scan of one tile
+constexpr int NWD = NT / WAVE;       // the draw: waves per block (one partial sum per wave and tile)
+constexpr int DRAW_BLOCKS = 768;     // the draw: blocks in all (one round on the chip)
+#ifndef GBS_SPEC_ROWS_MIN
+#define GBS_SPEC_ROWS_MIN 192
+#endif
+constexpr int ROWS_KERNEL_MIN = GBS_SPEC_ROWS_MIN;  // rows from which one block per row fills the chip
 
 size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
@@ -31,6 +75,12 @@ int splits_for(int rows, int vocab) {
     const int by_size = (vocab + MIN_CHUNK - 1) / MIN_CHUNK;
     if (s > by_size) s = by_size;
     return s < 1 ? 1 : s;
+}
+
+// chunk of a split: whole 4-element groups, so that 16-byte loads stay inside one split
+int chunk_for(int vocab, int S) {
+    const int c = (vocab + S - 1) / S;
+    return (c + 3) / 4 * 4;
 }
 
 struct RowInfo {
@@ -42,7 +92,10 @@ struct RowInfo {
 
 struct SeqInfo {
     int status, accepted, row, mode;  // mode 0: token fixed; 1: residual draw; 2: bonus draw
-    int token, pad[3];
+    int token, argmax;                // argmax: the draw row's target argmax (the draw of a zero total)
+    float Mp, Mq, c2;                 // the draw row's maxima and 1/T scale
+    int pad;
+    u64 zp, zq;                       // the draw row's mass sums
 };
 
 struct SpecWs {
@@ -54,7 +107,7 @@ struct SpecWs {
     u64* sumparts;           // [R][S][2]
     RowInfo* rows;           // [R]
     SeqInfo* seqs;           // [n_seq]
-    u128* wparts;            // [n_seq][S3]
+    u128* wparts;            // [n_seq][tiles][DU][NWD]: the draw's sub-tile weights
 };
 
 // The counters that must be zero between launches sit at fixed offsets in the first SPEC_CTL_BYTES (room for 65535
@@ -63,7 +116,7 @@ struct SpecWs {
 constexpr size_t SPEC_CTL_BYTES = 3 * (size_t)65536 * 4;
 
 struct Plan {
-    int R, S, S3;
+    int R, S, S3, tpb;
     size_t bytes;
 };
 
@@ -71,10 +124,15 @@ Plan plan(int n_seq, int width, int vocab) {
     Plan p;
     p.R = n_seq * (width + 1);
     p.S = splits_for(p.R, vocab);
-    p.S3 = splits_for(n_seq, vocab);
+    // the draw: tiles per block (tpb), then the blocks per sequence that cover every tile
+    const int tiles = (vocab + TILE - 1) / TILE;
+    int want = (DRAW_BLOCKS + n_seq - 1) / n_seq;
+    want = want < 1 ? 1 : (want > tiles ? tiles : want);
+    p.tpb = (tiles + want - 1) / want;
+    p.S3 = (tiles + p.tpb - 1) / p.tpb;
     p.bytes = SPEC_CTL_BYTES + align256((size_t)p.R * p.S * 16) + align256((size_t)p.R * p.S * 4) + align256((size_t)p.R * p.S * 16) +
               align256((size_t)p.R * sizeof(RowInfo)) + align256((size_t)n_seq * sizeof(SeqInfo)) +
-              align256((size_t)n_seq * p.S3 * 16);
+              align256((size_t)n_seq * tiles * DU * NWD * 16);
     return p;
 }
 
@@ -91,6 +149,67 @@ SpecWs carve(void* ws, int n_seq, const Plan& p) {
     w.seqs = (SeqInfo*)c; c += align256((size_t)n_seq * sizeof(SeqInfo));
     w.wparts = (u128*)c;
     return w;
+}
+
+// Buffer resource over `bytes` bytes at `base`: a load at or past the end returns zeros and touches no memory.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, u32 bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// Streams elements [lo, hi) of a target row (and of the draft row when `two`) through f(t, d, i), each element once,
+// in ascending index order per thread (descending when REV). Elements a thread is handed past `hi` arrive as -inf,
+// which no pass counts. vec: rows are 16-byte aligned and lo is a multiple of 4, so a thread reads 4-element groups
+// by 16-byte non-temporal loads, U groups of each row in flight; otherwise it reads single elements.
+template <bool REV, int NTH = NT, class F>
+__device__ __forceinline__ void stream_rows(const float* tr, const float* dr, bool two, int vocab, int lo, int hi, bool vec, F&& f) {
+    constexpr int GSTEP = NTH * 4, ISTEP = GSTEP * U;
+    const int tid = (int)threadIdx.x;
+    if (!vec) {
+        for (int i = lo + tid; i < hi; i += NTH) f(tr[i], two ? dr[i] : -INFINITY, i);
+        return;
+    }
+    const __amdgpu_buffer_rsrc_t rt = rsrc(tr, (u32)vocab * 4u), rd = rsrc(two ? dr : tr, (u32)vocab * 4u);
+    const int nit = (hi - lo + ISTEP - 1) / ISTEP;
+    auto base_of = [&](int k) { return lo + (REV ? nit - 1 - k : k) * ISTEP + tid * 4; };
+    auto issue = [&](int base, u32x4 (&t)[U], u32x4 (&d)[U]) {
+#pragma unroll
+        for (int j = 0; j < U; ++j) {
+            const u32 off = (u32)(base + j * GSTEP) * 4u;
+            t[j] = __builtin_amdgcn_raw_buffer_load_b128(rt, off, 0, REV ? GBS_SPEC_AUX_REV : GBS_SPEC_AUX_FWD);
+            if (two) d[j] = __builtin_amdgcn_raw_buffer_load_b128(rd, off, 0, REV ? GBS_SPEC_AUX_REV : GBS_SPEC_AUX_FWD);
+        }
+    };
+#if GBS_SPEC_PIPE
+    u32x4 tn[U], dn[U];
+    if (nit > 0) issue(base_of(0), tn, dn);
+#endif
+    for (int k = 0; k < nit; ++k) {
+        const int base = base_of(k);
+        u32x4 t[U], d[U];
+#if GBS_SPEC_PIPE
+#pragma unroll
+        for (int j = 0; j < U; ++j) {
+            t[j] = tn[j];
+            d[j] = dn[j];
+        }
+        if (k + 1 < nit) issue(base_of(k + 1), tn, dn);
+#else
+        issue(base, t, d);
+#endif
+#pragma unroll
+        for (int jj = 0; jj < U; ++jj) {
+            const int j = REV ? U - 1 - jj : jj;
+            const int e = base + j * GSTEP;
+#pragma unroll
+            for (int qq = 0; qq < 4; ++qq) {
+                const int q = REV ? 3 - qq : qq;
+                const bool in = e + q < hi;
+                const float tv = in ? __uint_as_float(t[j][q]) : -INFINITY;
+                const float dv = (two && in) ? __uint_as_float(d[j][q]) : -INFINITY;
+                f(tv, dv, e + q);
+            }
+        }
+    }
 }
 
 __device__ __forceinline__ u64 max_key(float v, int i) { return (v != v || v == -INFINITY) ? 0ull : make_key(okey_f32(v), (u32)i); }
@@ -137,15 +256,44 @@ __device__ __forceinline__ void store_seq(SeqInfo* seqs, int s, const SeqInfo& v
     st_agent(&seqs[s].row, v.row);
     st_agent(&seqs[s].mode, v.mode);
     st_agent(&seqs[s].token, v.token);
+    st_agent(&seqs[s].argmax, v.argmax);
+    st_agent((u32*)&seqs[s].Mp, __float_as_uint(v.Mp));
+    st_agent((u32*)&seqs[s].Mq, __float_as_uint(v.Mq));
+    st_agent((u32*)&seqs[s].c2, __float_as_uint(v.c2));
+    st_agent(&seqs[s].zp, v.zp);
+    st_agent(&seqs[s].zq, v.zq);
+}
+
+// a value every lane of the wave holds, moved to a scalar register (so that buffer resources and branches built from it
+// are uniform)
+__device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ unsigned uni(unsigned v) { return (unsigned)__builtin_amdgcn_readfirstlane((int)v); }
+__device__ __forceinline__ u64 uni(u64 v) { return ((u64)uni((unsigned)(v >> 32)) << 32) | uni((unsigned)v); }
+
+// the row's record, read by every thread of a block and held in scalar registers
+__device__ __forceinline__ RowInfo load_row_uniform(const RowInfo* rows, int r) {
+    RowInfo ri = load_row(rows, r);
+    ri.tkey = uni(ri.tkey);
+    ri.dkey = uni(ri.dkey);
+    ri.zp = uni(ri.zp);
+    ri.zq = uni(ri.zq);
+    ri.nan = uni(ri.nan);
+    return ri;
 }
 
 __device__ __forceinline__ SeqInfo load_seq(const SeqInfo* seqs, int s) {
     SeqInfo v{};
-    v.status = ld_agent(&seqs[s].status);
-    v.accepted = ld_agent(&seqs[s].accepted);
-    v.row = ld_agent(&seqs[s].row);
-    v.mode = ld_agent(&seqs[s].mode);
-    v.token = ld_agent(&seqs[s].token);
+    v.status = uni(ld_agent(&seqs[s].status));
+    v.accepted = uni(ld_agent(&seqs[s].accepted));
+    v.row = uni(ld_agent(&seqs[s].row));
+    v.mode = uni(ld_agent(&seqs[s].mode));
+    v.token = uni(ld_agent(&seqs[s].token));
+    v.argmax = uni(ld_agent(&seqs[s].argmax));
+    v.Mp = __uint_as_float(uni(ld_agent((const u32*)&seqs[s].Mp)));
+    v.Mq = __uint_as_float(uni(ld_agent((const u32*)&seqs[s].Mq)));
+    v.c2 = __uint_as_float(uni(ld_agent((const u32*)&seqs[s].c2)));
+    v.zp = uni(ld_agent(&seqs[s].zp));
+    v.zq = uni(ld_agent(&seqs[s].zq));
     return v;
 }
 
@@ -156,7 +304,7 @@ __device__ __forceinline__ u128 load_u128(const u128* p) {
 
 // ---- launch 1: maxima ----
 __global__ void __launch_bounds__(NT) spec_max_k(const float* __restrict__ target, const float* __restrict__ draft, int width, int vocab,
-                                                 int chunk, SpecWs ws) {
+                                                 int chunk, bool vec, SpecWs ws) {
     __shared__ u64 s_red[NT];
     __shared__ unsigned s_flag;
     const int S = gridDim.x, sp = blockIdx.x, r = blockIdx.y;
@@ -164,20 +312,20 @@ __global__ void __launch_bounds__(NT) spec_max_k(const float* __restrict__ targe
     const float* tr = target + (size_t)r * vocab;
     const float* dr = draft + (size_t)r * vocab;
     const int lo = sp * chunk, hi = min(vocab, lo + chunk);
-    u64 tk = 0, dk = 0;
+    // per thread: the largest value and its first index (elements arrive in ascending index order, and a strict > keeps
+    // the first of equal values, -0 and +0 included); NaN and -inf never replace -inf
+    float tm = -INFINITY, dm = -INFINITY;
+    int ti = 0, di = 0;
     bool nan = false;
-    for (int i = lo + (int)threadIdx.x; i < hi; i += NT) {
-        const float t = tr[i];
-        nan |= t != t;
-        const u64 k = max_key(t, i);
-        tk = k > tk ? k : tk;
-        if (has_draft) {
-            const float d = dr[i];
-            nan |= d != d;
-            const u64 kd = max_key(d, i);
-            dk = kd > dk ? kd : dk;
-        }
-    }
+    stream_rows<false>(tr, dr, has_draft, vocab, lo, hi, vec, [&](float t, float d, int i) {
+        nan |= __builtin_isunordered(t, d);
+        ti = t > tm ? i : ti;
+        tm = t > tm ? t : tm;
+        di = d > dm ? i : di;
+        dm = d > dm ? d : dm;
+    });
+    u64 tk = tm == -INFINITY ? 0ull : make_key(okey_f32(tm), (u32)ti);
+    u64 dk = dm == -INFINITY ? 0ull : make_key(okey_f32(dm), (u32)di);
     tk = block_reduce_max(tk, s_red);
     dk = block_reduce_max(dk, s_red);
     const unsigned bn = block_reduce_max((u64)(nan ? 1 : 0), s_red) != 0ull;
@@ -187,18 +335,21 @@ __global__ void __launch_bounds__(NT) spec_max_k(const float* __restrict__ targe
         st_agent(&ws.nanparts[(size_t)r * S + sp], bn);
     }
     if (!arrive_last(&ws.row_counters[r], (unsigned)S, &s_flag)) return;
+    // the row's partials, loaded in parallel (one per thread) and reduced
+    u64 a = 0, b = 0, n = 0;
+    for (int o = (int)threadIdx.x; o < S; o += NT) {
+        const u64 x = ld_agent(&ws.maxparts[((size_t)r * S + o) * 2]), y = ld_agent(&ws.maxparts[((size_t)r * S + o) * 2 + 1]);
+        a = x > a ? x : a;
+        b = y > b ? y : b;
+        n |= ld_agent(&ws.nanparts[(size_t)r * S + o]);
+    }
+    a = block_reduce_max(a, s_red);
+    b = block_reduce_max(b, s_red);
+    n = block_reduce_max(n, s_red);
     if (threadIdx.x == 0) {
-        u64 a = 0, b = 0;
-        unsigned n = 0;
-        for (int o = 0; o < S; ++o) {
-            const u64 x = ld_agent(&ws.maxparts[((size_t)r * S + o) * 2]), y = ld_agent(&ws.maxparts[((size_t)r * S + o) * 2 + 1]);
-            a = x > a ? x : a;
-            b = y > b ? y : b;
-            n |= ld_agent(&ws.nanparts[(size_t)r * S + o]);
-        }
         st_agent(&ws.rows[r].tkey, a);
         st_agent(&ws.rows[r].dkey, b);
-        st_agent(&ws.rows[r].nan, n);
+        st_agent(&ws.rows[r].nan, (unsigned)n);
     }
 }
 
@@ -209,9 +360,82 @@ __device__ __forceinline__ bool accept_test(float u, u128 a, u128 b) { return mu
 
 __device__ __forceinline__ float key_value(u64 k) { return okey_to_f32(key_ok(k)); }
 
+// The sequence's decisions, by the block that completes the sequence's last row (all its rows' records are written).
+__device__ void decide_sequence(int seq, int width, int vocab, const float* __restrict__ target, const float* __restrict__ draft,
+                                const int* __restrict__ draft_ids, const float* __restrict__ temps, const float* __restrict__ u_accept,
+                                const float* __restrict__ u_resample, SpecWs ws) {
+    const int W1 = width + 1;
+    // Each thread checks rows j = tid, tid + blockDim.x, ... <= width (their parameters, flags and, for
+    // a draft row, the acceptance test), all rows at once: the status flags are or-ed and the first rejection is the
+    // minimum rejecting j.
+    __shared__ int s_all, s_first;
+    if (threadIdx.x == 0) {
+        s_all = 0;
+        s_first = width;
+    }
+    __syncthreads();
+    const int r0 = seq * W1;
+    for (int j = (int)threadIdx.x; j <= width; j += (int)blockDim.x) {
+        const RowInfo ri = load_row(ws.rows, r0 + j);
+        const float Tj = temps[r0 + j];
+        bool bad = !temp_ok(Tj);
+        if (j == 0) bad |= !(u_resample[seq] >= 0.0f && u_resample[seq] < 1.0f);
+        bool acc = false;
+        if (j < width) {
+            const float u = u_accept[(size_t)seq * width + j];
+            const int x = draft_ids[(size_t)seq * width + j];
+            bad |= !(u >= 0.0f && u < 1.0f) || x < 0 || x >= vocab;
+            if (!bad && !ri.nan && ri.tkey != 0ull && ri.dkey != 0ull) {
+                if (Tj == 0.0f) acc = x == (int)key_id(ri.tkey);
+                else {
+                    const float cj = temp_scale(Tj);
+                    const float tx = target[(size_t)(r0 + j) * vocab + x], dx = draft[(size_t)(r0 + j) * vocab + x];
+                    const u64 ep = tx > -INFINITY ? mass(tx, key_value(ri.tkey), cj) : 0ull;
+                    const u64 eq = dx > -INFINITY ? mass(dx, key_value(ri.dkey), cj) : 0ull;
+                    acc = accept_test(u, (u128)eq * ri.zp, (u128)ep * ri.zq);
+                }
+            }
+            if (!acc) atomicMin(&s_first, j);
+        }
+        int f = bad ? 1 : 0;
+        f |= ri.nan != 0u ? 2 : 0;
+        f |= (ri.tkey == 0ull || (j < width && ri.dkey == 0ull)) ? 4 : 0;
+        if (f) atomicOr(&s_all, f);
+    }
+    __syncthreads();
+    if (threadIdx.x != 0) return;
+    SeqInfo si{};
+    si.status = GBS_ROW_OK;
+    const int all = s_all;
+    if (all & 1) si.status = GBS_ROW_INVALID_PARAMS;
+    else if (all & 2) si.status = GBS_ROW_NAN_LOGIT;
+    else if (all & 4) si.status = GBS_ROW_NO_CANDIDATES;
+    if (si.status == GBS_ROW_OK) {
+        const int k = s_first;
+        si.accepted = k;
+        si.row = r0 + k;
+        const float Tk = temps[r0 + k];
+        const RowInfo ri = load_row(ws.rows, r0 + k);
+        si.argmax = (int)key_id(ri.tkey);
+        if (Tk == 0.0f) {
+            si.mode = 0;
+            si.token = si.argmax;
+        } else {
+            si.mode = k < width ? 1 : 2;
+            si.token = -1;
+            si.Mp = key_value(ri.tkey);
+            si.Mq = key_value(ri.dkey);
+            si.c2 = temp_scale(Tk);
+            si.zp = ri.zp;
+            si.zq = ri.zq;
+        }
+    }
+    store_seq(ws.seqs, seq, si);
+}
+
 // ---- launch 2: mass sums, then the sequence's acceptances ----
 __global__ void __launch_bounds__(NT) spec_mass_k(const float* __restrict__ target, const float* __restrict__ draft, int width, int vocab,
-                                                  int chunk, const int* __restrict__ draft_ids, const float* __restrict__ temps,
+                                                  int chunk, bool vec, const int* __restrict__ draft_ids, const float* __restrict__ temps,
                                                   const float* __restrict__ u_accept, const float* __restrict__ u_resample, SpecWs ws) {
     __shared__ u64 s_red[NT];
     __shared__ unsigned s_flag;
@@ -221,7 +445,7 @@ __global__ void __launch_bounds__(NT) spec_mass_k(const float* __restrict__ targ
     const bool has_draft = (r % W1) < width;
     const float T = temps[r];
     const bool draw = temp_ok(T) && T > 0.0f;
-    const RowInfo info = load_row(ws.rows, r);
+    const RowInfo info = load_row_uniform(ws.rows, r);
     const float Mp = key_value(info.tkey), Mq = key_value(info.dkey);
     const float c2 = draw ? temp_scale(T) : 0.0f;
     const float* tr = target + (size_t)r * vocab;
@@ -229,14 +453,19 @@ __global__ void __launch_bounds__(NT) spec_mass_k(const float* __restrict__ targ
     const int lo = sp * chunk, hi = min(vocab, lo + chunk);
     u64 zp = 0, zq = 0;
     if (draw && info.tkey != 0ull && !info.nan) {
-        for (int i = lo + (int)threadIdx.x; i < hi; i += NT) {
-            const float t = tr[i];
-            if (t > -INFINITY) zp += mass(t, Mp, c2);
-            if (has_draft && info.dkey != 0ull) {
-                const float d = dr[i];
-                if (d > -INFINITY) zq += mass(d, Mq, c2);
-            }
-        }
+        // the reverse of the maxima pass's order: the bytes that pass read last are the likeliest still in cache
+        const bool two = has_draft && info.dkey != 0ull;
+        const float Mq2 = two ? Mq : Mp;  // a missing draft row streams -inf, of mass 0 under either maximum
+        if (mass_fast_ok(Mp, c2) && mass_fast_ok(Mq2, c2))
+            stream_rows<true>(tr, dr, two, vocab, lo, hi, vec, [&](float t, float d, int) {
+                zp += mass_fast(t, Mp, c2);
+                zq += mass_fast(d, Mq2, c2);
+            });
+        else
+            stream_rows<true>(tr, dr, two, vocab, lo, hi, vec, [&](float t, float d, int) {
+                zp += t > -INFINITY ? mass(t, Mp, c2) : 0ull;
+                zq += d > -INFINITY ? mass(d, Mq2, c2) : 0ull;
+            });
     }
     zp = block_reduce_sum(zp, s_red);
     zq = block_reduce_sum(zq, s_red);
@@ -245,171 +474,343 @@ __global__ void __launch_bounds__(NT) spec_mass_k(const float* __restrict__ targ
         st_agent(&ws.sumparts[((size_t)r * S + sp) * 2 + 1], zq);
     }
     if (!arrive_last(&ws.row_counters[r], (unsigned)S, &s_flag)) return;
-    if (threadIdx.x == 0) {
+    {
+        // the row's partial sums, loaded in parallel (one per thread) and reduced
         u64 a = 0, b = 0;
-        for (int o = 0; o < S; ++o) {
+        for (int o = (int)threadIdx.x; o < S; o += NT) {
             a += ld_agent(&ws.sumparts[((size_t)r * S + o) * 2]);
             b += ld_agent(&ws.sumparts[((size_t)r * S + o) * 2 + 1]);
         }
-        st_agent(&ws.rows[r].zp, a);
-        st_agent(&ws.rows[r].zq, b);
+        a = block_reduce_sum(a, s_red);
+        b = block_reduce_sum(b, s_red);
+        if (threadIdx.x == 0) {
+            st_agent(&ws.rows[r].zp, a);
+            st_agent(&ws.rows[r].zq, b);
+        }
     }
     if (!arrive_last(&ws.seq_counters[seq], (unsigned)W1, &s_flag)) return;
-    if (threadIdx.x != 0) return;
-    // the sequence's decisions (one thread; width is small)
-    SeqInfo si{};
-    si.status = GBS_ROW_OK;
-    const int r0 = seq * W1;
-    bool bad = !(u_resample[seq] >= 0.0f && u_resample[seq] < 1.0f);
-    for (int j = 0; j <= width; ++j) bad |= !temp_ok(temps[r0 + j]);
-    for (int j = 0; j < width; ++j) {
-        const float u = u_accept[(size_t)seq * width + j];
-        const int x = draft_ids[(size_t)seq * width + j];
-        bad |= !(u >= 0.0f && u < 1.0f) || x < 0 || x >= vocab;
-    }
-    bool nan = false, empty = false;
-    for (int j = 0; j <= width; ++j) {
-        const RowInfo ri = load_row(ws.rows, r0 + j);
-        nan |= ri.nan != 0u;
-        empty |= ri.tkey == 0ull || (j < width && ri.dkey == 0ull);
-    }
-    if (bad) si.status = GBS_ROW_INVALID_PARAMS;
-    else if (nan) si.status = GBS_ROW_NAN_LOGIT;
-    else if (empty) si.status = GBS_ROW_NO_CANDIDATES;
-    if (si.status == GBS_ROW_OK) {
-        int j = 0;
-        for (; j < width; ++j) {
-            const RowInfo ri = load_row(ws.rows, r0 + j);
-            const float Tj = temps[r0 + j];
-            const int x = draft_ids[(size_t)seq * width + j];
-            bool acc;
-            if (Tj == 0.0f) acc = x == (int)key_id(ri.tkey);
-            else {
-                const float cj = temp_scale(Tj);
-                const float tx = target[(size_t)(r0 + j) * vocab + x], dx = draft[(size_t)(r0 + j) * vocab + x];
-                const u64 ep = tx > -INFINITY ? mass(tx, key_value(ri.tkey), cj) : 0ull;
-                const u64 eq = dx > -INFINITY ? mass(dx, key_value(ri.dkey), cj) : 0ull;
-                acc = accept_test(u_accept[(size_t)seq * width + j], (u128)eq * ri.zp, (u128)ep * ri.zq);
-            }
-            if (!acc) break;
-        }
-        si.accepted = j;
-        si.row = r0 + j;
-        const float Tj = temps[r0 + j];
-        if (Tj == 0.0f) {
-            si.mode = 0;
-            si.token = (int)key_id(ld_agent(&ws.rows[r0 + j].tkey));
-        } else {
-            si.mode = j < width ? 1 : 2;
-            si.token = -1;
-        }
-    }
-    store_seq(ws.seqs, seq, si);
+    decide_sequence(seq, width, vocab, target, draft, draft_ids, temps, u_accept, u_resample, ws);
 }
 
-// residual (mode 1) or bonus (mode 2) weight of element i of the sequence's draw row
-__device__ __forceinline__ u128 draw_weight(int mode, const float* tr, const float* dr, int i, float Mp, float Mq, float c2, u64 zp, u64 zq) {
-    const float t = tr[i];
-    const u64 ep = t > -INFINITY ? mass(t, Mp, c2) : 0ull;
+// the mass of a token of logit l in a row of maximum M; FAST: mass_fast's preconditions hold for the row
+template <bool FAST>
+__device__ __forceinline__ u64 row_mass(float l, float M, float c2) {
+    if (FAST) return mass_fast(l, M, c2);
+    return l > -INFINITY ? mass(l, M, c2) : 0ull;
+}
+
+// residual (mode 1) or bonus (mode 2) weight of a token of target logit t and draft logit d
+template <bool FAST = false>
+__device__ __forceinline__ u128 pair_weight(int mode, float t, float d, float Mp, float Mq, float c2, u64 zp, u64 zq) {
+    const u64 ep = row_mass<FAST>(t, Mp, c2);
     if (mode == 2) return (u128)ep;
-    const float d = dr[i];
-    const u64 eq = d > -INFINITY ? mass(d, Mq, c2) : 0ull;
+    const u64 eq = row_mass<FAST>(d, Mq, c2);
     const u128 a = (u128)ep * zq, b = (u128)eq * zp;
     return a > b ? a - b : (u128)0;
 }
 
+// the same, of element i of the sequence's draw row
+__device__ __forceinline__ u128 draw_weight(int mode, const float* tr, const float* dr, int i, float Mp, float Mq, float c2, u64 zp, u64 zq) {
+    return pair_weight(mode, tr[i], mode == 2 ? -INFINITY : dr[i], Mp, Mq, c2, zp, zq);
+}
+
+// sum of a u128 over the wave, in lane 0 (other lanes: partial sums)
+__device__ __forceinline__ u128 wave_sum_u128(u128 v) {
+    u64 lo = (u64)v, hi = (u64)(v >> 64);
+#pragma unroll
+    for (int m = 1; m < WAVE; m <<= 1) {
+        const u64 olo = shfl_xor64(lo, m), ohi = shfl_xor64(hi, m);
+        const u64 s = lo + olo;
+        hi = hi + ohi + (s < lo ? 1ull : 0ull);
+        lo = s;
+    }
+    return ((u128)hi << 64) | lo;
+}
+
+// ---- launches 1 + 2 in one, for many rows: one block per row ----
+// The block reads its target and draft row twice: forward for the maxima and NaN flag, then backward for the integer
+// mass sums (the bytes read last in the forward sweep are the likeliest to be served by the cache). It writes the row's
+// record itself (no hand-off of partials); the block that completes a sequence's last row decides the sequence.
+#ifndef GBS_SPEC_RNT
+#define GBS_SPEC_RNT 1024
+#endif
+constexpr int RNT = GBS_SPEC_RNT;  // threads of the one-block-per-row kernel
+
+template <int NTH>
+__device__ __forceinline__ u64 block_max_u64(u64 v, u64* s) {
+    const int w = (int)threadIdx.x / WAVE, l = lane_id();
+    v = wave_max_u64(v);
+    if (l == 0) s[w] = v;
+    __syncthreads();
+    u64 r = 0;
+#pragma unroll
+    for (int k = 0; k < NTH / WAVE; ++k) r = s[k] > r ? s[k] : r;
+    __syncthreads();
+    return r;
+}
+
+template <int NTH>
+__device__ __forceinline__ u64 block_sum_u64(u64 v, u64* s) {
+    const int w = (int)threadIdx.x / WAVE, l = lane_id();
+    v = wave_sum_u64(v);
+    if (l == 0) s[w] = v;
+    __syncthreads();
+    u64 r = 0;
+#pragma unroll
+    for (int k = 0; k < NTH / WAVE; ++k) r += s[k];
+    __syncthreads();
+    return r;
+}
+
+__global__ void __launch_bounds__(RNT) spec_rows_k(const float* __restrict__ target, const float* __restrict__ draft, int width, int vocab,
+                                                   bool vec, const int* __restrict__ draft_ids, const float* __restrict__ temps,
+                                                   const float* __restrict__ u_accept, const float* __restrict__ u_resample, SpecWs ws) {
+    __shared__ u64 s_red[RNT / WAVE];
+    __shared__ unsigned s_flag;
+    const int r = blockIdx.x;
+    const int W1 = width + 1;
+    const int seq = r / W1;
+    const bool has_draft = (r % W1) < width;
+    const float* tr = target + (size_t)r * vocab;
+    const float* dr = draft + (size_t)r * vocab;
+    // forward: per thread the largest value and its first index (elements arrive in ascending index order per thread,
+    // and a strict > keeps the first of equal values, -0 and +0 included); NaN and -inf never replace -inf
+    float tm = -INFINITY, dm = -INFINITY;
+    int ti = 0, di = 0;
+    bool nanf = false;
+    stream_rows<false, RNT>(tr, dr, has_draft, vocab, 0, vocab, vec, [&](float t, float d, int i) {
+        nanf |= __builtin_isunordered(t, d);
+        ti = t > tm ? i : ti;
+        tm = t > tm ? t : tm;
+        di = d > dm ? i : di;
+        dm = d > dm ? d : dm;
+    });
+    const u64 tkey = block_max_u64<RNT>(tm == -INFINITY ? 0ull : make_key(okey_f32(tm), (u32)ti), s_red);
+    const u64 dkey = block_max_u64<RNT>(dm == -INFINITY ? 0ull : make_key(okey_f32(dm), (u32)di), s_red);
+    const bool nan = block_max_u64<RNT>(nanf ? 1ull : 0ull, s_red) != 0ull;
+    // backward: the mass sums at the row's temperature (none at T = 0, for an invalid T, a NaN or an empty row)
+    const float T = temps[r];
+    const bool draw = temp_ok(T) && T > 0.0f;
+    u64 zp = 0, zq = 0;
+    if (draw && tkey != 0ull && !nan) {
+        const float c2 = temp_scale(T);
+        const float Mp = key_value(tkey);
+        const bool two = has_draft && dkey != 0ull;
+        const float Mq = two ? key_value(dkey) : Mp;  // a missing draft row streams -inf, of mass 0 under either maximum
+        if (mass_fast_ok(Mp, c2) && mass_fast_ok(Mq, c2))
+            stream_rows<true, RNT>(tr, dr, two, vocab, 0, vocab, vec, [&](float t, float d, int) {
+                zp += mass_fast(t, Mp, c2);
+                zq += mass_fast(d, Mq, c2);
+            });
+        else
+            stream_rows<true, RNT>(tr, dr, two, vocab, 0, vocab, vec, [&](float t, float d, int) {
+                zp += t > -INFINITY ? mass(t, Mp, c2) : 0ull;
+                zq += d > -INFINITY ? mass(d, Mq, c2) : 0ull;
+            });
+        zp = block_sum_u64<RNT>(zp, s_red);
+        zq = block_sum_u64<RNT>(zq, s_red);
+    }
+    if (threadIdx.x == 0) {
+        st_agent(&ws.rows[r].tkey, tkey);
+        st_agent(&ws.rows[r].dkey, dkey);
+        st_agent(&ws.rows[r].zp, zp);
+        st_agent(&ws.rows[r].zq, zq);
+        st_agent(&ws.rows[r].nan, nan ? 1u : 0u);
+    }
+    if (!arrive_last(&ws.seq_counters[seq], (unsigned)W1, &s_flag)) return;
+    decide_sequence(seq, width, vocab, target, draft, draft_ids, temps, u_accept, u_resample, ws);
+}
+
+// inclusive prefix sum of a u128 over the wave
+__device__ __forceinline__ u128 wave_scan_u128(u128 v) {
+    const int l = lane_id();
+    u64 lo = (u64)v, hi = (u64)(v >> 64);
+#pragma unroll
+    for (int m = 1; m < WAVE; m <<= 1) {
+        const int src = l >= m ? l - m : l;
+        const u64 olo = shfl64(lo, src), ohi = shfl64(hi, src);
+        if (l >= m) {
+            const u64 s = lo + olo;
+            hi = hi + ohi + (s < lo ? 1ull : 0ull);
+            lo = s;
+        }
+    }
+    return ((u128)hi << 64) | lo;
+}
+
+// exclusive prefix sum of a u128 over the block (thread order) and the block's total; all threads call it.
+// s_wt: NT / WAVE entries of LDS, free on entry; free again on return.
+__device__ __forceinline__ u128 block_scan_u128(u128 v, u128& total, u128* s_wt) {
+    const int w = (int)threadIdx.x / WAVE, l = lane_id();
+    const u128 inc = wave_scan_u128(v);
+    if (l == WAVE - 1) s_wt[w] = inc;
+    __syncthreads();
+    u128 off = 0, tot = 0;
+#pragma unroll
+    for (int k = 0; k < NT / WAVE; ++k) {
+        const u128 x = s_wt[k];
+        off += k < w ? x : (u128)0;
+        tot += x;
+    }
+    __syncthreads();
+    total = tot;
+    return off + inc - v;
+}
+
 // ---- launch 3: the draw ----
+// Grid (blocks per sequence, n_seq). The row that a sequence draws from (its first rejected row: the residual; or its
+// last row: the bonus from p) is cut into tiles of TILE elements; block b takes tiles [b * tpb, (b + 1) * tpb), the
+// next tile's loads in flight while one is summed. A wave covers 256 contiguous elements of a tile per 4-element group
+// index j, so the wave sums of (tile, j, wave) are the weights of consecutive 256-element sub-tiles: sub-tile
+// p = (tile * DU + j) * NWD + wave holds elements [256 p, 256 p + 256). The sequence's last block finds the sub-tile
+// that holds t = floor(u * total) by a block scan over them, then the element by a block scan over the sub-tile (one
+// element per thread).
+template <int MODE, bool FAST>
+__device__ __forceinline__ void draw_tiles(const float* tr, const float* dr, int vocab, int t0, int t1, bool vec, float Mp, float Mq,
+                                           float c2, u64 zp, u64 zq, u128* wparts) {
+    const int tid = (int)threadIdx.x, w = tid / WAVE, l = lane_id();
+    const __amdgpu_buffer_rsrc_t rt = rsrc(tr, (u32)vocab * 4u), rd = rsrc(MODE == 1 ? dr : tr, (u32)vocab * 4u);
+    auto issue = [&](int tile, float (&t)[DU * 4], float (&d)[DU * 4]) {
+#pragma unroll
+        for (int j = 0; j < DU; ++j) {
+            const int e = tile * TILE + j * GSTEP + tid * 4;
+            if (vec) {
+                const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(rt, (u32)e * 4u, 0, 2);
+                u32x4 b = {0u, 0u, 0u, 0u};
+                if (MODE == 1) b = __builtin_amdgcn_raw_buffer_load_b128(rd, (u32)e * 4u, 0, 2);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    t[j * 4 + q] = __uint_as_float(a[q]);
+                    d[j * 4 + q] = __uint_as_float(b[q]);
+                }
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    t[j * 4 + q] = e + q < vocab ? tr[e + q] : -INFINITY;
+                    d[j * 4 + q] = (MODE == 1 && e + q < vocab) ? dr[e + q] : -INFINITY;
+                }
+            }
+        }
+    };
+    float tn[DU * 4], dn[DU * 4];
+    if (t0 < t1) issue(t0, tn, dn);
+    for (int tile = t0; tile < t1; ++tile) {
+        float t[DU * 4], d[DU * 4];
+#pragma unroll
+        for (int i = 0; i < DU * 4; ++i) {
+            t[i] = tn[i];
+            d[i] = dn[i];
+        }
+        if (tile + 1 < t1) issue(tile + 1, tn, dn);
+#pragma unroll
+        for (int j = 0; j < DU; ++j) {
+            const int e = tile * TILE + j * GSTEP + tid * 4;
+            u128 part = 0;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const bool in = e + q < vocab;  // buffer loads past the row's end return 0, not -inf
+#if GBS_EXP_DRAW_NOCOMPUTE
+                part += (u128)__float_as_uint(t[j * 4 + q]) + __float_as_uint(d[j * 4 + q]) + (in ? 1u : 0u);
+#else
+                part += pair_weight<FAST>(MODE, in ? t[j * 4 + q] : -INFINITY, in ? d[j * 4 + q] : -INFINITY, Mp, Mq, c2, zp, zq);
+#endif
+            }
+            part = wave_sum_u128(part);
+            if (l == 0) {
+                u64* o = (u64*)&wparts[((size_t)tile * DU + j) * NWD + w];
+                st_agent(o, (u64)part);
+                st_agent(o + 1, (u64)(part >> 64));
+            }
+        }
+    }
+}
+
 __global__ void __launch_bounds__(NT) spec_draw_k(const float* __restrict__ target, const float* __restrict__ draft, int width, int vocab,
-                                                  int chunk, const int* __restrict__ draft_ids, const float* __restrict__ temps,
-                                                  const float* __restrict__ u_resample, SpecWs ws, int* __restrict__ out_accepted,
-                                                  int* __restrict__ out_tokens, int* __restrict__ out_status) {
-    __shared__ u128 s_red[NT];
+                                                  int tpb, bool vec, const int* __restrict__ draft_ids, const float* __restrict__ u_resample,
+                                                  SpecWs ws, int* __restrict__ out_accepted, int* __restrict__ out_tokens,
+                                                  int* __restrict__ out_status) {
+    static_assert(NT == WAVE * 4, "a sub-tile (256 elements) is one element per thread");
+    __shared__ u128 s_rem;
+    __shared__ u128 s_wt[NT / WAVE];
     __shared__ unsigned s_flag;
     __shared__ int s_tok;
     const int S = gridDim.x, sp = blockIdx.x, seq = blockIdx.y;
+    const int tiles = (vocab + TILE - 1) / TILE;
+    const int nsub = tiles * DU * NWD;
+    const u64 t_begin = wall_clock64();
     const SeqInfo si = load_seq(ws.seqs, seq);
     const bool drawing = si.status == GBS_ROW_OK && si.mode != 0;
-    const int lo = sp * chunk, hi = min(vocab, lo + chunk);
-    float Mp = 0.f, Mq = 0.f, c2 = 0.f;
-    u64 zp = 0, zq = 0;
-    const float* tr = target;
-    const float* dr = draft;
+    const float* tr = target + (size_t)si.row * vocab;
+    const float* dr = draft + (size_t)si.row * vocab;
+    u128* wp = ws.wparts + (size_t)seq * nsub;
+    const bool fast = mass_fast_ok(si.Mp, si.c2) && (si.mode == 2 || mass_fast_ok(si.Mq, si.c2));
     if (drawing) {
-        const RowInfo ri = load_row(ws.rows, si.row);
-        Mp = key_value(ri.tkey);
-        Mq = key_value(ri.dkey);
-        zp = ri.zp;
-        zq = ri.zq;
-        c2 = temp_scale(temps[si.row]);
-        tr = target + (size_t)si.row * vocab;
-        dr = draft + (size_t)si.row * vocab;
+        const int t0 = sp * tpb, t1 = min(tiles, t0 + tpb);
+        if (si.mode == 1 && fast) draw_tiles<1, true>(tr, dr, vocab, t0, t1, vec, si.Mp, si.Mq, si.c2, si.zp, si.zq, wp);
+        else if (si.mode == 1) draw_tiles<1, false>(tr, dr, vocab, t0, t1, vec, si.Mp, si.Mq, si.c2, si.zp, si.zq, wp);
+        else if (fast) draw_tiles<2, true>(tr, dr, vocab, t0, t1, vec, si.Mp, si.Mq, si.c2, si.zp, si.zq, wp);
+        else draw_tiles<2, false>(tr, dr, vocab, t0, t1, vec, si.Mp, si.Mq, si.c2, si.zp, si.zq, wp);
     }
-    u128 part = 0;
-    if (drawing)
-        for (int i = lo + (int)threadIdx.x; i < hi; i += NT) part += draw_weight(si.mode, tr, dr, i, Mp, Mq, c2, zp, zq);
-    part = block_reduce_sum(part, s_red);
-    if (threadIdx.x == 0) {
-        st_agent((u64*)&ws.wparts[(size_t)seq * S + sp], (u64)part);
-        st_agent((u64*)&ws.wparts[(size_t)seq * S + sp] + 1, (u64)(part >> 64));
-    }
+    const u64 t_streamed = wall_clock64();
     if (!arrive_last(&ws.draw_counters[seq], (unsigned)S, &s_flag)) return;
+#if GBS_EXP_DRAWT
+    if (threadIdx.x == 0) { g_dbg[(size_t)seq * 8 + 0] = t_begin; g_dbg[(size_t)seq * 8 + 1] = t_streamed; }
+#else
+    (void)t_begin;
+    (void)t_streamed;
+#endif
+    DBGT(2);
     int token = si.token;
-    if (drawing) {
-        if (threadIdx.x == 0) {
-            u128 total = 0;
-            for (int o = 0; o < S; ++o) total += load_u128(&ws.wparts[(size_t)seq * S + o]);
-            const u128 t = mul_floor(u_resample[seq], total, nullptr);
-            u128 before = 0;
-            int c = 0;
-            for (; c < S; ++c) {
-                const u128 w = load_u128(&ws.wparts[(size_t)seq * S + c]);
-                if (before + w > t) break;
-                before += w;
-            }
-            s_red[0] = t - before;  // target within chunk c
-            s_flag = (unsigned)c;
+    if (drawing && !GBS_EXP_DRAW_NOTAIL) {
+        const int tid = (int)threadIdx.x;
+        if (tid == 0) {
+            s_flag = (unsigned)nsub;  // a zero total selects no sub-tile
+            s_tok = si.argmax;        // and draws the target's argmax
         }
-        __syncthreads();
-        const u128 tc = s_red[0];
-        const int c = (int)s_flag;
-        __syncthreads();
-        // chunk c, split into NT contiguous ranges; thread sums, then the owning range is scanned
-        const int clo = c * chunk, chi = min(vocab, clo + chunk);
-        const int per = (chi - clo + NT - 1) / NT;
-        const int a = clo + (int)threadIdx.x * per, b = min(chi, a + per);
-        u128 mine = 0;
-        for (int i = a; i < b; ++i) mine += draw_weight(si.mode, tr, dr, i, Mp, Mq, c2, zp, zq);
-        s_red[threadIdx.x] = mine;
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            u128 before = 0;
-            int owner = NT - 1;
-            for (int k = 0; k < NT; ++k) {
-                if (before + s_red[k] > tc) {
-                    owner = k;
-                    break;
-                }
-                before += s_red[k];
-            }
-            s_red[NT - 1] = tc - before;  // reuse: the owner's remaining target (its own slot is read below first)
-            s_flag = (unsigned)owner;
+        // thread k sums the sub-tiles [k * SPT, (k + 1) * SPT) (loaded in parallel); a block scan; t
+        constexpr int SPT = (128 * DU * NWD + NT - 1) / NT;  // sub-tiles per thread at the largest vocabulary
+        u128 sub[SPT];
+        u128 v = 0;
+#pragma unroll
+        for (int k = 0; k < SPT; ++k) {
+            const int p = tid * SPT + k;
+            sub[k] = p < nsub ? load_u128(&wp[p]) : (u128)0;
+            v += sub[k];
         }
-        __syncthreads();
-        const int owner = (int)s_flag;
-        const u128 to = s_red[NT - 1];
-        if ((int)threadIdx.x == owner) {
-            u128 acc = 0;
-            int tok = b > a ? b - 1 : a;
-            for (int i = a; i < b; ++i) {
-                acc += draw_weight(si.mode, tr, dr, i, Mp, Mq, c2, zp, zq);
-                if (acc > to) {
-                    tok = i;
-                    break;
+        u128 total;
+        const u128 ex = block_scan_u128(v, total, s_wt);
+        const u128 t = mul_floor(u_resample[seq], total, nullptr);
+        if (v != 0 && ex <= t && t - ex < v) {  // this thread's sub-tiles hold t: find which
+            u128 before = ex;
+            int kk = -1;
+#pragma unroll
+            for (int k = 0; k < SPT; ++k) {
+                if (kk < 0) {
+                    if (t - before < sub[k]) kk = k;
+                    else before += sub[k];
                 }
             }
-            s_tok = tok;
+            s_flag = (unsigned)(tid * SPT + kk);
+            s_rem = t - before;
         }
         __syncthreads();
+        DBGT(3);
+        const int p = (int)s_flag;
+        const u128 rem = s_rem;
+        // sub-tile p: one element per thread, coalesced; a block scan; the element whose range holds rem
+        const int e = p * NT + tid;
+        const bool in = p < nsub && e < vocab;
+        const float te = in ? tr[e] : -INFINITY;
+        const float de = (in && si.mode == 1) ? dr[e] : -INFINITY;
+        const u128 we = fast ? pair_weight<true>(si.mode, te, de, si.Mp, si.Mq, si.c2, si.zp, si.zq)
+                             : pair_weight(si.mode, te, de, si.Mp, si.Mq, si.c2, si.zp, si.zq);
+        DBGT(4);
+        u128 sub_total;
+        const u128 before = block_scan_u128(we, sub_total, s_wt);
+        DBGT(5);
+        if (p < nsub && we != 0 && before <= rem && rem - before < we) s_tok = e;
+        __syncthreads();
+        DBGT(6);
         token = s_tok;
     }
     if (threadIdx.x == 0) {
@@ -425,9 +826,14 @@ __global__ void __launch_bounds__(NT) spec_draw_k(const float* __restrict__ targ
             out_tokens[(size_t)seq * W1 + j] = v;
         }
     }
+    DBGT(7);
 }
 
 }  // namespace
+
+#if GBS_EXP_DRAWT
+GBS_EXPORT int gbs_debug_times(void* host) { return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_dbg), sizeof(g_dbg)); }
+#endif
 
 GBS_EXPORT size_t gbs_spec_verify_workspace_bytes(int n_seq, int width, int vocab) {
     if (n_seq <= 0 || width < 0 || vocab <= 0 || vocab > GBS_MAX_VOCAB) return 0;
@@ -445,17 +851,25 @@ GBS_EXPORT int gbs_spec_verify(const float* target, const float* draft, int n_se
     if (p.R > 65535 || ws_bytes < p.bytes) return GBS_ERR_INVALID;
     const SpecWs w = carve(ws, n_seq, p);
     const hipStream_t st = to_stream(stream);
-    const int chunk = (vocab + p.S - 1) / p.S;
-    const int chunk3 = (vocab + p.S3 - 1) / p.S3;
+    const int chunk = chunk_for(vocab, p.S);
     const float* dr = width > 0 ? draft : target;
-    hipLaunchKernelGGL(spec_max_k, dim3(p.S, p.R), dim3(NT), 0, st, target, dr, width, vocab, chunk, w);
-    int rc = launch_status();
-    if (rc) return rc;
-    hipLaunchKernelGGL(spec_mass_k, dim3(p.S, p.R), dim3(NT), 0, st, target, dr, width, vocab, chunk, draft_ids, temperatures, u_accept,
-                       u_resample, w);
-    rc = launch_status();
-    if (rc) return rc;
-    hipLaunchKernelGGL(spec_draw_k, dim3(p.S3, n_seq), dim3(NT), 0, st, target, dr, width, vocab, chunk3, draft_ids, temperatures,
-                       u_resample, w, out_accepted, out_tokens, out_status);
+    const bool vec = vocab % 4 == 0 && aligned(target, 16) && aligned(dr, 16);
+    int rc;
+    if (p.R >= ROWS_KERNEL_MIN) {
+        hipLaunchKernelGGL(spec_rows_k, dim3(p.R), dim3(RNT), 0, st, target, dr, width, vocab, vec, draft_ids, temperatures, u_accept,
+                           u_resample, w);
+        rc = launch_status();
+        if (rc) return rc;
+    } else {
+        hipLaunchKernelGGL(spec_max_k, dim3(p.S, p.R), dim3(NT), 0, st, target, dr, width, vocab, chunk, vec, w);
+        rc = launch_status();
+        if (rc) return rc;
+        hipLaunchKernelGGL(spec_mass_k, dim3(p.S, p.R), dim3(NT), 0, st, target, dr, width, vocab, chunk, vec, draft_ids, temperatures,
+                           u_accept, u_resample, w);
+        rc = launch_status();
+        if (rc) return rc;
+    }
+    hipLaunchKernelGGL(spec_draw_k, dim3(p.S3, n_seq), dim3(NT), 0, st, target, dr, width, vocab, p.tpb, vec, draft_ids, u_resample, w,
+                       out_accepted, out_tokens, out_status);
     return launch_status();
 }

@@ -35,16 +35,17 @@ def test_config5_full_vocab():
     assert np.array_equal(s, ws) and np.array_equal(a, wa) and np.array_equal(t, wt)
 
 
-def test_spec_greedy_and_errors():
+@pytest.mark.parametrize("n_seq", [6, 60])  # 24 rows: split kernels; 240 rows: one block per row
+def test_spec_greedy_and_errors(n_seq):
     need_gpu()
-    cfg = W.config5(seed=3, n_seq=6, width=3, vocab=1000)
+    cfg = W.config5(seed=3, n_seq=n_seq, width=3, vocab=1000)
     cfg["temperatures"][0:4] = 0.0        # sequence 0 greedy
     cfg["draft_ids"][1, 1] = 1000          # invalid id
     cfg["target"][2 * 4 + 2, 5] = np.nan   # NaN in sequence 2
     cfg["u_resample"][3] = 1.0             # invalid
     cfg["draft"][4 * 4 + 1, :] = -np.inf   # empty draft row
     (a, t, s), (wa, wt, ws) = run(cfg)
-    assert list(ws) == [0, 3, 2, 3, 1, 0]
+    assert list(ws[:6]) == [0, 3, 2, 3, 1, 0]
     assert np.array_equal(s, ws) and np.array_equal(a, wa) and np.array_equal(t, wt)
 
 
@@ -56,3 +57,42 @@ def test_spec_workspace_reused_across_shapes():
         log(f"spec workspace reuse n_seq={n_seq} width={width}")
         (a, t, s), (wa, wt, ws) = run(cfg)
         assert np.array_equal(s, ws) and np.array_equal(a, wa) and np.array_equal(t, wt), (n_seq, width)
+
+
+@pytest.mark.parametrize("n_seq", [12, 50])  # 48 rows: split kernels; 200 rows: one block per row
+@pytest.mark.parametrize("vocab", [3001, 8196, 12288])
+def test_spec_vocab_shapes_and_max_ties(vocab, n_seq):
+    """Odd vocabularies (single-element loads), splits that end mid-iteration, and greedy rows whose maximum is tied
+    (the lowest id wins, -0 ties +0)."""
+    need_gpu()
+    cfg = W.config5(seed=70 + vocab % 17, n_seq=n_seq, width=3, vocab=vocab)
+    log(f"spec vocab={vocab} n_seq={n_seq}")
+    cfg["temperatures"][0:4] = 0.0                       # sequence 0 greedy, tied maxima in every row
+    for j in range(4):
+        cfg["target"][j, :] = np.minimum(cfg["target"][j, :], 5.0)
+        cfg["target"][j, [vocab - 1, 7 + j, vocab // 2]] = 30.0
+    cfg["temperatures"][4:8] = 0.0                       # sequence 1 greedy, a row that is all zeros of both signs
+    cfg["target"][5, :] = 0.0
+    cfg["target"][5, : vocab // 3] = -0.0
+    cfg["target"][6, :] = -np.inf
+    cfg["target"][6, vocab - 2] = -0.0
+    cfg["target"][6, vocab - 1] = 0.0
+    (a, t, s), (wa, wt, ws) = run(cfg)
+    assert np.array_equal(s, ws) and np.array_equal(a, wa) and np.array_equal(t, wt)
+
+
+def test_spec_zero_residual_draws_target_argmax():
+    """A rejected draft with zero residual mass everywhere (draft row == target row, the draft token at -inf in both)
+    resamples the target's argmax, as the definition's fallback says."""
+    need_gpu()
+    cfg = W.config5(seed=91, n_seq=50, width=3, vocab=5000)
+    for s in range(4):
+        r = s * 4
+        cfg["draft"][r] = cfg["target"][r]
+        x = 17 + s
+        cfg["target"][r, x] = -np.inf
+        cfg["draft"][r, x] = -np.inf
+        cfg["draft_ids"][s, 0] = x
+    (a, t, s), (wa, wt, ws) = run(cfg)
+    assert list(wa[:4]) == [0, 0, 0, 0]
+    assert np.array_equal(s, ws) and np.array_equal(a, wa) and np.array_equal(t, wt)
