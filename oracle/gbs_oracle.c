@@ -514,7 +514,8 @@ int gbo_keyed_sample_row(const void* row, int dtype, int valid, const GbsKeyedRo
  *  10. draw:        Z = sum of the kept masses; t = floor(u * Z) exactly; the kept tokens taken in ascending id order, the
  *                   token is the first whose running mass sum exceeds t.
  *  prob = (float)((double)E_token / (double)Z); logprob = log-softmax over A at temperature T (1 when T == 0), double
- *  (NaN when the maximum is +inf).
+ *  (NaN when the maximum is +inf, or when 1/T overflows f32: a subnormal temperature, for which every token but the
+ *  maximum has probability 0 to within any f32 arithmetic).
  * ===================================================================================================================== */
 
 uint32_t gbo_order_key_f32(float v) {
@@ -790,7 +791,7 @@ void gbo_sample_row(const void* logits, int dtype, int vocab, const int32_t* cou
         const double Tp = T > 0.0f ? (double)T : 1.0;
         const double m = (double)M;
         double s = 0.0;
-        if (isinf(M)) { /* a +inf maximum: the log-softmax is undefined */
+        if (isinf(M) || (T > 0.0f && isinf(gbo_temp_scale(T)))) { /* undefined: a +inf maximum, or 1/T beyond f32 */
             out->logprob = NAN;
         } else {
             for (int i = 0; i < vocab; ++i)

@@ -257,7 +257,7 @@ __device__ RowOut finish_row(u64 list, const RowParamsDev& p, float u, bool inva
     }
     // log-softmax of the chosen token over the allowed tokens, base-2 online sums
     const float lx = __uint_as_float(readlane32(__float_as_uint(lval), chosen_rank));
-    if (isinf(M)) o.logprob = __uint_as_float(0x7fc00000u);
+    if (isinf(M) || !isfinite(clp)) o.logprob = __uint_as_float(0x7fc00000u);  // undefined: +inf maximum, 1/T beyond f32
     else o.logprob = ((lx - lse.m) * clp - log2f(lse.s)) * 0.6931471805599453f;
     return o;
 }

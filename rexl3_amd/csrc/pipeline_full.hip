@@ -18,6 +18,15 @@ using namespace gbs::modeu;
 
 namespace {
 
+#ifndef GBS_EXP_FULLT
+#define GBS_EXP_FULLT 0
+#endif
+#if GBS_EXP_FULLT
+__device__ u64 g_fdbg[65536];
+#define FT(k) do { if (threadIdx.x == 0) g_fdbg[(size_t)blockIdx.x * 8 + (k)] = wall_clock64(); } while (0)
+#else
+#define FT(k) do { } while (0)
+#endif
 constexpr int NTF = 1024;
 constexpr int NWF = NTF / WAVE;
 constexpr int DB = 11;
@@ -41,6 +50,40 @@ struct Row {
             return a - ((float)cnt * freq + pres);
         }
         return v;
+    }
+
+    // Raw loads of one 4-element group, for the pipelined streaming of whole rows (vec rows only): buffer loads whose
+    // range check returns zeros past the row's end, so nothing waits on a bounds test before the loads are issued.
+    struct Raw {
+        u32x4 x;  // f32: 4 values; bf16: the first two words
+        u32x4 c;
+        u32 m;
+    };
+    __device__ __forceinline__ void load_raw(int e, const __amdgpu_buffer_rsrc_t& rx, const __amdgpu_buffer_rsrc_t& rc,
+                                             const __amdgpu_buffer_rsrc_t& rm, Raw& w) const {
+        if (DT == GBS_DTYPE_F32) w.x = __builtin_amdgcn_raw_buffer_load_b128(rx, (u32)e * 4u, 0, 0);
+        else {
+            const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rx, (u32)e * 2u, 0, 0);
+            w.x = u32x4{v.x, v.y, 0u, 0u};
+        }
+        if (COUNTS) w.c = __builtin_amdgcn_raw_buffer_load_b128(rc, (u32)e * 4u, 0, 0);
+        if (MASK) w.m = __builtin_amdgcn_raw_buffer_load_b32(rm, (u32)(e >> 5) * 4u, 0, 0);
+    }
+    // the penalised, masked logits of a raw group at e (out of range: -inf)
+    __device__ __forceinline__ void from_raw(const Raw& w, int e, float (&l)[4]) const {
+        float xv[4];
+        if (DT == GBS_DTYPE_F32) {
+            xv[0] = __uint_as_float(w.x.x); xv[1] = __uint_as_float(w.x.y); xv[2] = __uint_as_float(w.x.z); xv[3] = __uint_as_float(w.x.w);
+        } else {
+            xv[0] = __uint_as_float(w.x.x << 16); xv[1] = __uint_as_float(w.x.x & 0xFFFF0000u);
+            xv[2] = __uint_as_float(w.x.y << 16); xv[3] = __uint_as_float(w.x.y & 0xFFFF0000u);
+        }
+        const u32 mw = MASK ? w.m >> (e & 31) : 0xFu;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const bool in = e + q < vocab && ((mw >> q) & 1u);
+            l[q] = in ? pen(xv[q], COUNTS ? (int)w.c[q] : 0) : -INFINITY;
+        }
     }
 
     // the penalised, masked logits of elements e..e+3 (out of range: -inf)
@@ -79,6 +122,50 @@ struct Row {
 
 __device__ __forceinline__ bool valid_l(float v) { return v > -INFINITY; }  // false for NaN and -inf
 
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t full_rsrc(const void* base, u32 bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// Streams the row tile by tile (tile t: elements [t * TILE, (t + 1) * TILE), thread tid the group at t * TILE + 4 tid),
+// calling f(t, e, l) with the group's penalised, masked logits; every thread calls f for every tile, so f may hold
+// block barriers. Rows that allow 16-byte loads keep the loads of DEPTH tiles in flight.
+constexpr int DEPTH = 4;
+template <int DT, bool COUNTS, bool MASK, class F>
+__device__ __forceinline__ void stream_tiles(const Row<DT, COUNTS, MASK>& R, F&& f) {
+    const int tid = threadIdx.x;
+    const int ntiles = (R.vocab + TILE - 1) / TILE;
+    if (!R.vec || R.vocab % 4 != 0) {  // the buffer loads below read whole 4-element groups
+        for (int t = 0; t < ntiles; ++t) {
+            const int e = t * TILE + tid * 4;
+            float l[4];
+            R.group(e, l);
+            f(t, e, l);
+        }
+        return;
+    }
+    const u32 esz = DT == GBS_DTYPE_F32 ? 4u : 2u;
+    const __amdgpu_buffer_rsrc_t rx = full_rsrc(R.x, (u32)R.vocab * esz);
+    const __amdgpu_buffer_rsrc_t rc = full_rsrc(R.c, COUNTS ? (u32)R.vocab * 4u : 0u);
+    const __amdgpu_buffer_rsrc_t rm = full_rsrc(R.m, MASK ? (u32)((R.vocab + 31) / 32) * 4u : 0u);
+    typename Row<DT, COUNTS, MASK>::Raw buf[DEPTH];
+#pragma unroll
+    for (int k = 0; k < DEPTH; ++k)
+        if (k < ntiles) R.load_raw(k * TILE + tid * 4, rx, rc, rm, buf[k]);
+    for (int t0 = 0; t0 < ntiles; t0 += DEPTH) {
+#pragma unroll
+        for (int k = 0; k < DEPTH; ++k) {
+            const int t = t0 + k;
+            if (t < ntiles) {
+                const int e = t * TILE + tid * 4;
+                float l[4];
+                R.from_raw(buf[k], e, l);
+                if (t + DEPTH < ntiles) R.load_raw(e + DEPTH * TILE, rx, rc, rm, buf[k]);
+                f(t, e, l);
+            }
+        }
+    }
+}
+
 template <typename T>
 __device__ __forceinline__ T block_sum(T v, T* s_red) {
     const int w = threadIdx.x / WAVE;
@@ -110,14 +197,22 @@ __device__ __forceinline__ u64 block_max_u64(u64 v, u64* s_red) {
     return r;
 }
 
+// The binned cut: 128 bins per unit of y = log2 of the mass relative to the maximum, down to y = -52 (below -51.5 every
+// mass is 0; the last bin takes them).
+constexpr int BINS_PER_UNIT = 128;
+constexpr int NBINS = 52 * BINS_PER_UNIT;
+constexpr int CAP = NB;  // collected tokens of the crossing bin (keys in sh.maxk, masses in sh.mass)
+
 struct Shared {
     u32 cnt[NB];
-    u64 mass[NB];
+    u64 mass[NBINS];  // the radix digits' masses (NB), or the binned cut's mass per bin (NBINS)
     u64 maxk[NB];
     u64 red[NWF];
     u64 tile[MAX_TILES];
+    u64 tilew[MAX_TILES][NWF];  // per-wave partial sums of a tile (no barrier per tile)
     float lse_m[NWF], lse_s[NWF];
     u64 bc[8];  // broadcast slots
+    u32 ncol;   // tokens collected by the binned cut
 };
 
 // One radix selection over the keys >= lb of the row: the key K at which the descending cumulative weight (count when
@@ -213,6 +308,140 @@ __device__ u64 radix_select(const Row<DT, COUNTS, MASK>& R, float M, float c2, u
     }
 }
 
+// ---- the binned cut (no top-k, finite maximum and 1/T): top-p and min-p in two reads of the row.
+// Tokens are binned by y = (l - M) * c2 (log2 of the mass relative to the maximum, computed exactly as the mass is):
+// bin = min(floor(-32 y), NBINS - 1), which never increases along the (value desc, id asc) order. Read 1 sums the
+// masses per bin; the crossing bin b* is the first bin (from the top) where the cumulative mass reaches
+// P = ceil(top_p * Z). Read 2 adds the kept masses of the bins above b* (mass >= Q, the min-p floor) per 4096-element
+// tile and collects the keys and masses of bin b*; sorting the collected keys gives the exact top-p key (the first
+// whose cumulative mass reaches P), and the kept ones of them are added to their tiles. Returns false (nothing kept
+// of its state) when bin b* holds more than CAP tokens: the caller takes the radix path.
+__device__ __forceinline__ u32 bin_of(float l, float M, float c2) {
+    const float y = (l - M) * c2;
+    return (u32)fminf(-y * (float)BINS_PER_UNIT, (float)(NBINS - 1));
+}
+
+template <int DT, bool COUNTS, bool MASK>
+__device__ bool binned_cut(const Row<DT, COUNTS, MASK>& R, float M, float c2, float top_p, u64 Q, u64* kp_out, Shared& sh) {
+    const int tid = threadIdx.x, w = tid / WAVE, l = lane_id();
+    const int ntiles = (R.vocab + TILE - 1) / TILE;
+    const bool topp = top_p > 0.0f && top_p < 1.0f;
+    u32 bstar = NBINS;  // no top-p: every bin is above the cut
+    u64 above = 0, P = 0;
+    if (topp) {
+        for (int i = tid; i < NBINS; i += NTF) sh.mass[i] = 0;
+        __syncthreads();
+        stream_tiles(R, [&](int, int, const float (&lv)[4]) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const u64 E = mass_fast(lv[q], M, c2);
+                if (E) atomicAdd((unsigned long long*)&sh.mass[bin_of(lv[q], M, c2)], (unsigned long long)E);
+            }
+        });
+        __syncthreads();
+        if (tid < WAVE) {
+            // lane i owns bins [32 i, 32 i + 32): the total, P, then the bin where the cumulative mass reaches P
+            constexpr int PB = NBINS / WAVE;
+            u64 s = 0;
+            for (int k = 0; k < PB; ++k) s += sh.mass[l * PB + k];
+            const u64 Z = wave_sum_u64(s);
+            const u64 Pv = mul_ceil64(top_p, Z);
+            const u64 incl = wave_scan_u64(s);
+            const u64 hit = ballot(incl >= Pv);
+            const int f = (int)__builtin_ctzll(hit);  // P <= Z: some lane reaches it
+            if (l == f) {
+                u64 acc = incl - s;
+                int b = l * PB;
+                for (int k = 0; k < PB; ++k) {
+                    b = l * PB + k;
+                    if (acc + sh.mass[b] >= Pv) break;
+                    acc += sh.mass[b];
+                }
+                sh.bc[0] = (u64)b;
+                sh.bc[1] = acc;
+                sh.bc[2] = Pv;
+            }
+        }
+        __syncthreads();
+        FT(2);
+        bstar = (u32)sh.bc[0];
+        above = sh.bc[1];
+        P = sh.bc[2];
+    }
+    // read 2: kept masses of the bins above b* per tile; the tokens of bin b* into (sh.maxk, sh.mass)
+    if (tid == 0) sh.ncol = 0;
+    __syncthreads();
+    stream_tiles(R, [&](int t, int e, const float (&lv)[4]) {
+        u64 s = 0;
+        u64 Eq[4];
+        bool col[4];
+        int ncol = 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            Eq[q] = mass_fast(lv[q], M, c2);
+            const u32 b = topp ? bin_of(lv[q], M, c2) : 0u;
+            const bool ok = valid_l(lv[q]);
+            if (ok && b < bstar && Eq[q] >= Q) s += Eq[q];
+            col[q] = ok && b == bstar;
+            ncol += col[q] ? 1 : 0;
+        }
+        // the group's tokens of bin b*: one LDS append per wave (an exclusive scan of the lanes' counts)
+        if (ballot(ncol > 0)) {
+            const u64 inc = wave_scan_u64((u64)ncol);
+            u32 base = 0;
+            if (l == WAVE - 1) base = atomicAdd(&sh.ncol, (u32)inc);
+            base = (u32)__builtin_amdgcn_readlane((int)base, WAVE - 1);
+            u32 idx = base + (u32)(inc - (u64)ncol);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                if (col[q]) {
+                    if (idx < (u32)CAP) {
+                        sh.maxk[idx] = make_key(okey_f32(lv[q]), (u32)(e + q));
+                        sh.mass[idx] = Eq[q];
+                    }
+                    ++idx;
+                }
+            }
+        }
+        s = wave_sum_u64(s);
+        if (l == 0) sh.tilew[t][w] = s;
+    });
+    __syncthreads();
+    for (int t = tid; t < ntiles; t += NTF) {
+        u64 v = 0;
+#pragma unroll
+        for (int k = 0; k < NWF; ++k) v += sh.tilew[t][k];
+        sh.tile[t] = v;
+    }
+    __syncthreads();
+    FT(3);
+    const u32 n = sh.ncol;
+    if (n > (u32)CAP) return false;
+    u64 kp = (u64)VALID_MIN_OK << 32;  // every valid key
+    if (topp) {
+        // For each collected token i, G_i = the mass of the collected tokens with larger keys (every thread reads the
+        // same key at once: LDS broadcasts). The top-p key is the one token with above + G_i < P <= above + G_i + E_i.
+        for (u32 i = tid; i < n; i += NTF) {
+            const u64 ki = sh.maxk[i];
+            u64 g = 0;
+            for (u32 j = 0; j < n; ++j) g += sh.maxk[j] > ki ? sh.mass[j] : 0ull;
+            const u64 lo = above + g;
+            if (lo < P && P <= lo + sh.mass[i]) sh.bc[3] = ki;
+        }
+        __syncthreads();
+        FT(4);
+        kp = sh.bc[3];
+        // the kept tokens of bin b* (key >= the top-p key, mass >= Q) into their tiles
+        for (u32 j = tid; j < n; j += NTF) {
+            const u64 E = sh.mass[j];
+            if (sh.maxk[j] >= kp && E >= Q) atomicAdd((unsigned long long*)&sh.tile[key_id(sh.maxk[j]) / TILE], (unsigned long long)E);
+        }
+        __syncthreads();
+    }
+    *kp_out = kp;
+    return true;
+}
+
 template <int DT, bool COUNTS, bool MASK>
 __global__ void __launch_bounds__(NTF) sample_full_k(const void* __restrict__ logits, long long stride, int vocab,
                                                      const int* __restrict__ counts, const u32* __restrict__ mask,
@@ -245,6 +474,7 @@ __global__ void __launch_bounds__(NTF) sample_full_k(const void* __restrict__ lo
             if (out_status) out_status[r] = status;
         }
     };
+    FT(0);
     if (params_invalid(p, u)) {
         finish(-1, -1, GBS_ROW_INVALID_PARAMS, 0.f, 0.f);
         return;
@@ -254,10 +484,7 @@ __global__ void __launch_bounds__(NTF) sample_full_k(const void* __restrict__ lo
     u64 kmaxv = 0;
     u32 nan = 0, nallowed = 0;
     Lse lse{-INFINITY, 0.f};
-    for (int base = 0; base < vocab; base += TILE) {
-        const int e = base + tid * 4;
-        float lv[4];
-        R.group(e, lv);
+    stream_tiles(R, [&](int, int e, const float (&lv)[4]) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             nan |= lv[q] != lv[q];
@@ -272,7 +499,7 @@ __global__ void __launch_bounds__(NTF) sample_full_k(const void* __restrict__ lo
                 lse.s += exp2f((lv[q] - lse.m) * clp);
             }
         }
-    }
+    });
     for (int m = 1; m < WAVE; m <<= 1) {
         const Lse o{__shfl_xor(lse.m, m, WAVE), __shfl_xor(lse.s, m, WAVE)};
         lse = lse_merge(lse, o, clp);
@@ -281,6 +508,7 @@ __global__ void __launch_bounds__(NTF) sample_full_k(const void* __restrict__ lo
         sh.lse_m[w] = lse.m;
         sh.lse_s[w] = lse.s;
     }
+    FT(1);
     const u32 nan_any = (u32)block_sum((u64)nan, sh.red);
     const u64 n_allowed = block_sum((u64)nallowed, sh.red);
     const u64 top = block_max_u64(kmaxv, sh.red);
@@ -297,7 +525,7 @@ __global__ void __launch_bounds__(NTF) sample_full_k(const void* __restrict__ lo
     const int greedy = (int)key_id(top);
     const float M = okey_to_f32(key_ok(top));
     auto logprob_of = [&](float lx) {
-        if (isinf(M)) return __uint_as_float(0x7fc00000u);
+        if (isinf(M) || !isfinite(clp)) return __uint_as_float(0x7fc00000u);  // undefined: +inf maximum, 1/T beyond f32
         return ((lx - rl.m) * clp - log2f(rl.s)) * 0.6931471805599453f;
     };
     if (p.temperature == 0.0f) {
@@ -306,12 +534,19 @@ __global__ void __launch_bounds__(NTF) sample_full_k(const void* __restrict__ lo
     }
     const float c2 = temp_scale(p.temperature);
 
+    const u64 Q = p.min_p > 0.0f ? mul_ceil64(p.min_p, MASS_ONE) : 0ull;
+    const int ntiles = (vocab + TILE - 1) / TILE;
+    const bool topk_on = p.top_k > 0 && (u64)p.top_k < n_allowed;
+    u64 kp = 0;
+    // the binned cut fills the tiles' kept masses itself
+    const bool binned = !topk_on && mass_fast_ok(M, c2) && binned_cut(R, M, c2, p.top_p, Q, &kp, sh);
+    if (!binned) {
     // ---- top-k
     const u64 floor_key = (u64)VALID_MIN_OK << 32;
     u64 lb = floor_key;
     u64 zk = 0;
     bool have_zk = false;
-    if (p.top_k > 0 && (u64)p.top_k < n_allowed) {
+    if (topk_on) {
         u64 above = 0;
         const u64 kk = radix_select(R, M, c2, floor_key, false, (u64)p.top_k, 0.0f, &above, nullptr, sh);
         lb = kk;
@@ -319,34 +554,32 @@ __global__ void __launch_bounds__(NTF) sample_full_k(const void* __restrict__ lo
         have_zk = true;
     }
     // ---- top-p
-    u64 kp = lb;
+    kp = lb;
     if (p.top_p > 0.0f && p.top_p < 1.0f) {
         u64 tot = 0;
         if (have_zk) kp = radix_select(R, M, c2, lb, true, mul_ceil64(p.top_p, zk), 0.0f, nullptr, nullptr, sh);
         else kp = radix_select(R, M, c2, lb, true, 0, p.top_p, nullptr, &tot, sh);
     }
+    }
     // ---- draw: kept = key >= kp and mass >= Q, in ascending id order
-    const u64 Q = p.min_p > 0.0f ? mul_ceil64(p.min_p, MASS_ONE) : 0ull;
     auto kept_mass = [&](float v, int i) -> u64 {
         if (!valid_l(v)) return 0ull;
         if (make_key(okey_f32(v), (u32)i) < kp) return 0ull;
         const u64 E = mass(v, M, c2);
         return E >= Q ? E : 0ull;
     };
-    const int ntiles = (vocab + TILE - 1) / TILE;
-    u64 z = 0;
-    for (int t = 0; t < ntiles; ++t) {
-        const int e = t * TILE + tid * 4;
-        float lv[4];
-        R.group(e, lv);
-        u64 s = 0;
+    if (!binned) {
+        stream_tiles(R, [&](int t, int e, const float (&lv)[4]) {
+            u64 s = 0;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) s += kept_mass(lv[q], e + q);
-        s = block_sum(s, sh.red);
-        if (tid == 0) sh.tile[t] = s;
-        z += s;
+            for (int q = 0; q < 4; ++q) s += kept_mass(lv[q], e + q);
+            s = block_sum(s, sh.red);
+            if (tid == 0) sh.tile[t] = s;
+        });
     }
     __syncthreads();
+    u64 z = 0;
+    for (int t = 0; t < ntiles; ++t) z += sh.tile[t];
     const u64 target = (u64)mul_floor(u, (u128)z, nullptr);
     int tsel = ntiles - 1;
     u64 before = 0;
@@ -392,9 +625,14 @@ __global__ void __launch_bounds__(NTF) sample_full_k(const void* __restrict__ lo
     const u64 ec = sh.bc[6];
     const float lx = __uint_as_float((u32)sh.bc[7]);
     finish(id, greedy, GBS_ROW_OK, (float)((double)ec / (double)z), logprob_of(lx));
+    FT(5);
 }
 
 }  // namespace
+
+#if GBS_EXP_FULLT
+GBS_EXPORT int gbs_debug_full_times(void* host) { return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_fdbg), sizeof(g_fdbg)); }
+#endif
 
 namespace gbs {
 

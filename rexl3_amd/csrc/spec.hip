@@ -60,7 +60,6 @@ constexpr int U = GBS_SPEC_U;        // 4-element groups per thread in flight, p
 constexpr int GSTEP = NT * 4;        // elements between a thread's groups (the draw)
 constexpr int DU = 4;                // the draw: 4-element groups per thread per tile
 constexpr int TILE = NT * 4 * DU;    // the draw: elements per tile
-constexpr int PER = TILE / NT;       // the draw: elements per thread in the scan of one tile
 constexpr int NWD = NT / WAVE;       // the draw: waves per block (one partial sum per wave and tile)
 constexpr int DRAW_BLOCKS = 768;     // the draw: blocks in all (one round on the chip)
 #ifndef GBS_SPEC_ROWS_MIN

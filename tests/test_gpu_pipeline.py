@@ -256,3 +256,32 @@ def test_workspace_reused_across_row_counts():
         log(what)
         g, w = run_both(cfg)
         compare(g, w, what)
+
+
+def test_full_path_binned_cut_edges():
+    """The full path's binned top-p cut and its fallbacks: a crossing bin of exactly 2048 tokens (collected) and of 2049
+    (the radix path), +inf in a row and a temperature whose 1/T overflows (the radix path), top-k with top-p (the
+    radix path), min-p with top-p, and config 3 at its full size."""
+    need_gpu()
+    rng = np.random.default_rng(23)
+    B, V = 12, 50_000
+    x = (rng.standard_normal((B, V)) * 2).astype(np.float32)
+    for r, n in [(0, 2048), (1, 2049), (2, 2047)]:
+        x[r] = -30.0
+        x[r, rng.choice(V, n, replace=False)] = 3.0
+    x[3, rng.choice(V, 4000, replace=False)] = 5.0 + rng.uniform(0, 1e-3, 4000).astype(np.float32)
+    x[4, 123] = np.inf
+    p = S.row_params(B, temperature=0.9, top_p=0.6, min_p=0.0, top_k=0)
+    p["temperature"][5] = 1e-39
+    p["top_k"][6] = 40
+    p["min_p"][7] = 0.05
+    p["top_p"][8] = 0.999999
+    p["top_p"][9] = 1e-7
+    u = W.uniforms_f32(29, B)
+    cfg = dict(logits=x, dtype="f32", params=p, uniforms=u, counts=None, mask=None)
+    g, w = run_both(cfg, kmax=0)
+    compare(g, w, "binned edges")
+    cfg = W.config3()
+    log("config3 full size, full path")
+    g, w = run_both(cfg, kmax=0)
+    compare(g, w, "config3 full size")
