@@ -187,7 +187,7 @@ def main():
 
         ms = time_launches(launch, args.steps, args.warmup)
         nbytes = algorithmic_bytes(rows, vocab, 4, False, False)
-        kernel = "keyed_sample_k"
+        kernel = "keyed_fast_k"
         dtype = "f32 (choose in f64)"
         workload = "keyed sampler (reference parity): exact top-58 of full rows + try_choose (T 0.8, top-k 50, top-p 0.9)"
         if not args.no_cpu:

@@ -66,12 +66,19 @@ __device__ int keyed_choose_wave(const float* vals, const u32* ids, int k, u64 s
         s_tmp[l] = l < k ? exp(sc - sc0) : 0.0;
         wave_lds_sync();
         int kp = 0;
+        // the quotients probs[i] / total on their own lanes (the same IEEE divisions), the running sum on lane 0
+        double total = 0.0;
+        if (l == 0) total = pairwise_small(s_tmp, k);
+        total = __shfl(total, 0, WAVE);
+        const double q = l < k ? s_tmp[l] / total : 0.0;
+        wave_lds_sync();
+        s_tmp[l] = q;
+        wave_lds_sync();
         if (l == 0) {
-            const double total = pairwise_small(s_tmp, k);
             double c = 0.0;
             int below = 0;
             for (int i = 0; i < k; ++i) {
-                c += s_tmp[i] / total;
+                c += s_tmp[i];
                 if (c < top_p) ++below;
             }
             kp = below + 1 < k ? below + 1 : k;
@@ -179,6 +186,10 @@ __global__ void greedy_gather_k(const int* __restrict__ ids, const float* __rest
 
 // ------------------------------------------------------------------------------------------------ fused keyed sampler
 
+#ifndef GBS_KEYED_FAST
+#define GBS_KEYED_FAST 1
+#endif
+constexpr bool KEYED_FAST = GBS_KEYED_FAST;  // the one-block-per-row kernel (else the split kernel)
 constexpr int KS_TARGET_BLOCKS = 1024;
 constexpr int KS_MIN_CHUNK = 4096;
 
@@ -197,9 +208,13 @@ size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 // workspace cleared once serves launches of any shape.
 constexpr size_t KEYED_CTL_BYTES = (size_t)65536 * 4;
 
+int keyed_fast_splits(int rows, int valid);
+
 size_t keyed_ws_bytes(int rows, int valid) {
     if (rows <= 0 || valid <= 0) return 0;
-    const int s = keyed_splits(rows, valid);
+    int s = keyed_splits(rows, valid);
+    const int sf = keyed_fast_splits(rows, valid);
+    s = s > sf ? s : sf;
     return KEYED_CTL_BYTES + (size_t)rows * s * WAVE * sizeof(u64);
 }
 
@@ -243,7 +258,7 @@ __global__ void __launch_bounds__(NT) keyed_sample_k(const void* logits, long lo
     int status = ok ? GBS_ROW_OK : GBS_ROW_INVALID_PARAMS;
     const u32 id = key_id(list);
     float v = 0.f;
-    if (l < count) {
+    if (l < count && list != 0ull) {  // the first `count` keys are elements of the row (every valid element is offered)
         if (DT == DT_F32) v = ((const float*)row)[id];
         else v = okey16_to_f32<DT == DT_F16>(key_ok(list));
     }
@@ -264,6 +279,313 @@ __global__ void __launch_bounds__(NT) keyed_sample_k(const void* logits, long lo
         if (out_status) out_status[r] = status;
     }
 }
+
+// ------------------------------------------------------------------------------------------------ fused keyed sampler,
+// one block per row
+//
+// The same result as keyed_sample_k, on the north-star kernel's streaming design: a block of KNT threads per row (rows
+// split over blocks only when there are fewer rows than CUs). Wave-steps of KWSTEP contiguous elements (KGROUPS
+// 4-element groups per lane) are handed out through an LDS counter, two in flight per wave; each wave keeps its gated
+// top-64 list, the gate raised by the block bound of every wave's best keys. With one block per row the block merges
+// its wave lists and draws; otherwise the blocks hand their lists to the row's last block.
+#ifndef GBS_KEYED_NT
+#define GBS_KEYED_NT 1024
+#endif
+#ifndef GBS_EXP_KBARE
+#define GBS_EXP_KBARE 0
+#endif
+#ifndef GBS_KEYED_ROT
+#define GBS_KEYED_ROT 1
+#endif
+#ifndef GBS_KEYED_GROUPS
+#define GBS_KEYED_GROUPS 4
+#endif
+#ifndef GBS_EXP_KTIMES
+#define GBS_EXP_KTIMES 0
+#endif
+#if GBS_EXP_KTIMES
+__device__ u64 g_kdbg[65536];
+#endif
+constexpr int KNT = GBS_KEYED_NT;
+constexpr int KNW = KNT / WAVE;
+constexpr int KGROUPS = GBS_KEYED_GROUPS;
+constexpr int KGS = WAVE * 4;           // elements between a lane's groups
+constexpr int KWSTEP = KGS * KGROUPS;   // elements of one wave-step
+constexpr int KBUF = WAVE * (4 + 1);  // < 64 keys left after a flush + one 4-element group per lane (flushed per group)
+constexpr int KF_TARGET_BLOCKS = 256;
+constexpr u32 NEG_INF_OK = 0x007FFFFFu;  // okey_f32(-inf)
+constexpr int KF_MIN_CHUNK = 4096;
+
+int keyed_fast_splits(int rows, int valid) {
+    int s = (KF_TARGET_BLOCKS + rows - 1) / rows;
+    const int by_size = (valid + KF_MIN_CHUNK - 1) / KF_MIN_CHUNK;
+    if (s > by_size) s = by_size;
+    return s < 1 ? 1 : s;
+}
+
+template <int DT>
+struct KRaw {
+    typename std::conditional<DT == DT_F32, u32x4, u32x2>::type x[KGROUPS];
+};
+
+template <int DT>
+__device__ __forceinline__ void kraw_keys(const KRaw<DT>& r, int j, u32 (&k)[4]) {
+    if constexpr (DT == DT_F32) {
+        const u32x4 v = r.x[j];
+        k[0] = okey_f32_nanlow(__uint_as_float(v.x)); k[1] = okey_f32_nanlow(__uint_as_float(v.y));
+        k[2] = okey_f32_nanlow(__uint_as_float(v.z)); k[3] = okey_f32_nanlow(__uint_as_float(v.w));
+    } else {
+        const u32x2 v = r.x[j];
+        k[0] = okey_16<DT == DT_F16>(v.x); k[1] = okey_16<DT == DT_F16>(v.x >> 16);
+        k[2] = okey_16<DT == DT_F16>(v.y); k[3] = okey_16<DT == DT_F16>(v.y >> 16);
+    }
+}
+
+template <int DT>
+__global__ void __launch_bounds__(KNT, 1) keyed_fast_k(const void* logits, long long stride, int valid, int chunk,
+                                                       const KeyedRowDev* __restrict__ params, int depth, bool vec, unsigned* counters,
+                                                       u64* parts, int* out_ids, float* out_vals, int* out_status) {
+    __shared__ u64 s_buf[KNW][KBUF];
+    __shared__ u64 s_list[KNW][WAVE];
+    __shared__ float s_v[WAVE];
+    __shared__ u32 s_id[WAVE];
+    __shared__ double s_tmp[WAVE];
+    __shared__ unsigned s_flag;
+    __shared__ u64 s_thr;
+    __shared__ u32 s_top[KNW * WaveTop<KBUF>::TOPN];
+    __shared__ int s_next;
+    const int S = gridDim.x, sp = blockIdx.x, r = blockIdx.y;
+    const int tid = threadIdx.x, w = tid / WAVE, l = lane_id();
+#if GBS_EXP_KTIMES
+    const u64 t0 = wall_clock64();
+    if (tid == 0) g_kdbg[(size_t)r * 8 + 0] = t0;
+#endif
+    if (tid == 0) {
+        s_thr = 0;
+        s_next = KNW;
+    }
+    if (tid < KNW * WaveTop<KBUF>::TOPN) s_top[tid] = 0;
+    __syncthreads();
+    const size_t esz = DT == DT_F32 ? 4 : 2;
+    const void* row = (const char*)logits + (size_t)r * (size_t)stride * esz;
+    const KeyedRowDev p = params[r];
+    const bool ok = keyed_params_ok(p);
+    const int count = ok ? min(p.top_k + 8, valid) : min(WAVE, valid);
+    const int lo = sp * chunk;
+    const int hi = min(valid, lo + chunk);
+    WaveTop<KBUF> wt;
+    wt.init(s_buf[w], count, 0ull, &s_thr);
+    wt.set_top(s_top, w, KNW);
+    int e0 = lo;
+    u32 bare_acc = 0;
+    if (vec) {
+        // loads past the row's valid columns (rounded up to a whole group, inside the row) return zeros; the last
+        // wave-step's elements at or past `hi` are not offered
+        const u32 nbytes = (u32)((valid + 3) / 4 * 4) * (u32)esz;
+        const __amdgpu_buffer_rsrc_t R = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(row), (short)0, (int)nbytes, 0x00020000);
+        const int nws = (hi - lo + KWSTEP - 1) / KWSTEP;
+        // wave-step idx covers [lo + pos(idx) KWSTEP, ...): the order is rotated by a row-dependent offset, so that the
+        // blocks of a batch do not all read the same offsets of their rows at once
+        const int rot = GBS_KEYED_ROT ? (int)(((unsigned)r * 37u) % (unsigned)(nws > 0 ? nws : 1)) : 0;
+        auto pos = [&](int idx) { const int q = idx + rot; return q >= nws ? q - nws : q; };
+        auto load = [&](int idx, KRaw<DT>& b) {
+            const u32 e = (u32)(lo + pos(idx) * KWSTEP + l * 4);
+#pragma unroll
+            for (int j = 0; j < KGROUPS; ++j) {
+                if constexpr (DT == DT_F32) b.x[j] = __builtin_amdgcn_raw_buffer_load_b128(R, (e + j * KGS) * 4u, 0, 2);
+                else b.x[j] = __builtin_amdgcn_raw_buffer_load_b64(R, (e + j * KGS) * 2u, 0, 2);
+            }
+        };
+        auto grab = [&]() {
+            int t = 0;
+            if (l == 0) t = __hip_atomic_fetch_add(&s_next, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            return __builtin_amdgcn_readfirstlane(t);
+        };
+        // the keys of one loaded wave-step (out of the chunk: key 0, not offered); `first` seeds the gate
+        auto step = [&](KRaw<DT>& B, int idx, bool first, auto&& reload) __attribute__((always_inline)) {
+            const int e = lo + pos(idx) * KWSTEP + l * 4;
+            wt.apply_shared();
+            wt.prefetch_shared();
+            // f32 rows whose gate is a float at or above -inf test the gate with one float compare per element (NaN
+            // never passes, as its key 0 is below any such gate); the order keys are built for the elements that pass
+            if constexpr (DT == DT_F32) {
+                if (!first && wt.gate >= NEG_INF_OK) {
+                    float v[KGROUPS * 4];
+                    bool in[KGROUPS * 4];
+#pragma unroll
+                    for (int j = 0; j < KGROUPS; ++j) {
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            in[j * 4 + q] = e + j * KGS + q < hi;
+                            v[j * 4 + q] = __uint_as_float(B.x[j][q]);
+                        }
+                    }
+                    reload();
+                    const float gf = okey_to_f32(wt.gate);
+                    bool any = false;
+#pragma unroll
+                    for (int i = 0; i < KGROUPS * 4; ++i) any |= in[i] && v[i] >= gf;
+                    if (ballot(any)) {
+#pragma unroll
+                        for (int j = 0; j < KGROUPS; ++j) {
+#pragma unroll
+                            for (int q = 0; q < 4; ++q) {
+                                const int i = j * 4 + q;
+                                const bool pass = in[i] && v[i] >= gf;
+                                wt.offer_ok(pass ? okey_f32_nanlow(v[i]) : 0u, (u32)(e + j * KGS + q), pass);
+                            }
+                            wt.flush(false);
+                        }
+                    }
+                    return;
+                }
+            }
+            u32 k[KGROUPS * 4];
+            bool in[KGROUPS * 4];
+#pragma unroll
+            for (int j = 0; j < KGROUPS; ++j) {
+                u32 kj[4];
+                kraw_keys<DT>(B, j, kj);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    in[j * 4 + q] = e + j * KGS + q < hi;
+                    k[j * 4 + q] = in[j * 4 + q] ? kj[q] : 0u;
+                }
+            }
+            reload();
+            if (first) {
+                u32 m = 0;
+#pragma unroll
+                for (int i = 0; i < KGROUPS * 4; ++i) m = k[i] > m ? k[i] : m;
+                wt.seed(m);
+                __syncthreads();
+#if GBS_EXP_KTIMES
+                if (tid == 0) g_kdbg[(size_t)r * 8 + 1] = wall_clock64();
+#endif
+                wt.block_bound();
+            }
+#if GBS_EXP_KBARE
+            for (int i = 0; i < KGROUPS * 4; ++i) bare_acc ^= k[i];
+            return;
+#endif
+            const u32 g = wt.gate;
+            bool any = false;
+#pragma unroll
+            for (int i = 0; i < KGROUPS * 4; ++i) any |= in[i] && k[i] >= g;
+            if (ballot(any)) {
+#pragma unroll
+                for (int j = 0; j < KGROUPS; ++j) {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) wt.offer_ok(k[j * 4 + q], (u32)(e + j * KGS + q), in[j * 4 + q]);
+                    wt.flush(false);
+                }
+            }
+        };
+        KRaw<DT> A, B;
+        int ia = w;
+        (void)bare_acc;
+        int ib = grab();
+        if (ia < nws) load(ia, A);
+        if (ib < nws) load(ib, B);
+        if (ia >= nws) {
+            // no wave-step of its own: take part in the block's seeding barrier
+            wt.seed(0u);
+            __syncthreads();
+            wt.block_bound();
+        } else {
+            for (bool first = true;; first = false) {
+                int na = 0, nb = 0;
+                step(A, ia, first, [&]() {
+                    na = grab();
+                    if (na < nws) load(na, A);
+                });
+                ia = na;
+                if (ib >= nws) break;
+                step(B, ib, false, [&]() {
+                    nb = grab();
+                    if (nb < nws) load(nb, B);
+                });
+                ib = nb;
+                if (ia >= nws) break;
+            }
+        }
+        e0 = hi;
+    }
+    // unaligned rows: one guarded group per lane per round
+    const int rounds = (hi - e0 + KNT * 4 - 1) / (KNT * 4);
+    for (int rr = 0; rr < rounds; ++rr) {
+        const int eg = e0 + rr * KNT * 4 + tid * 4;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) wt.offer_ok(eg + q < hi ? elem_key<DT>(row, eg + q) : 0u, (u32)(eg + q), eg + q < hi);
+        wt.flush(false);
+    }
+    wt.prefetch_shared();
+    wt.apply_shared();
+    wt.flush(true);
+#if GBS_EXP_KTIMES
+    {
+        __shared__ u64 s_tw[KNW];
+        if (l == 0) s_tw[w] = wall_clock64();
+        __syncthreads();
+        if (tid == 0) {
+            u64 mn = ~0ull, mx = 0;
+            for (int o = 0; o < KNW; ++o) { mn = s_tw[o] < mn ? s_tw[o] : mn; mx = s_tw[o] > mx ? s_tw[o] : mx; }
+            g_kdbg[(size_t)r * 8 + 2] = mn;
+            g_kdbg[(size_t)r * 8 + 3] = mx;
+        }
+    }
+#endif
+#if GBS_EXP_KBARE
+    // the bare variant offers nothing: its lists hold no element, so it ends before the finish reads any
+    if (tid == 0) out_ids[r] = (int)bare_acc;
+    return;
+#endif
+    u64 list = block_tree_merge<KNW>(wt.list, s_list);
+    if (S > 1) {
+        if (tid < WAVE) st_agent(&parts[((size_t)r * S + sp) * WAVE + tid], list);
+        if (!arrive_last(&counters[r], (unsigned)S, &s_flag)) return;
+        list = block_merge_lists<KNW>(parts + (size_t)r * S * WAVE, S, s_list);
+    }
+    if (tid >= WAVE) return;
+#if GBS_EXP_KTIMES
+    if (tid == 0) g_kdbg[(size_t)r * 8 + 5] = wall_clock64();
+#endif
+    int status = ok ? GBS_ROW_OK : GBS_ROW_INVALID_PARAMS;
+    const u32 id = key_id(list);
+    float v = 0.f;
+    if (l < count && list != 0ull) {  // the first `count` keys are elements of the row (every valid element is offered)
+        if (DT == DT_F32) v = ((const float*)row)[id];
+        else v = okey16_to_f32<DT == DT_F16>(key_ok(list));
+    }
+    if (status == GBS_ROW_OK && ballot(l < count && v != v)) status = GBS_ROW_NAN_LOGIT;
+    int pick = 0;
+#if GBS_EXP_KTIMES
+    if (tid == 0) g_kdbg[(size_t)r * 8 + 6] = wall_clock64();
+#endif
+    if (status == GBS_ROW_OK && p.temperature > 0.0) {
+        s_v[l] = v;
+        s_id[l] = id;
+        wave_lds_sync();
+        const int k = min(p.top_k, count);
+        pick = keyed_choose_wave(s_v, s_id, k, p.seed, p.temperature, p.top_p, p.min_p, p.first_position + (u64)depth, s_tmp);
+    }
+    const u32 pid = readlane32(id, pick);
+    const float pv = __uint_as_float(readlane32(__float_as_uint(v), pick));
+    if (l == 0) {
+        out_ids[r] = status == GBS_ROW_OK ? (int)pid : -1;
+        if (out_vals) out_vals[r] = status == GBS_ROW_OK ? pv : __uint_as_float(0x7fc00000u);
+        if (out_status) out_status[r] = status;
+#if GBS_EXP_KTIMES
+        g_kdbg[(size_t)r * 8 + 4] = wall_clock64();
+#endif
+    }
+}
+
+#if GBS_EXP_KTIMES
+}  // namespace
+GBS_EXPORT int gbs_debug_keyed_times(void* host) { return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_kdbg), sizeof(g_kdbg)); }
+namespace {
+#endif
 
 // ------------------------------------------------------------------------------------------------ accept steps
 
@@ -351,13 +673,31 @@ GBS_EXPORT int gbs_keyed_sample_rows(const void* logits, int dtype, int rows, in
     if (rows == 0) return 0;
     if (rows > 65535 || !logits || !params || !out_ids || !ws || !aligned(ws, 256)) return GBS_ERR_INVALID;
     if (ws_bytes < keyed_ws_bytes(rows, valid)) return GBS_ERR_INVALID;
+    unsigned* counters = (unsigned*)ws;
+    u64* parts = (u64*)((char*)ws + KEYED_CTL_BYTES);
+    const KeyedRowDev* p = (const KeyedRowDev*)params;
+    if (KEYED_FAST) {
+        const int S = keyed_fast_splits(rows, valid);
+        int chunk = (valid + S - 1) / S;
+        chunk = (chunk + 3) / 4 * 4;
+        const size_t esz = dtype == GBS_DTYPE_F32 ? 4 : 2;
+        const bool vec = stride % 4 == 0 && aligned(logits, 4 * esz);
+        const dim3 grid(S, rows);
+        if (dtype == GBS_DTYPE_F32)
+            hipLaunchKernelGGL(keyed_fast_k<DT_F32>, grid, dim3(KNT), 0, to_stream(stream), logits, (long long)stride, valid, chunk, p,
+                               depth, vec, counters, parts, out_ids, out_vals, out_status);
+        else if (dtype == GBS_DTYPE_BF16)
+            hipLaunchKernelGGL(keyed_fast_k<DT_BF16>, grid, dim3(KNT), 0, to_stream(stream), logits, (long long)stride, valid, chunk, p,
+                               depth, vec, counters, parts, out_ids, out_vals, out_status);
+        else
+            hipLaunchKernelGGL(keyed_fast_k<DT_F16>, grid, dim3(KNT), 0, to_stream(stream), logits, (long long)stride, valid, chunk, p,
+                               depth, vec, counters, parts, out_ids, out_vals, out_status);
+        return launch_status();
+    }
     const int S = keyed_splits(rows, valid);
     int chunk = (valid + S - 1) / S;
     chunk = (chunk + 3) / 4 * 4;
-    unsigned* counters = (unsigned*)ws;
-    u64* parts = (u64*)((char*)ws + KEYED_CTL_BYTES);
     const dim3 grid(S, rows);
-    const KeyedRowDev* p = (const KeyedRowDev*)params;
     if (dtype == GBS_DTYPE_F32)
         hipLaunchKernelGGL(keyed_sample_k<DT_F32>, grid, dim3(NT), 0, to_stream(stream), logits, (long long)stride, valid, chunk, p,
                            depth, counters, parts, out_ids, out_vals, out_status);

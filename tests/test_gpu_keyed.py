@@ -218,3 +218,37 @@ def test_fused_keyed_workspace_reused_across_row_counts():
         gi, gs, _ = S.keyed_sample_rows(dev(x), recs, 0)
         wi, _, ws = O.keyed_sample_rows(x, O.DTYPE_F32, vocab, recs, 0)
         assert np.array_equal(host(gs), ws) and np.array_equal(host(gi), wi), rows
+
+
+@pytest.mark.parametrize("dtype,rows,stride,valid", [(O.DTYPE_F32, 256, 151936, 151936), (O.DTYPE_BF16, 256, 151936, 151936),
+                                                     (O.DTYPE_F16, 260, 20000, 19999), (O.DTYPE_F32, 256, 151940, 151933),
+                                                     (O.DTYPE_F32, 300, 1001, 1001), (O.DTYPE_BF16, 257, 4098, 4097)])
+def test_fused_keyed_full_batches(dtype, rows, stride, valid):
+    """One block per row (256 rows and more): full vocabularies in every dtype, padded rows (valid < stride, columns
+    past `valid` poisoned), and strides that rule out 16-byte loads."""
+    need_gpu()
+    rng = np.random.default_rng(rows + stride)
+    x = W.peaked_logits(int(rng.integers(1 << 30)), rows, stride, 2.0, (4, 16), 6.0, 14.0)
+    x[:, valid:] = 1e30  # never a candidate: past the valid columns
+    x[5, :] = 0.5        # a row of one value
+    x[7, rng.choice(valid, 100, replace=False)] = np.nan
+    if dtype == O.DTYPE_BF16:
+        data = W.to_bf16_bits(x)
+        t = dev(data, torch.bfloat16)
+    elif dtype == O.DTYPE_F16:
+        data = np.clip(x, -6e4, 6e4).astype(np.float16).view(np.uint16)
+        t = dev(data, torch.float16)
+    else:
+        data = x
+        t = dev(data)
+    recs = np.zeros(rows, dtype=S.KEYED_ROW_DTYPE)
+    for r in range(rows):
+        recs[r] = (int(rng.integers(1 << 62)), int(rng.integers(1 << 20)), float(rng.choice([0.0, 0.7, 1.0])),
+                   float(rng.choice([1.0, 0.9, 0.5])), float(rng.choice([0.0, 0.05])), int(rng.choice([1, 20, 50, 56])), 1)
+    log(f"fused keyed full batch dtype={dtype} rows={rows} stride={stride} valid={valid}")
+    gi, gs, gv = S.keyed_sample_rows(t, recs, 2, valid=valid, out_vals=True)
+    wi, wv, ws = O.keyed_sample_rows(data, dtype, valid, recs, 2)
+    gi, gs, gv = host(gi), host(gs), host(gv)
+    assert np.array_equal(gs, ws)
+    assert np.array_equal(gi, wi), np.nonzero(gi != wi)[0][:10]
+    assert np.array_equal(gv.view(np.uint32), wv.view(np.uint32))
