@@ -118,6 +118,15 @@ size_t gb_glm_topk_f16_workspace_bytes(int rows, int valid, int count);
 int gb_glm_topk_f16(const void* logits, int rows, int stride, int valid, int count, int* ids, float* vals, void* workspace,
                     size_t ws_bytes, void* stream);
 
+/* Replaces crates/cuda/csrc/ling_kda_proj_fused.cu:2735-2764 (gb_ling_topk_f16_workspace_bytes / gb_ling_topk_f16):
+ * gb_glm_topk_f16's results in ONE launch (the row's last chunk block merges the row's lists). Workspace: 256 bytes of
+ * per-row arrival counters, then gb_glm_topk_f16_workspace_bytes(rows, valid, count); 16-byte aligned; the counters
+ * must be zero before the first call (clear the workspace once, e.g. gbs_workspace_clear) and every call leaves them
+ * zero. rows <= 64 (the counter region's capacity; more rows return GBS_ERR_INVALID). */
+size_t gb_ling_topk_f16_workspace_bytes(int rows, int valid, int count);
+int gb_ling_topk_f16(const void* logits, int rows, int stride, int valid, int count, int* ids, float* vals, void* workspace,
+                     size_t ws_bytes, void* stream);
+
 /*
  * Replaces crates/cuda/csrc/glm_mtp.cu:272-280 (gb_glm_keyed_pick). ids i32 / vals f32 [rows, count] sorted by
  * (value desc, id asc), count <= 64; params GbsKeyedRow[rows]. A keyed row with temperature > 0 takes

@@ -23,6 +23,8 @@ SIGNATURES = {
     "gb_nemo_glue_topk": (I, [P, I, I, I, I, P, Z, P, P, P]),
     "gb_glm_topk_f16_workspace_bytes": (Z, [I, I, I]),
     "gb_glm_topk_f16": (I, [P, I, I, I, I, P, P, P, Z, P]),
+    "gb_ling_topk_f16_workspace_bytes": (Z, [I, I, I]),
+    "gb_ling_topk_f16": (I, [P, I, I, I, I, P, P, P, Z, P]),
     "gb_glm_keyed_pick": (I, [P, P, I, I, P, I, P, P, P]),
     "gb_qfn_greedy_gather": (I, [P, P, I, I, P, P, P]),
     "gbs_workspace_clear": (I, [P, Z, P]),

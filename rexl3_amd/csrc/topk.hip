@@ -63,6 +63,48 @@ __global__ void __launch_bounds__(NT) topk_stage2_k(const void* logits, long lon
     }
 }
 
+// Stage 1 and stage 2 in ONE launch: every chunk block writes its list to the workspace (agent-scope stores) and counts
+// its arrival; the row's last block merges the row's lists (agent-scope loads) and writes ids / values, as stage 2 does.
+// The arrival counter of row r is counters[r]; the last block resets it to 0.
+template <int DT>
+__global__ void __launch_bounds__(NT) topk_fused_k(const void* logits, long long stride, int valid, int chunk, int nchunks, int count,
+                                                   int pitch, unsigned* counters, u64* ws, int* ids, float* vals) {
+    __shared__ u64 s_buf[NW][BUF];
+    __shared__ u64 s_list[NW][WAVE];
+    __shared__ unsigned s_flag;
+    const int c = blockIdx.x, r = blockIdx.y;
+    const int w = threadIdx.x / WAVE, l = lane_id();
+    const size_t esz = DT == DT_F32 ? 4 : 2;
+    const void* row = (const char*)logits + (size_t)r * (size_t)stride * esz;
+    const int lo = c * chunk;
+    const int hi = min(valid, lo + chunk);
+    const bool vec = (stride % 4 == 0) && aligned(logits, DT == DT_F32 ? 16 : 8);
+    WaveTop<BUF> wt;
+    wt.init(s_buf[w], count, 0ull);
+    block_select<DT>(row, lo, hi, vec, count, wt, s_list);
+    u64* lists = ws + (size_t)r * nchunks * pitch;
+    if ((int)threadIdx.x < pitch) st_agent(&lists[(size_t)c * pitch + threadIdx.x], wt.list);
+    if (!arrive_last(&counters[r], (unsigned)nchunks, &s_flag)) return;
+    u64 list = 0;
+    for (int o = w; o < nchunks; o += NW) {
+        const u64 g = l < pitch ? ld_agent(&lists[(size_t)o * pitch + l]) : 0ull;
+        list = wave_merge_desc(list, g);
+    }
+    __syncthreads();
+    list = block_tree_merge<NW>(list, s_list);
+    if (w == 0 && l < count) {
+        int id = -1;
+        float v = -INFINITY;
+        if (list != 0ull) {
+            id = (int)key_id(list);
+            if (DT == DT_F32) v = ((const float*)logits)[(size_t)r * (size_t)stride + (size_t)id];  // as stored
+            else v = okey16_to_f32<DT == DT_F16>(key_ok(list));
+        }
+        ids[(size_t)r * count + l] = id;
+        vals[(size_t)r * count + l] = v;
+    }
+}
+
 template <int DT>
 int launch_topk(const void* logits, int rows, long long stride, int valid, int count, int chunk, int nchunks, int pitch, int* ids,
                 float* vals, u64* ws, void* stream) {
@@ -136,4 +178,29 @@ GBS_EXPORT int gb_nemo_glue_topk(const void* logits, int rows, int vocab, int co
     const int nchunks = (int)(((long long)vocab + chunk - 1) / chunk);
     return launch_topk<DT_F32>(logits, rows, vocab, vocab, count, (int)chunk, nchunks, count, (int*)ids, (float*)vals, (u64*)ws,
                                stream);
+}
+
+// The single-launch fp16 variant (crates/cuda/csrc/ling_kda_proj_fused.cu:2735-2764): bytes [0, 256) of the workspace
+// hold the per-row arrival counters (64 rows; zero before the first call, every call leaves them zero), then the
+// lists of the gb_glm_topk_f16 plan. Results are gb_glm_topk_f16's.
+constexpr int LING_ROWS_MAX = 64;
+constexpr size_t LING_CTL_BYTES = 256;
+
+GBS_EXPORT size_t gb_ling_topk_f16_workspace_bytes(int rows, int valid, int count) {
+    if (rows <= 0 || valid <= 0 || count <= 0 || count > GBS_MAX_COUNT) return 0;
+    return LING_CTL_BYTES + topk16_ws_bytes(rows, valid, count);
+}
+
+GBS_EXPORT int gb_ling_topk_f16(const void* logits, int rows, int stride, int valid, int count, int* ids, float* vals, void* workspace,
+                                size_t ws_bytes, void* stream) {
+    if (rows < 0 || valid < 1 || valid > stride || count < 1 || count > GBS_MAX_COUNT || count > valid) return GBS_ERR_INVALID;
+    if (rows == 0) return 0;
+    // the counter region holds 64 rows: more would put counters where the lists are
+    if (rows > LING_ROWS_MAX || !logits || !ids || !vals || !workspace || !aligned(workspace, 16)) return GBS_ERR_INVALID;
+    if (ws_bytes < gb_ling_topk_f16_workspace_bytes(rows, valid, count)) return GBS_ERR_INVALID;
+    const int nchunks = (int)ref_nchunks(valid);
+    hipLaunchKernelGGL(topk_fused_k<DT_F16>, dim3(nchunks, rows), dim3(NT), 0, to_stream(stream), logits, (long long)stride, valid,
+                       REF_CHUNK, nchunks, count, ref_pitch(count), (unsigned*)workspace,
+                       (u64*)((char*)workspace + LING_CTL_BYTES), ids, vals);
+    return launch_status();
 }

@@ -125,6 +125,24 @@ def topk(logits: torch.Tensor, count: int, valid: int | None = None, blocks: int
     return ids, vals
 
 
+def topk_f16_single_launch(logits: torch.Tensor, count: int, valid: int | None = None, workspace: torch.Tensor | None = None):
+    """gb_ling_topk_f16 (crates/cuda/src/ling_kda_proj_fused.rs:1409-1452, `topk_f16`): gb_glm_topk_f16's exact per-row
+    top-`count` of fp16 logits in one launch. The workspace's first 256 bytes are self-resetting arrival counters: a
+    caller-owned workspace must be cleared once before its first use (the default one is). Returns (ids, vals)."""
+    _require_cuda(logits, "logits")
+    if logits.dtype != torch.float16:
+        raise ValueError("gb_ling_topk_f16 takes fp16 logits")
+    rows, stride = logits.shape
+    valid = stride if valid is None else valid
+    dev = logits.device
+    ids = torch.empty((rows, count), dtype=torch.int32, device=dev)
+    vals = torch.empty((rows, count), dtype=torch.float32, device=dev)
+    wsb = _lib.load().gb_ling_topk_f16_workspace_bytes(rows, valid, count)
+    ws = WORKSPACE.get(dev, "ling_topk", wsb) if workspace is None else workspace
+    _lib.call("gb_ling_topk_f16", _ptr(logits), rows, stride, valid, count, _ptr(ids), _ptr(vals), _ptr(ws), ws.numel(), _stream(dev))
+    return ids, vals
+
+
 def keyed_rows(samplings, positions) -> np.ndarray:
     """KeyedRow records (crates/cuda/csrc/glm_mtp.cu:258-264) for a list of Sampling and absolute positions."""
     recs = np.zeros(len(samplings), dtype=KEYED_ROW_DTYPE)

@@ -187,3 +187,32 @@ def test_refusals():
     assert lib.gb_topk_valid_workspace_bytes(1, 100, 65) == 0
     assert lib.gb_topk_valid(P(b), 2, 100, 100, 10, P(ids), P(vals), P(ws), 1 << 20, None) == 0
     torch.cuda.synchronize()
+
+
+def test_ling_single_launch_f16_matches_two_launch_and_oracle():
+    """gb_ling_topk_f16 (one launch, the last chunk block merges) gives gb_glm_topk_f16's ids and values; its counters
+    reset themselves across calls of varying row counts on one workspace (crates/cuda/tests/ling_kda_proj_fused_ab.rs:
+    3404-3470 checks the same two properties); more than 64 rows is refused."""
+    need_gpu()
+    rng = np.random.default_rng(41)
+    ws = torch.zeros(S._lib.load().gb_ling_topk_f16_workspace_bytes(64, 151_936, 64), dtype=torch.uint8, device="cuda")
+    for rows, stride, valid, count in [(1, 151_936, 151_936, 64), (7, 32_768, 32_000, 40), (64, 151_936, 151_900, 50),
+                                       (3, 100, 97, 16), (33, 16_384, 16_384, 1), (64, 65_540, 65_540, 32), (2, 5, 5, 5)]:
+        bits = rng.integers(0, 1 << 16, rows * stride, dtype=np.uint64).astype(np.uint16)
+        bits[rng.choice(rows * stride, rows * stride // 50, replace=False)] = 0x3C00  # ties at 1.0
+        bits = bits.reshape(rows, stride)
+        bits[:, valid:] = 0x7C00  # +inf past valid: never read
+        t = dev(bits, torch.float16)
+        log(f"ling topk rows={rows} stride={stride} valid={valid} count={count}")
+        gi, gv = S.topk_f16_single_launch(t, count, valid=valid, workspace=ws)
+        wi, wv = S.topk(t, count, valid=valid)
+        gi, gv, wi, wv = host(gi), host(gv), host(wi), host(wv)
+        assert np.array_equal(gi, wi)
+        assert np.array_equal(gv.view(np.uint32), wv.view(np.uint32))
+        for r in range(0, rows, max(1, rows // 4)):
+            oi, ov = O.topk_row(bits[r, :valid], count, O.DTYPE_F16)
+            assert np.array_equal(gi[r], oi) and np.array_equal(gv[r].view(np.uint32), ov.view(np.uint32))
+    assert int(host(ws[:256]).astype(np.uint8).sum()) == 0  # every call left its counters at zero
+    big = dev(np.zeros((65, 64), dtype=np.uint16), torch.float16)
+    with pytest.raises(S._lib.GbsError):
+        S.topk_f16_single_launch(big, 8, workspace=torch.zeros(1 << 16, dtype=torch.uint8, device="cuda"))
