@@ -183,6 +183,21 @@ int gbs_accept_tree(const int* tokens, const int* parents, const int* samples, i
                     void* stream);
 
 /*
+ * A tree round committed on the device (crates/engine/src/lib.rs:2376-2410: every row keyed-sampled at its own
+ * position, then crates/spec/src/tree.rs:417-438's accept walk). logits [n_tree * nodes, stride] (f32 / bf16 / f16, as
+ * gbs_keyed_sample_rows; columns [0, valid)); params GbsKeyedRow[n_tree * nodes], row r's first_position = the
+ * position the engine samples that node at (the sequence's length plus the node's depth); tokens / parents i32
+ * [n_tree, nodes] as gbs_accept_tree. Outputs: out_samples i32 [n_tree * nodes] (the keyed samples, -1 for a failed
+ * row), out_path i32 [n_tree, nodes] and out_path_len i32 [n_tree] (as gbs_accept_tree), out_status i32 [n_tree] (the
+ * first failed row's status: a tree with a failed row has path_len 0 and an all -1 path, as the engine fails the
+ * sequence). n_tree * nodes <= 65535. The committed tokens are out_samples at the path's rows.
+ */
+size_t gbs_tree_verify_workspace_bytes(int n_tree, int nodes, int valid);
+int gbs_tree_verify(const void* logits, int dtype, int n_tree, int nodes, int stride, int valid, const GbsKeyedRow* params,
+                    const int* tokens, const int* parents, int* out_samples, int* out_path, int* out_path_len, int* out_status,
+                    void* ws, size_t ws_bytes, void* stream);
+
+/*
  * Extended sampling pipeline. logits [rows, stride] (dtype f32 or bf16, bf16 widened exactly), columns [0, vocab);
  * counts i32 [rows, vocab] (NULL = all zero); mask u32 [rows, ceil(vocab/32)] (bit i%32 of word i/32 set = token
  * allowed; NULL = all allowed); params GbsRowParams[rows]; uniforms f32 [rows], each in [0, 1).

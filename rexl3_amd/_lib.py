@@ -32,6 +32,8 @@ SIGNATURES = {
     "gbs_keyed_sample_rows": (I, [P, I, I, I, I, P, I, P, P, P, P, Z, P]),
     "gbs_accept": (I, [P, P, I, I, P, P]),
     "gbs_accept_tree": (I, [P, P, P, I, I, P, P, P]),
+    "gbs_tree_verify_workspace_bytes": (Z, [I, I, I]),
+    "gbs_tree_verify": (I, [P, I, I, I, I, I, P, P, P, P, P, P, P, P, Z, P]),
     "gbs_sample_workspace_bytes": (Z, [I, I, I]),
     "gbs_sample_rows": (I, [P, I, I, I, I, P, P, P, P, I, P, P, P, P, P, P, Z, P]),
     "gbs_spec_verify_workspace_bytes": (Z, [I, I, I]),

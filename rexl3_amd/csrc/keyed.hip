@@ -625,6 +625,48 @@ __global__ void accept_tree_k(const int* __restrict__ tokens, const int* __restr
     path_len[t] = len;
 }
 
+// accept_tree_k over trees whose rows were sampled on the device: a tree with a failed row (status != 0) gets that
+// status (its first failed row's), path_len 0 and an all -1 path, as the engine fails a sequence when any of its rows'
+// try_choose fails (crates/engine/src/lib.rs:2376-2404).
+__global__ void tree_commit_k(const int* __restrict__ tokens, const int* __restrict__ parents, const int* __restrict__ samples,
+                              const int* __restrict__ row_status, int n_tree, int nodes, int* path, int* path_len, int* status) {
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= n_tree) return;
+    int st = GBS_ROW_OK;
+    for (int r = 0; r < nodes && st == GBS_ROW_OK; ++r) st = row_status[(size_t)t * nodes + r];
+    if (status) status[t] = st;
+    if (st == GBS_ROW_OK) return;  // accept_tree_k, launched after this kernel, leaves the path of an OK tree
+    int* out = path + (size_t)t * nodes;
+    for (int i = 0; i < nodes; ++i) out[i] = -1;
+    path_len[t] = 0;
+}
+
+__global__ void accept_tree_ok_k(const int* __restrict__ tokens, const int* __restrict__ parents, const int* __restrict__ samples,
+                                 const int* __restrict__ status, int n_tree, int nodes, int* path, int* path_len) {
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= n_tree || status[t] != GBS_ROW_OK) return;
+    const int* tok = tokens + (size_t)t * nodes;
+    const int* par = parents + (size_t)t * nodes;
+    const int* smp = samples + (size_t)t * nodes;
+    int* out = path + (size_t)t * nodes;
+    int len = 0, cur = 0;
+    out[len++] = 0;
+    for (;;) {
+        const int sv = smp[cur];
+        int next = -1;
+        for (int r = cur + 1; r < nodes; ++r)
+            if (par[r] == cur && tok[r] == sv) {
+                next = r;
+                break;
+            }
+        if (next < 0) break;
+        out[len++] = next;
+        cur = next;
+    }
+    for (int i = len; i < nodes; ++i) out[i] = -1;
+    path_len[t] = len;
+}
+
 __global__ void clear_k(uint4* p, size_t n16, unsigned char* tail, size_t ntail) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     const size_t stride = (size_t)gridDim.x * blockDim.x;
@@ -725,6 +767,37 @@ GBS_EXPORT int gbs_accept_tree(const int* tokens, const int* parents, const int*
     if (!tokens || !parents || !samples || !path || !path_len) return GBS_ERR_INVALID;
     hipLaunchKernelGGL(accept_tree_k, dim3((n_tree + 63) / 64), dim3(64), 0, to_stream(stream), tokens, parents, samples, n_tree, nodes,
                        path, path_len);
+    return launch_status();
+}
+
+GBS_EXPORT size_t gbs_tree_verify_workspace_bytes(int n_tree, int nodes, int valid) {
+    if (n_tree <= 0 || nodes <= 0 || valid <= 0 || (long long)n_tree * nodes > 65535) return 0;
+    const int rows = n_tree * nodes;
+    return align256(keyed_ws_bytes(rows, valid)) + align256((size_t)rows * 4);
+}
+
+GBS_EXPORT int gbs_tree_verify(const void* logits, int dtype, int n_tree, int nodes, int stride, int valid, const GbsKeyedRow* params,
+                               const int* tokens, const int* parents, int* out_samples, int* out_path, int* out_path_len,
+                               int* out_status, void* ws, size_t ws_bytes, void* stream) {
+    if (n_tree < 0 || nodes < 1 || stride <= 0 || valid <= 0 || valid > stride) return GBS_ERR_INVALID;
+    if (n_tree == 0) return 0;
+    if ((long long)n_tree * nodes > 65535 || !tokens || !parents || !out_samples || !out_path || !out_path_len || !out_status ||
+        !ws || !aligned(ws, 256))
+        return GBS_ERR_INVALID;
+    const int rows = n_tree * nodes;
+    if (ws_bytes < gbs_tree_verify_workspace_bytes(n_tree, nodes, valid)) return GBS_ERR_INVALID;
+    const size_t kb = align256(keyed_ws_bytes(rows, valid));
+    int* row_status = (int*)((char*)ws + kb);
+    int rc = gbs_keyed_sample_rows(logits, dtype, rows, stride, valid, params, 0, out_samples, nullptr, row_status, ws, kb, stream);
+    if (rc) return rc;
+    // the trees' statuses (a tree is OK when all its rows are), then the accept walk of the OK trees
+    int* tst = out_status;
+    hipLaunchKernelGGL(tree_commit_k, dim3((n_tree + 63) / 64), dim3(64), 0, to_stream(stream), tokens, parents, out_samples, row_status,
+                       n_tree, nodes, out_path, out_path_len, tst);
+    rc = launch_status();
+    if (rc) return rc;
+    hipLaunchKernelGGL(accept_tree_ok_k, dim3((n_tree + 63) / 64), dim3(64), 0, to_stream(stream), tokens, parents, out_samples, tst,
+                       n_tree, nodes, out_path, out_path_len);
     return launch_status();
 }
 

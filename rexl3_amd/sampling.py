@@ -230,6 +230,31 @@ def accept_tree(tokens: torch.Tensor, parents: torch.Tensor, samples: torch.Tens
     return path, plen
 
 
+def tree_verify(logits: torch.Tensor, params: np.ndarray | torch.Tensor, tokens: torch.Tensor, parents: torch.Tensor,
+                valid: int | None = None):
+    """gbs_tree_verify: a speculative tree round committed on the device (crates/engine/src/lib.rs:2376-2410). logits
+    [n_tree * nodes, stride]; params KeyedRow per row with first_position = the node's position; tokens / parents
+    [n_tree, nodes]. Returns (samples [n_tree * nodes], path [n_tree, nodes], path_len [n_tree], status [n_tree])."""
+    _require_cuda(logits, "logits")
+    rows, stride = logits.shape
+    n_tree, nodes = tokens.shape
+    if rows != n_tree * nodes:
+        raise ValueError("tree_verify: logits rows != n_tree * nodes")
+    valid = stride if valid is None else valid
+    dev = logits.device
+    if isinstance(params, np.ndarray):
+        params = torch.from_numpy(np.ascontiguousarray(params, dtype=KEYED_ROW_DTYPE).view(np.uint8)).to(dev)
+    samples = torch.empty(rows, dtype=torch.int32, device=dev)
+    path = torch.empty((n_tree, nodes), dtype=torch.int32, device=dev)
+    plen = torch.empty(n_tree, dtype=torch.int32, device=dev)
+    st = torch.empty(n_tree, dtype=torch.int32, device=dev)
+    wsb = _lib.load().gbs_tree_verify_workspace_bytes(n_tree, nodes, valid)
+    ws = WORKSPACE.get(dev, "tree", wsb)
+    _lib.call("gbs_tree_verify", _ptr(logits), DTYPE_CODE[logits.dtype], n_tree, nodes, stride, valid, _ptr(params), _ptr(tokens),
+              _ptr(parents), _ptr(samples), _ptr(path), _ptr(plen), _ptr(st), _ptr(ws), ws.numel(), _stream(dev))
+    return samples, path, plen, st
+
+
 # ------------------------------------------------------------------------------------------------ extended pipeline
 
 def row_params(rows: int, temperature=1.0, top_p=1.0, min_p=0.0, repetition=1.0, presence=0.0, frequency=0.0,

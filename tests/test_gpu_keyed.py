@@ -252,3 +252,50 @@ def test_fused_keyed_full_batches(dtype, rows, stride, valid):
     assert np.array_equal(gs, ws)
     assert np.array_equal(gi, wi), np.nonzero(gi != wi)[0][:10]
     assert np.array_equal(gv.view(np.uint32), wv.view(np.uint32))
+
+
+def test_tree_verify_on_device():
+    """A tree round on the device: every node keyed-sampled at its own position (base + depth), then the accept walk;
+    against the oracle's top-(k+8) + try_choose per row and accept_tree. Siblings share their depth's position; trees
+    are built so that some drafts match the samples (long paths) and one tree holds a NaN row (a failed sequence)."""
+    need_gpu()
+    rng = np.random.default_rng(5)
+    n_tree, nodes, vocab = 40, 15, 32_000
+    rows = n_tree * nodes
+    x = W.peaked_logits(77, rows, vocab, 2.0, (1, 3), 9.0, 14.0)  # few, high peaks: samples are predictable
+    parents = np.zeros((n_tree, nodes), dtype=np.int32)
+    depth = np.zeros((n_tree, nodes), dtype=np.int64)
+    for t in range(n_tree):
+        parents[t, 0] = -1
+        for r in range(1, nodes):
+            parents[t, r] = rng.integers(0, r)
+            depth[t, r] = depth[t, parents[t, r]] + 1
+    recs = np.zeros(rows, dtype=S.KEYED_ROW_DTYPE)
+    base = rng.integers(100, 5000, n_tree)
+    for t in range(n_tree):
+        for r in range(nodes):
+            recs[t * nodes + r] = (1234 + t, int(base[t] + depth[t, r]), [0.0, 0.7, 1.0][t % 3], 0.9, 0.0, 20, 1)
+    # the oracle's samples, then tokens that follow them on some branches (so that paths go deep)
+    wi, _, ws = O.keyed_sample_rows(x, O.DTYPE_F32, vocab, recs, 0)
+    tokens = rng.integers(0, vocab, (n_tree, nodes)).astype(np.int32)
+    for t in range(n_tree):
+        for r in range(1, nodes):
+            if rng.random() < 0.6:
+                tokens[t, r] = wi[t * nodes + parents[t, r]]
+    x[5 * nodes + 3, 17] = np.nan  # tree 5: row 3 has a NaN ... made a candidate below
+    x[5 * nodes + 3, :] = np.nan
+    wi, _, ws = O.keyed_sample_rows(x, O.DTYPE_F32, vocab, recs, 0)
+    smp, path, plen, st = S.tree_verify(dev(x), recs, dev(tokens), dev(parents))
+    smp, path, plen, st = host(smp), host(path), host(plen), host(st)
+    assert np.array_equal(smp, wi)
+    deep = 0
+    for t in range(n_tree):
+        rs = ws[t * nodes:(t + 1) * nodes]
+        bad = rs[rs != 0]
+        if bad.size:
+            assert st[t] == bad[0] and plen[t] == 0 and (path[t] == -1).all()
+            continue
+        want = O.accept_tree(tokens[t], parents[t], wi[t * nodes:(t + 1) * nodes])
+        assert st[t] == 0 and list(path[t, :plen[t]]) == want and (path[t, plen[t]:] == -1).all()
+        deep += len(want) > 2
+    assert st[5] == 2 and deep > 5
