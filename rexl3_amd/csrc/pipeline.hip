@@ -88,7 +88,9 @@ int fast_splits(int rows, int vocab) {
 // depend only on the row (room for 65535 rows whatever this launch's row count); every launch leaves them zero. The
 // partial results after them are written before they are read. So a workspace cleared once serves launches of any
 // shape.
-constexpr size_t CTL_BYTES = (size_t)65536 * 4;
+// The full-distribution path (kmax 0) keeps three counters per row in the same region (three quarters of it), so one
+// workspace also serves launches that alternate between the two paths.
+constexpr size_t CTL_BYTES = (size_t)3 * 65536 * 4;
 
 struct FastWs {
     unsigned* arrive;  // [rows] the row's blocks that have handed over their partials
@@ -678,7 +680,7 @@ void dispatch_flags(bool c, bool m, bool lp, F&& f) {
 
 GBS_EXPORT size_t gbs_sample_workspace_bytes(int rows, int vocab, int kmax) {
     if (rows <= 0 || vocab <= 0 || vocab > GBS_MAX_VOCAB || kmax < 0 || kmax > GBS_MAX_COUNT) return 0;
-    if (kmax == 0) return 256;  // the full-distribution path keeps its state in LDS
+    if (kmax == 0) return sample_full_workspace_bytes(rows, vocab);
     return CTL_BYTES + fast_part_bytes(rows, fast_splits(rows, vocab));
 }
 
@@ -689,9 +691,11 @@ GBS_EXPORT int gbs_sample_rows(const void* logits, int dtype, int rows, int stri
     if (dtype != GBS_DTYPE_F32 && dtype != GBS_DTYPE_BF16) return GBS_ERR_INVALID;
     if (rows == 0) return 0;
     if (rows > 65535 || !logits || !params || !uniforms || !out_ids) return GBS_ERR_INVALID;
-    if (kmax == 0)
+    if (kmax == 0) {
+        if (ws_bytes < sample_full_workspace_bytes(rows, vocab)) return GBS_ERR_INVALID;
         return launch_sample_full(logits, dtype, rows, stride, vocab, counts, mask, params, uniforms, out_ids, out_greedy, out_probs,
-                                  out_logprobs, out_status, stream);
+                                  out_logprobs, out_status, ws, ws_bytes, stream);
+    }
     if (!ws || !aligned(ws, 256)) return GBS_ERR_INVALID;
     const int S = fast_splits(rows, vocab);
     if (ws_bytes < gbs_sample_workspace_bytes(rows, vocab, kmax)) return GBS_ERR_INVALID;

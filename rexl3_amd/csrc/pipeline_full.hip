@@ -18,6 +18,9 @@ using namespace gbs::modeu;
 
 namespace {
 
+#ifndef GBS_EXP_NOATOM
+#define GBS_EXP_NOATOM 0
+#endif
 #ifndef GBS_EXP_FULLT
 #define GBS_EXP_FULLT 0
 #endif
@@ -131,11 +134,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t full_rsrc(const void* base, u3
 // block barriers. Rows that allow 16-byte loads keep the loads of DEPTH tiles in flight.
 constexpr int DEPTH = 4;
 template <int DT, bool COUNTS, bool MASK, class F>
-__device__ __forceinline__ void stream_tiles(const Row<DT, COUNTS, MASK>& R, F&& f) {
+__device__ __forceinline__ void stream_tiles(const Row<DT, COUNTS, MASK>& R, int t0, int t1, F&& f) {
     const int tid = threadIdx.x;
-    const int ntiles = (R.vocab + TILE - 1) / TILE;
     if (!R.vec || R.vocab % 4 != 0) {  // the buffer loads below read whole 4-element groups
-        for (int t = 0; t < ntiles; ++t) {
+        for (int t = t0; t < t1; ++t) {
             const int e = t * TILE + tid * 4;
             float l[4];
             R.group(e, l);
@@ -150,20 +152,26 @@ __device__ __forceinline__ void stream_tiles(const Row<DT, COUNTS, MASK>& R, F&&
     typename Row<DT, COUNTS, MASK>::Raw buf[DEPTH];
 #pragma unroll
     for (int k = 0; k < DEPTH; ++k)
-        if (k < ntiles) R.load_raw(k * TILE + tid * 4, rx, rc, rm, buf[k]);
-    for (int t0 = 0; t0 < ntiles; t0 += DEPTH) {
+        if (t0 + k < t1) R.load_raw((t0 + k) * TILE + tid * 4, rx, rc, rm, buf[k]);
+    for (int tb = t0; tb < t1; tb += DEPTH) {
 #pragma unroll
         for (int k = 0; k < DEPTH; ++k) {
-            const int t = t0 + k;
-            if (t < ntiles) {
+            const int t = tb + k;
+            if (t < t1) {
                 const int e = t * TILE + tid * 4;
                 float l[4];
                 R.from_raw(buf[k], e, l);
-                if (t + DEPTH < ntiles) R.load_raw(e + DEPTH * TILE, rx, rc, rm, buf[k]);
+                if (t + DEPTH < t1) R.load_raw(e + DEPTH * TILE, rx, rc, rm, buf[k]);
                 f(t, e, l);
             }
         }
     }
+}
+
+// the whole row
+template <int DT, bool COUNTS, bool MASK, class F>
+__device__ __forceinline__ void stream_tiles(const Row<DT, COUNTS, MASK>& R, F&& f) {
+    stream_tiles(R, 0, (R.vocab + TILE - 1) / TILE, f);
 }
 
 template <typename T>
@@ -213,6 +221,17 @@ struct Shared {
     float lse_m[NWF], lse_s[NWF];
     u64 bc[8];  // broadcast slots
     u32 ncol;   // tokens collected by the binned cut
+};
+
+// The split path's per-row record (see fs_pass0_k): state FS_CUT (the binned cut continues), FS_DONE (the row's results
+// are written), FS_RADIX (the single-block kernel takes the row).
+enum : u32 { FS_CUT = 0, FS_DONE = 1, FS_RADIX = 2 };
+
+struct FsRow {
+    u64 top;  // the maximum's key
+    float lse_m, lse_s;
+    u32 nallowed, state, bstar, pad;
+    u64 above, P;
 };
 
 // One radix selection over the keys >= lb of the row: the key K at which the descending cumulative weight (count when
@@ -331,13 +350,23 @@ __device__ bool binned_cut(const Row<DT, COUNTS, MASK>& R, float M, float c2, fl
     if (topp) {
         for (int i = tid; i < NBINS; i += NTF) sh.mass[i] = 0;
         __syncthreads();
+#if GBS_EXP_NOATOM
+        u64 fake = 0;
+#endif
         stream_tiles(R, [&](int, int, const float (&lv)[4]) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const u64 E = mass_fast(lv[q], M, c2);
+#if GBS_EXP_NOATOM
+                fake += E + bin_of(lv[q], M, c2);
+#else
                 if (E) atomicAdd((unsigned long long*)&sh.mass[bin_of(lv[q], M, c2)], (unsigned long long)E);
+#endif
             }
         });
+#if GBS_EXP_NOATOM
+        if (fake == 12345) sh.mass[0] = fake;
+#endif
         __syncthreads();
         if (tid < WAVE) {
             // lane i owns bins [32 i, 32 i + 32): the total, P, then the bin where the cumulative mass reaches P
@@ -421,6 +450,8 @@ __device__ bool binned_cut(const Row<DT, COUNTS, MASK>& R, float M, float c2, fl
     if (topp) {
         // For each collected token i, G_i = the mass of the collected tokens with larger keys (every thread reads the
         // same key at once: LDS broadcasts). The top-p key is the one token with above + G_i < P <= above + G_i + E_i.
+        if (tid == 0) sh.bc[3] = kp;
+        __syncthreads();
         for (u32 i = tid; i < n; i += NTF) {
             const u64 ki = sh.maxk[i];
             u64 g = 0;
@@ -447,9 +478,12 @@ __global__ void __launch_bounds__(NTF) sample_full_k(const void* __restrict__ lo
                                                      const int* __restrict__ counts, const u32* __restrict__ mask,
                                                      const RowParamsDev* __restrict__ params, const float* __restrict__ uniforms, bool vec,
                                                      int* __restrict__ out_ids, int* __restrict__ out_greedy, float* __restrict__ out_probs,
-                                                     float* __restrict__ out_logprobs, int* __restrict__ out_status) {
+                                                     float* __restrict__ out_logprobs, int* __restrict__ out_status,
+                                                     const FsRow* __restrict__ only_radix) {
     __shared__ Shared sh;
     const int r = blockIdx.x;
+    // after the split path: only the rows it handed to the radix path
+    if (only_radix && ld_agent(&only_radix[r].state) != FS_RADIX) return;
     const int tid = threadIdx.x, w = tid / WAVE, l = lane_id();
     const RowParamsDev p = params[r];
     const float u = uniforms[r];
@@ -628,6 +662,482 @@ __global__ void __launch_bounds__(NTF) sample_full_k(const void* __restrict__ lo
     FT(5);
 }
 
+// ================================================================================================== the split path
+// Batches with fewer rows than CUs: S blocks per row, block sp over whole tiles [sp * tpb, (sp + 1) * tpb). Three
+// launches, each with a last-block hand-off per row (agent-scope stores and loads, an arrival counter):
+//   fs_pass0_k    maximum, NaN flag, allowed count, LSE; the row's last block finishes every row that needs no cut (an
+//                 invalid, NaN or empty row, T = 0) and marks the rows that need the radix path (top-k with a cut,
+//                 an infinite maximum or 1/T)
+//   fs_hist_k     the binned cut's mass histogram (rows with top-p); the last block sums the blocks' histograms and
+//                 finds the crossing bin
+//   fs_collect_k  kept masses per tile and the crossing bin's tokens; the last block finds the exact top-p key, the
+//                 tile that holds the draw, and the token
+// then sample_full_k for the rows marked for the radix path (and rows whose crossing bin held more than CAP tokens).
+constexpr int FS_TARGET_BLOCKS = 256;
+constexpr int FS_MAX_SPLITS = 128;
+
+
+struct FsPart0 {
+    u64 key;
+    u32 nan, nallowed;
+    float m, s;
+    u32 pad[2];
+};
+
+struct FsWs {
+    unsigned *cnt0, *cnt1, *cnt2;  // per-row arrival counters, at fixed offsets (zero between launches)
+    FsRow* rows;                   // [rows]
+    FsPart0* p0;                   // [rows][S]
+    u64* hist;                     // [rows][S][NBINS]
+    u64 *ckey, *cmass;             // [rows][S][CAP]
+    u32* ccount;                   // [rows][S]
+    u64* tiles;                    // [rows][ntiles]
+};
+
+constexpr size_t FS_CTL = (size_t)3 * 65536 * 4;  // the same control region as the fast path's (pipeline.hip)
+
+size_t fs_align(size_t b) { return (b + 255) & ~(size_t)255; }
+
+struct FsPlan {
+    int S, tpb, ntiles;
+    size_t bytes;
+};
+
+FsPlan fs_plan(int rows, int vocab) {
+    FsPlan p;
+    p.ntiles = (vocab + TILE - 1) / TILE;
+    int want = (FS_TARGET_BLOCKS + rows - 1) / rows;
+    if (want > p.ntiles) want = p.ntiles;
+    if (want > FS_MAX_SPLITS) want = FS_MAX_SPLITS;
+    if (want < 1) want = 1;
+    p.tpb = (p.ntiles + want - 1) / want;
+    p.S = (p.ntiles + p.tpb - 1) / p.tpb;
+    const size_t rs = (size_t)rows * p.S;
+    p.bytes = FS_CTL + fs_align((size_t)rows * sizeof(FsRow)) + fs_align(rs * sizeof(FsPart0)) + fs_align(rs * NBINS * 8) +
+              2 * fs_align(rs * CAP * 8) + fs_align(rs * 4) + fs_align((size_t)rows * p.ntiles * 8);
+    return p;
+}
+
+FsWs fs_carve(void* ws, int rows, const FsPlan& p) {
+    char* c = (char*)ws;
+    FsWs w;
+    w.cnt0 = (unsigned*)c;
+    w.cnt1 = w.cnt0 + 65536;
+    w.cnt2 = w.cnt1 + 65536;
+    c += FS_CTL;
+    const size_t rs = (size_t)rows * p.S;
+    w.rows = (FsRow*)c; c += fs_align((size_t)rows * sizeof(FsRow));
+    w.p0 = (FsPart0*)c; c += fs_align(rs * sizeof(FsPart0));
+    w.hist = (u64*)c; c += fs_align(rs * NBINS * 8);
+    w.ckey = (u64*)c; c += fs_align(rs * CAP * 8);
+    w.cmass = (u64*)c; c += fs_align(rs * CAP * 8);
+    w.ccount = (u32*)c; c += fs_align(rs * 4);
+    w.tiles = (u64*)c;
+    return w;
+}
+
+template <int DT, bool COUNTS, bool MASK>
+__device__ __forceinline__ Row<DT, COUNTS, MASK> make_row(const void* logits, long long stride, int vocab, const int* counts,
+                                                          const u32* mask, const RowParamsDev& p, bool vec, int r) {
+    Row<DT, COUNTS, MASK> R;
+    R.x = (const char*)logits + (size_t)r * (size_t)stride * (DT == GBS_DTYPE_F32 ? 4 : 2);
+    R.c = COUNTS ? counts + (size_t)r * vocab : nullptr;
+    R.m = MASK ? mask + (size_t)r * ((vocab + 31) / 32) : nullptr;
+    R.vocab = vocab;
+    R.vec = vec;
+    R.rinv = 1.0f / p.repetition;
+    R.rep = p.repetition;
+    R.freq = p.frequency;
+    R.pres = p.presence;
+    return R;
+}
+
+__device__ __forceinline__ void fs_out(int r, int id, int greedy, int status, float prob, float lp, int* out_ids, int* out_greedy,
+                                       float* out_probs, float* out_logprobs, int* out_status) {
+    out_ids[r] = status == GBS_ROW_OK ? id : -1;
+    if (out_greedy) out_greedy[r] = status == GBS_ROW_OK ? greedy : -1;
+    if (out_probs) out_probs[r] = status == GBS_ROW_OK ? prob : 0.f;
+    if (out_logprobs) out_logprobs[r] = status == GBS_ROW_OK ? lp : __uint_as_float(0x7fc00000u);
+    if (out_status) out_status[r] = status;
+}
+
+__device__ __forceinline__ float fs_logprob(float lx, float M, float clp, float lse_m, float lse_s) {
+    if (isinf(M) || !isfinite(clp)) return __uint_as_float(0x7fc00000u);  // undefined: +inf maximum, 1/T beyond f32
+    return ((lx - lse_m) * clp - log2f(lse_s)) * 0.6931471805599453f;
+}
+
+__device__ __forceinline__ float fs_clp(const RowParamsDev& p) {
+    return p.temperature > 0.0f ? temp_scale(p.temperature) : 1.44269504088896340736f;
+}
+
+template <int DT, bool COUNTS, bool MASK>
+__global__ void __launch_bounds__(NTF) fs_pass0_k(const void* __restrict__ logits, long long stride, int vocab,
+                                                  const int* __restrict__ counts, const u32* __restrict__ mask,
+                                                  const RowParamsDev* __restrict__ params, const float* __restrict__ uniforms, bool vec,
+                                                  int tpb, FsWs ws, int* __restrict__ out_ids, int* __restrict__ out_greedy,
+                                                  float* __restrict__ out_probs, float* __restrict__ out_logprobs,
+                                                  int* __restrict__ out_status) {
+    __shared__ u64 s_red[NWF];
+    __shared__ float s_lm[NWF], s_ls[NWF];
+    __shared__ unsigned s_flag;
+    const int S = gridDim.x, sp = blockIdx.x, r = blockIdx.y;
+    const int tid = threadIdx.x, w = tid / WAVE, l = lane_id();
+    const RowParamsDev p = params[r];
+    const float u = uniforms[r];
+    if (params_invalid(p, u)) {  // every block of the row returns; the first writes the row's results
+        if (sp == 0 && tid == 0) {
+            fs_out(r, -1, -1, GBS_ROW_INVALID_PARAMS, 0.f, 0.f, out_ids, out_greedy, out_probs, out_logprobs, out_status);
+            st_agent(&ws.rows[r].state, (u32)FS_DONE);
+        }
+        return;
+    }
+    const Row<DT, COUNTS, MASK> R = make_row<DT, COUNTS, MASK>(logits, stride, vocab, counts, mask, p, vec, r);
+    const float clp = fs_clp(p);
+    const int ntiles = (vocab + TILE - 1) / TILE;
+    const int t0 = sp * tpb, t1 = min(ntiles, t0 + tpb);
+    u64 kmaxv = 0;
+    u32 nan = 0, nallowed = 0;
+    Lse lse{-INFINITY, 0.f};
+    stream_tiles(R, t0, t1, [&](int, int e, const float (&lv)[4]) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            nan |= lv[q] != lv[q];
+            if (valid_l(lv[q])) {
+                ++nallowed;
+                const u64 k = make_key(okey_f32(lv[q]), (u32)(e + q));
+                kmaxv = k > kmaxv ? k : kmaxv;
+                if (lv[q] > lse.m) {
+                    lse.s = lse.m == -INFINITY ? 0.f : lse.s * exp2f((lse.m - lv[q]) * clp);
+                    lse.m = lv[q];
+                }
+                lse.s += exp2f((lv[q] - lse.m) * clp);
+            }
+        }
+    });
+    for (int m = 1; m < WAVE; m <<= 1) {
+        const Lse o{__shfl_xor(lse.m, m, WAVE), __shfl_xor(lse.s, m, WAVE)};
+        lse = lse_merge(lse, o, clp);
+    }
+    if (l == 0) {
+        s_lm[w] = lse.m;
+        s_ls[w] = lse.s;
+    }
+    const u32 nan_any = (u32)block_sum((u64)nan, s_red);
+    const u64 nall = block_sum((u64)nallowed, s_red);
+    const u64 top = block_max_u64(kmaxv, s_red);
+    if (tid == 0) {
+        Lse b{-INFINITY, 0.f};
+        for (int o = 0; o < NWF; ++o) b = lse_merge(b, Lse{s_lm[o], s_ls[o]}, clp);
+        FsPart0* pp = &ws.p0[(size_t)r * S + sp];
+        st_agent(&pp->key, top);
+        st_agent(&pp->nan, nan_any);
+        st_agent(&pp->nallowed, (u32)nall);
+        st_agent((u32*)&pp->m, __float_as_uint(b.m));
+        st_agent((u32*)&pp->s, __float_as_uint(b.s));
+    }
+    if (!arrive_last(&ws.cnt0[r], (unsigned)S, &s_flag)) return;
+    // the row: the blocks' partials (one per thread), reduced
+    u64 k = 0, na = 0, nn = 0;
+    Lse rl{-INFINITY, 0.f};
+    if (tid < S) {
+        const FsPart0* pp = &ws.p0[(size_t)r * S + tid];
+        k = ld_agent(&pp->key);
+        nn = ld_agent(&pp->nan);
+        na = ld_agent(&pp->nallowed);
+        rl = Lse{__uint_as_float(ld_agent((const u32*)&pp->m)), __uint_as_float(ld_agent((const u32*)&pp->s))};
+    }
+    if (w == 0) {  // S <= 128: lanes hold two partials at most
+        if (tid + WAVE < S) {
+            const FsPart0* pp = &ws.p0[(size_t)r * S + tid + WAVE];
+            const u64 k2 = ld_agent(&pp->key);
+            k = k2 > k ? k2 : k;
+            nn += ld_agent(&pp->nan);
+            na += ld_agent(&pp->nallowed);
+            rl = lse_merge(rl, Lse{__uint_as_float(ld_agent((const u32*)&pp->m)), __uint_as_float(ld_agent((const u32*)&pp->s))}, clp);
+        }
+        for (int m = 1; m < WAVE; m <<= 1) {
+            const u64 ko = shfl_xor64(k, m);
+            k = ko > k ? ko : k;
+            nn += shfl_xor64(nn, m);
+            na += shfl_xor64(na, m);
+            const Lse o{__shfl_xor(rl.m, m, WAVE), __shfl_xor(rl.s, m, WAVE)};
+            rl = lse_merge(rl, o, clp);
+        }
+    }
+    if (tid != 0) return;
+    FsRow* row = &ws.rows[r];
+    u32 state = FS_CUT;
+    const float M = okey_to_f32(key_ok(k));
+    const int greedy = (int)key_id(k);
+    if (nn) {
+        fs_out(r, -1, -1, GBS_ROW_NAN_LOGIT, 0.f, 0.f, out_ids, out_greedy, out_probs, out_logprobs, out_status);
+        state = FS_DONE;
+    } else if (na == 0) {
+        fs_out(r, -1, -1, GBS_ROW_NO_CANDIDATES, 0.f, 0.f, out_ids, out_greedy, out_probs, out_logprobs, out_status);
+        state = FS_DONE;
+    } else if (p.temperature == 0.0f) {
+        fs_out(r, greedy, greedy, GBS_ROW_OK, 1.0f, fs_logprob(M, M, clp, rl.m, rl.s), out_ids, out_greedy, out_probs, out_logprobs,
+               out_status);
+        state = FS_DONE;
+    } else {
+        const bool topk_on = p.top_k > 0 && (u64)p.top_k < na;
+        if (topk_on || !mass_fast_ok(M, temp_scale(p.temperature))) state = FS_RADIX;
+    }
+    st_agent(&row->top, k);
+    st_agent((u32*)&row->lse_m, __float_as_uint(rl.m));
+    st_agent((u32*)&row->lse_s, __float_as_uint(rl.s));
+    st_agent(&row->nallowed, (u32)na);
+    st_agent(&row->bstar, (u32)NBINS);
+    st_agent(&row->above, (u64)0);
+    st_agent(&row->P, (u64)0);
+    st_agent(&row->state, state);
+}
+
+template <int DT, bool COUNTS, bool MASK>
+__global__ void __launch_bounds__(NTF) fs_hist_k(const void* __restrict__ logits, long long stride, int vocab,
+                                                 const int* __restrict__ counts, const u32* __restrict__ mask,
+                                                 const RowParamsDev* __restrict__ params, bool vec, int tpb, FsWs ws) {
+    __shared__ u64 s_hist[NBINS];
+    __shared__ unsigned s_flag;
+    const int S = gridDim.x, sp = blockIdx.x, r = blockIdx.y;
+    const int tid = threadIdx.x, l = lane_id();
+    const RowParamsDev p = params[r];
+    if (!(p.top_p > 0.0f && p.top_p < 1.0f)) return;  // no top-p: no histogram
+    if (ld_agent(&ws.rows[r].state) != FS_CUT) return;
+    const Row<DT, COUNTS, MASK> R = make_row<DT, COUNTS, MASK>(logits, stride, vocab, counts, mask, p, vec, r);
+    const float M = okey_to_f32(key_ok(ld_agent(&ws.rows[r].top)));
+    const float c2 = temp_scale(p.temperature);
+    const int ntiles = (vocab + TILE - 1) / TILE;
+    const int t0 = sp * tpb, t1 = min(ntiles, t0 + tpb);
+    for (int i = tid; i < NBINS; i += NTF) s_hist[i] = 0;
+    __syncthreads();
+    stream_tiles(R, t0, t1, [&](int, int, const float (&lv)[4]) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const u64 E = mass_fast(lv[q], M, c2);
+            if (E) atomicAdd((unsigned long long*)&s_hist[bin_of(lv[q], M, c2)], (unsigned long long)E);
+        }
+    });
+    __syncthreads();
+    u64* mine = ws.hist + ((size_t)r * S + sp) * NBINS;
+    for (int i = tid; i < NBINS; i += NTF) st_agent(&mine[i], s_hist[i]);
+    if (!arrive_last(&ws.cnt1[r], (unsigned)S, &s_flag)) return;
+    // the row's histogram: the blocks' histograms summed bin by bin
+    const u64* all = ws.hist + (size_t)r * S * NBINS;
+    for (int i = tid; i < NBINS; i += NTF) {
+        u64 v = 0;
+        for (int o = 0; o < S; ++o) v += ld_agent(&all[(size_t)o * NBINS + i]);
+        s_hist[i] = v;
+    }
+    __syncthreads();
+    if (tid < WAVE) {
+        // lane i owns bins [PB i, PB i + PB): the total, P, then the bin where the cumulative mass reaches P
+        constexpr int PB = NBINS / WAVE;
+        u64 s = 0;
+        for (int k = 0; k < PB; ++k) s += s_hist[l * PB + k];
+        const u64 Z = wave_sum_u64(s);
+        const u64 Pv = mul_ceil64(p.top_p, Z);
+        const u64 incl = wave_scan_u64(s);
+        const u64 hit = ballot(incl >= Pv);
+        const int f = (int)__builtin_ctzll(hit);
+        if (l == f) {
+            u64 acc = incl - s;
+            int b = l * PB;
+            for (int k = 0; k < PB; ++k) {
+                b = l * PB + k;
+                if (acc + s_hist[b] >= Pv) break;
+                acc += s_hist[b];
+            }
+            FsRow* row = &ws.rows[r];
+            st_agent(&row->bstar, (u32)b);
+            st_agent(&row->above, acc);
+            st_agent(&row->P, Pv);
+        }
+    }
+}
+
+template <int DT, bool COUNTS, bool MASK>
+__global__ void __launch_bounds__(NTF) fs_collect_k(const void* __restrict__ logits, long long stride, int vocab,
+                                                    const int* __restrict__ counts, const u32* __restrict__ mask,
+                                                    const RowParamsDev* __restrict__ params, const float* __restrict__ uniforms,
+                                                    bool vec, int tpb, FsWs ws, int* __restrict__ out_ids, int* __restrict__ out_greedy,
+                                                    float* __restrict__ out_probs, float* __restrict__ out_logprobs,
+                                                    int* __restrict__ out_status) {
+    __shared__ u64 s_key[CAP], s_mass[CAP];
+    __shared__ u64 s_tilew[MAX_TILES][NWF];
+    __shared__ u64 s_tile[MAX_TILES];
+    __shared__ u64 s_red[NWF];
+    __shared__ u64 s_bc[4];
+    __shared__ u32 s_ncol, s_off[FS_MAX_SPLITS + 1];
+    __shared__ unsigned s_flag;
+    const int S = gridDim.x, sp = blockIdx.x, r = blockIdx.y;
+    const int tid = threadIdx.x, w = tid / WAVE, l = lane_id();
+    const RowParamsDev p = params[r];
+    const FsRow* row = &ws.rows[r];
+    if (ld_agent(&row->state) != FS_CUT) return;
+    const Row<DT, COUNTS, MASK> R = make_row<DT, COUNTS, MASK>(logits, stride, vocab, counts, mask, p, vec, r);
+    const u64 top = ld_agent(&row->top);
+    const float M = okey_to_f32(key_ok(top));
+    const float c2 = temp_scale(p.temperature);
+    const bool topp = p.top_p > 0.0f && p.top_p < 1.0f;
+    const u32 bstar = ld_agent(&row->bstar);
+    const u64 Q = p.min_p > 0.0f ? mul_ceil64(p.min_p, MASS_ONE) : 0ull;
+    const int ntiles = (vocab + TILE - 1) / TILE;
+    const int t0 = sp * tpb, t1 = min(ntiles, t0 + tpb);
+    if (tid == 0) s_ncol = 0;
+    __syncthreads();
+    // kept masses of the bins above b* per tile (per-wave partials); the tokens of bin b* into LDS
+    stream_tiles(R, t0, t1, [&](int t, int e, const float (&lv)[4]) {
+        u64 s = 0;
+        u64 Eq[4];
+        bool col[4];
+        int ncol = 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            Eq[q] = mass_fast(lv[q], M, c2);
+            const u32 b = topp ? bin_of(lv[q], M, c2) : 0u;
+            const bool ok = valid_l(lv[q]);
+            if (ok && b < bstar && Eq[q] >= Q) s += Eq[q];
+            col[q] = ok && b == bstar;
+            ncol += col[q] ? 1 : 0;
+        }
+        if (ballot(ncol > 0)) {
+            const u64 inc = wave_scan_u64((u64)ncol);
+            u32 base = 0;
+            if (l == WAVE - 1) base = atomicAdd(&s_ncol, (u32)inc);
+            base = (u32)__builtin_amdgcn_readlane((int)base, WAVE - 1);
+            u32 idx = base + (u32)(inc - (u64)ncol);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                if (col[q]) {
+                    if (idx < (u32)CAP) {
+                        s_key[idx] = make_key(okey_f32(lv[q]), (u32)(e + q));
+                        s_mass[idx] = Eq[q];
+                    }
+                    ++idx;
+                }
+            }
+        }
+        s = wave_sum_u64(s);
+        if (l == 0) s_tilew[t - t0][w] = s;
+    });
+    __syncthreads();
+    for (int t = t0 + tid; t < t1; t += NTF) {
+        u64 v = 0;
+#pragma unroll
+        for (int k = 0; k < NWF; ++k) v += s_tilew[t - t0][k];
+        st_agent(&ws.tiles[(size_t)r * ntiles + t], v);
+    }
+    const u32 nb = s_ncol;
+    const size_t slot = (size_t)r * S + sp;
+    if (tid == 0) st_agent(&ws.ccount[slot], nb);
+    for (u32 i = tid; i < nb && i < (u32)CAP; i += NTF) {
+        st_agent(&ws.ckey[slot * CAP + i], s_key[i]);
+        st_agent(&ws.cmass[slot * CAP + i], s_mass[i]);
+    }
+    if (!arrive_last(&ws.cnt2[r], (unsigned)S, &s_flag)) return;
+    // ---- the row's last block: gather the collected tokens (or hand the row to the radix path)
+    if (tid == 0) {
+        u32 off = 0;
+        for (int o = 0; o < S; ++o) {
+            s_off[o] = off;
+            off += ld_agent(&ws.ccount[(size_t)r * S + o]);
+        }
+        s_off[S] = off;
+    }
+    __syncthreads();
+    const u32 n = s_off[S];
+    if (n > (u32)CAP) {  // every block's count is at most the total: no block overflowed unless the total did
+        if (tid == 0) st_agent(&ws.rows[r].state, (u32)FS_RADIX);
+        return;
+    }
+    for (int o = 0; o < S; ++o) {
+        const u32 cnt = s_off[o + 1] - s_off[o];
+        for (u32 i = tid; i < cnt; i += NTF) {
+            s_key[s_off[o] + i] = ld_agent(&ws.ckey[((size_t)r * S + o) * CAP + i]);
+            s_mass[s_off[o] + i] = ld_agent(&ws.cmass[((size_t)r * S + o) * CAP + i]);
+        }
+    }
+    for (int t = tid; t < ntiles; t += NTF) s_tile[t] = ld_agent(&ws.tiles[(size_t)r * ntiles + t]);
+    __syncthreads();
+    u64 kp = (u64)VALID_MIN_OK << 32;  // every valid key
+    if (topp) {
+        // the collected token with above + G < P <= above + G + E, G the mass of the collected tokens with larger keys
+        const u64 above = ld_agent(&row->above), P = ld_agent(&row->P);
+        if (tid == 0) s_bc[0] = kp;
+        __syncthreads();
+        for (u32 i = tid; i < n; i += NTF) {
+            const u64 ki = s_key[i];
+            u64 g = 0;
+            for (u32 j = 0; j < n; ++j) g += s_key[j] > ki ? s_mass[j] : 0ull;
+            const u64 lo = above + g;
+            if (lo < P && P <= lo + s_mass[i]) s_bc[0] = ki;
+        }
+        __syncthreads();
+        kp = s_bc[0];
+        for (u32 j = tid; j < n; j += NTF) {
+            const u64 E = s_mass[j];
+            if (s_key[j] >= kp && E >= Q) atomicAdd((unsigned long long*)&s_tile[key_id(s_key[j]) / TILE], (unsigned long long)E);
+        }
+        __syncthreads();
+    }
+    // ---- the draw: the tile that holds t, then its token (thread sums, a block scan, the owning thread's 4 elements)
+    u64 z = 0;
+    for (int t = 0; t < ntiles; ++t) z += s_tile[t];
+    const float u = uniforms[r];
+    const u64 target = (u64)mul_floor(u, (u128)z, nullptr);
+    int tsel = ntiles - 1;
+    u64 before = 0;
+    for (int t = 0; t < ntiles; ++t) {
+        if (before + s_tile[t] > target) {
+            tsel = t;
+            break;
+        }
+        before += s_tile[t];
+    }
+    auto kept_mass = [&](float v, int i) -> u64 {
+        if (!valid_l(v)) return 0ull;
+        if (make_key(okey_f32(v), (u32)i) < kp) return 0ull;
+        const u64 E = mass(v, M, c2);
+        return E >= Q ? E : 0ull;
+    };
+    const int e = tsel * TILE + tid * 4;
+    float lv[4];
+    R.group(e, lv);
+    u64 em[4], mine = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        em[q] = kept_mass(lv[q], e + q);
+        mine += em[q];
+    }
+    const u64 incl = wave_scan_u64(mine);
+    if (l == WAVE - 1) s_red[w] = incl;
+    __syncthreads();
+    u64 wbase = before;
+    for (int o = 0; o < w; ++o) wbase += s_red[o];
+    const u64 excl = wbase + incl - mine;
+    if (excl <= target && target < excl + mine) {
+        u64 acc = excl;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            acc += em[q];
+            if (acc > target) {
+                s_bc[1] = (u64)(e + q);
+                s_bc[2] = em[q];
+                s_bc[3] = __float_as_uint(lv[q]);
+                break;
+            }
+        }
+    }
+    __syncthreads();
+    if (tid == 0) {
+        const float clp = fs_clp(p);
+        const float lm = __uint_as_float(ld_agent((const u32*)&row->lse_m)), ls = __uint_as_float(ld_agent((const u32*)&row->lse_s));
+        fs_out(r, (int)s_bc[1], (int)key_id(top), GBS_ROW_OK, (float)((double)s_bc[2] / (double)z),
+               fs_logprob(__uint_as_float((u32)s_bc[3]), M, clp, lm, ls), out_ids, out_greedy, out_probs, out_logprobs, out_status);
+    }
+}
+
 }  // namespace
 
 #if GBS_EXP_FULLT
@@ -636,29 +1146,48 @@ GBS_EXPORT int gbs_debug_full_times(void* host) { return (int)hipMemcpyFromSymbo
 
 namespace gbs {
 
+size_t sample_full_workspace_bytes(int rows, int vocab) {
+    const FsPlan pl = fs_plan(rows, vocab);
+    return pl.S >= 2 ? pl.bytes : 256;
+}
+
 int launch_sample_full(const void* logits, int dtype, int rows, int stride, int vocab, const int32_t* counts, const uint32_t* mask,
                        const void* params, const float* uniforms, int* out_ids, int* out_greedy, float* out_probs, float* out_logprobs,
-                       int* out_status, void* stream) {
+                       int* out_status, void* ws, size_t ws_bytes, void* stream) {
     const size_t esz = dtype == GBS_DTYPE_F32 ? 4 : 2;
     const bool vec = stride % 4 == 0 && aligned(logits, 4 * esz) && (!counts || (vocab % 4 == 0 && aligned(counts, 16)));
     const hipStream_t st = to_stream(stream);
     const RowParamsDev* p = (const RowParamsDev*)params;
-#define GBS_FULL(D, C, Mk)                                                                                                        \
-    hipLaunchKernelGGL((sample_full_k<D, C, Mk>), dim3(rows), dim3(NTF), 0, st, logits, (long long)stride, vocab, counts, mask, p, \
-                       uniforms, vec, out_ids, out_greedy, out_probs, out_logprobs, out_status)
+    const FsPlan pl = fs_plan(rows, vocab);
+    const bool split = pl.S >= 2;
+    if (split && (!ws || !aligned(ws, 256) || ws_bytes < pl.bytes)) return GBS_ERR_INVALID;
+    const FsWs w = split ? fs_carve(ws, rows, pl) : FsWs{};
+    const FsRow* only = split ? w.rows : nullptr;
+    auto run = [&]<int D, bool C, bool Mk>() {
+        if (split) {
+            const dim3 grid(pl.S, rows);
+            hipLaunchKernelGGL((fs_pass0_k<D, C, Mk>), grid, dim3(NTF), 0, st, logits, (long long)stride, vocab, counts, mask, p, uniforms, vec,
+                               pl.tpb, w, out_ids, out_greedy, out_probs, out_logprobs, out_status);
+            hipLaunchKernelGGL((fs_hist_k<D, C, Mk>), grid, dim3(NTF), 0, st, logits, (long long)stride, vocab, counts, mask, p, vec, pl.tpb,
+                               w);
+            hipLaunchKernelGGL((fs_collect_k<D, C, Mk>), grid, dim3(NTF), 0, st, logits, (long long)stride, vocab, counts, mask, p,
+                               uniforms, vec, pl.tpb, w, out_ids, out_greedy, out_probs, out_logprobs, out_status);
+        }
+        hipLaunchKernelGGL((sample_full_k<D, C, Mk>), dim3(rows), dim3(NTF), 0, st, logits, (long long)stride, vocab, counts, mask, p,
+                           uniforms, vec, out_ids, out_greedy, out_probs, out_logprobs, out_status, only);
+    };
     const bool c = counts != nullptr, m = mask != nullptr;
     if (dtype == GBS_DTYPE_F32) {
-        if (c && m) GBS_FULL(GBS_DTYPE_F32, true, true);
-        else if (c) GBS_FULL(GBS_DTYPE_F32, true, false);
-        else if (m) GBS_FULL(GBS_DTYPE_F32, false, true);
-        else GBS_FULL(GBS_DTYPE_F32, false, false);
+        if (c && m) run.template operator()<GBS_DTYPE_F32, true, true>();
+        else if (c) run.template operator()<GBS_DTYPE_F32, true, false>();
+        else if (m) run.template operator()<GBS_DTYPE_F32, false, true>();
+        else run.template operator()<GBS_DTYPE_F32, false, false>();
     } else {
-        if (c && m) GBS_FULL(GBS_DTYPE_BF16, true, true);
-        else if (c) GBS_FULL(GBS_DTYPE_BF16, true, false);
-        else if (m) GBS_FULL(GBS_DTYPE_BF16, false, true);
-        else GBS_FULL(GBS_DTYPE_BF16, false, false);
+        if (c && m) run.template operator()<GBS_DTYPE_BF16, true, true>();
+        else if (c) run.template operator()<GBS_DTYPE_BF16, true, false>();
+        else if (m) run.template operator()<GBS_DTYPE_BF16, false, true>();
+        else run.template operator()<GBS_DTYPE_BF16, false, false>();
     }
-#undef GBS_FULL
     return launch_status();
 }
 

@@ -285,3 +285,17 @@ def test_full_path_binned_cut_edges():
     log("config3 full size, full path")
     g, w = run_both(cfg, kmax=0)
     compare(g, w, "config3 full size")
+
+
+def test_full_and_fast_paths_alternate_on_one_workspace():
+    """The fast path (kmax 64) and the split full path (kmax 0, fewer rows than CUs: several blocks per row, three
+    launches with last-block hand-offs) share one workspace; their counters sit in one control region and every
+    launch leaves them zero, so alternating launches stay exact. Also the split path at one row (38 blocks)."""
+    need_gpu()
+    cases = [(W.config3(rows=16), 0, "c3 16 rows full"), (W.northstar(seed=3, rows=40, vocab=60_000), 64, "ns 40 rows fast"),
+             (W.config1(5), 0, "c1 one row full"), (W.config4(rows=16), 64, "c4 16 rows fast"),
+             (W.northstar(seed=4, rows=40, vocab=60_000), 0, "ns 40 rows full"), (W.config3(rows=16), 0, "c3 16 rows full again")]
+    for cfg, kmax, what in cases:
+        log(what)
+        g, w = run_both(cfg, kmax=kmax)
+        compare(g, w, what)
