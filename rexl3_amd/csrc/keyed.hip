@@ -5,10 +5,11 @@
 //    cumsum run on lane 0, at most 64 terms), the Gumbel noise of each kept candidate on its own lane, and an argmax that
 //    keeps the first candidate on ties, as the reference's strict `>` does.
 //  - gb_glm_keyed_pick (crates/cuda/csrc/glm_mtp.cu:266-297), gb_qfn_greedy_gather (crates/cuda/csrc/qfn_verify.cu:11-40).
-//  - gbs_keyed_sample_rows: exact top-(top_k + 8) over the full row and the keyed draw in ONE launch. Grid (splits,
-//    rows); each block selects its chunk's best 64 keys, writes them to the workspace and counts its arrival; the last
-//    block of a row merges the row's lists and draws. Only the chosen id leaves the device.
+//  - gbs_keyed_sample_rows: exact top-(top_k + 8) over the full row and the keyed draw in ONE launch (keyed_fast_k: one
+//    block per row, or a few per row with a last-block hand-off when there are fewer rows than CUs). Only the chosen id
+//    leaves the device.
 //  - gbs_accept / gbs_accept_tree: crates/spec/src/lib.rs:30-35 and crates/spec/src/tree.rs:417-438.
+//  - gbs_tree_verify: a tree round on the device, keyed draws at each node's position then the accept walk.
 #include "gbs_select.hpp"
 
 using namespace gbs;
@@ -186,21 +187,6 @@ __global__ void greedy_gather_k(const int* __restrict__ ids, const float* __rest
 
 // ------------------------------------------------------------------------------------------------ fused keyed sampler
 
-#ifndef GBS_KEYED_FAST
-#define GBS_KEYED_FAST 1
-#endif
-constexpr bool KEYED_FAST = GBS_KEYED_FAST;  // the one-block-per-row kernel (else the split kernel)
-constexpr int KS_TARGET_BLOCKS = 1024;
-constexpr int KS_MIN_CHUNK = 4096;
-
-int keyed_splits(int rows, int valid) {
-    int s = (KS_TARGET_BLOCKS + rows - 1) / rows;
-    const int by_size = (valid + KS_MIN_CHUNK - 1) / KS_MIN_CHUNK;
-    if (s > by_size) s = by_size;
-    if (s < 1) s = 1;
-    return s;
-}
-
 size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
 // The per-row arrival counters (zero between launches) sit at fixed offsets in the first KEYED_CTL_BYTES, room for
@@ -212,10 +198,7 @@ int keyed_fast_splits(int rows, int valid);
 
 size_t keyed_ws_bytes(int rows, int valid) {
     if (rows <= 0 || valid <= 0) return 0;
-    int s = keyed_splits(rows, valid);
-    const int sf = keyed_fast_splits(rows, valid);
-    s = s > sf ? s : sf;
-    return KEYED_CTL_BYTES + (size_t)rows * s * WAVE * sizeof(u64);
+    return KEYED_CTL_BYTES + (size_t)rows * keyed_fast_splits(rows, valid) * WAVE * sizeof(u64);
 }
 
 __device__ __forceinline__ bool keyed_params_ok(const KeyedRowDev& p) {
@@ -225,65 +208,10 @@ __device__ __forceinline__ bool keyed_params_ok(const KeyedRowDev& p) {
     return t_ok && p_ok && m_ok && p.top_k >= 1 && p.top_k <= 56;
 }
 
-template <int DT>
-__global__ void __launch_bounds__(NT) keyed_sample_k(const void* logits, long long stride, int valid, int chunk,
-                                                     const KeyedRowDev* __restrict__ params, int depth, unsigned* counters, u64* parts,
-                                                     int* out_ids, float* out_vals, int* out_status) {
-    __shared__ u64 s_buf[NW][BUF];
-    __shared__ u64 s_list[NW][WAVE];
-    __shared__ float s_v[WAVE];
-    __shared__ u32 s_id[WAVE];
-    __shared__ double s_tmp[WAVE];
-    __shared__ unsigned s_flag;
-    const int S = gridDim.x, sp = blockIdx.x, r = blockIdx.y;
-    const size_t esz = DT == DT_F32 ? 4 : 2;
-    const void* row = (const char*)logits + (size_t)r * (size_t)stride * esz;
-    const KeyedRowDev p = params[r];
-    const bool ok = keyed_params_ok(p);
-    const int count = ok ? min(p.top_k + 8, valid) : min(WAVE, valid);
-    const int lo = sp * chunk;
-    const int hi = min(valid, lo + chunk);
-    const bool vec = (stride % 4 == 0) && aligned(logits, DT == DT_F32 ? 16 : 8);
-    WaveTop<BUF> wt;
-    wt.init(s_buf[threadIdx.x / WAVE], count, 0ull);
-    block_select<DT>(row, lo, hi, vec, count, wt, s_list);
-    u64 list = wt.list;
-    if (S > 1) {
-        if (threadIdx.x < WAVE) st_agent(&parts[((size_t)r * S + sp) * WAVE + threadIdx.x], wt.list);
-        if (!arrive_last(&counters[r], (unsigned)S, &s_flag)) return;
-        list = block_merge_lists<NW>(parts + (size_t)r * S * WAVE, S, s_list);
-    }
-    if (threadIdx.x >= WAVE) return;
-    const int l = lane_id();
-    int status = ok ? GBS_ROW_OK : GBS_ROW_INVALID_PARAMS;
-    const u32 id = key_id(list);
-    float v = 0.f;
-    if (l < count && list != 0ull) {  // the first `count` keys are elements of the row (every valid element is offered)
-        if (DT == DT_F32) v = ((const float*)row)[id];
-        else v = okey16_to_f32<DT == DT_F16>(key_ok(list));
-    }
-    if (status == GBS_ROW_OK && ballot(l < count && v != v)) status = GBS_ROW_NAN_LOGIT;
-    int pick = 0;
-    if (status == GBS_ROW_OK && p.temperature > 0.0) {
-        s_v[l] = v;
-        s_id[l] = id;
-        wave_lds_sync();
-        const int k = min(p.top_k, count);
-        pick = keyed_choose_wave(s_v, s_id, k, p.seed, p.temperature, p.top_p, p.min_p, p.first_position + (u64)depth, s_tmp);
-    }
-    const u32 pid = readlane32(id, pick);
-    const float pv = __uint_as_float(readlane32(__float_as_uint(v), pick));
-    if (l == 0) {
-        out_ids[r] = status == GBS_ROW_OK ? (int)pid : -1;
-        if (out_vals) out_vals[r] = status == GBS_ROW_OK ? pv : __uint_as_float(0x7fc00000u);
-        if (out_status) out_status[r] = status;
-    }
-}
-
 // ------------------------------------------------------------------------------------------------ fused keyed sampler,
 // one block per row
 //
-// The same result as keyed_sample_k, on the north-star kernel's streaming design: a block of KNT threads per row (rows
+// try_choose over each row's exact top-(top_k + 8), on the north-star kernel's streaming design: a block of KNT threads per row (rows
 // split over blocks only when there are fewer rows than CUs). Wave-steps of KWSTEP contiguous elements (KGROUPS
 // 4-element groups per lane) are handed out through an LDS counter, two in flight per wave; each wave keeps its gated
 // top-64 list, the gate raised by the block bound of every wave's best keys. With one block per row the block merges
@@ -291,20 +219,8 @@ __global__ void __launch_bounds__(NT) keyed_sample_k(const void* logits, long lo
 #ifndef GBS_KEYED_NT
 #define GBS_KEYED_NT 1024
 #endif
-#ifndef GBS_EXP_KBARE
-#define GBS_EXP_KBARE 0
-#endif
-#ifndef GBS_KEYED_ROT
-#define GBS_KEYED_ROT 1
-#endif
 #ifndef GBS_KEYED_GROUPS
 #define GBS_KEYED_GROUPS 4
-#endif
-#ifndef GBS_EXP_KTIMES
-#define GBS_EXP_KTIMES 0
-#endif
-#if GBS_EXP_KTIMES
-__device__ u64 g_kdbg[65536];
 #endif
 constexpr int KNT = GBS_KEYED_NT;
 constexpr int KNW = KNT / WAVE;
@@ -356,10 +272,6 @@ __global__ void __launch_bounds__(KNT, 1) keyed_fast_k(const void* logits, long 
     __shared__ int s_next;
     const int S = gridDim.x, sp = blockIdx.x, r = blockIdx.y;
     const int tid = threadIdx.x, w = tid / WAVE, l = lane_id();
-#if GBS_EXP_KTIMES
-    const u64 t0 = wall_clock64();
-    if (tid == 0) g_kdbg[(size_t)r * 8 + 0] = t0;
-#endif
     if (tid == 0) {
         s_thr = 0;
         s_next = KNW;
@@ -377,19 +289,14 @@ __global__ void __launch_bounds__(KNT, 1) keyed_fast_k(const void* logits, long 
     wt.init(s_buf[w], count, 0ull, &s_thr);
     wt.set_top(s_top, w, KNW);
     int e0 = lo;
-    u32 bare_acc = 0;
     if (vec) {
         // loads past the row's valid columns (rounded up to a whole group, inside the row) return zeros; the last
         // wave-step's elements at or past `hi` are not offered
         const u32 nbytes = (u32)((valid + 3) / 4 * 4) * (u32)esz;
         const __amdgpu_buffer_rsrc_t R = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(row), (short)0, (int)nbytes, 0x00020000);
         const int nws = (hi - lo + KWSTEP - 1) / KWSTEP;
-        // wave-step idx covers [lo + pos(idx) KWSTEP, ...): the order is rotated by a row-dependent offset, so that the
-        // blocks of a batch do not all read the same offsets of their rows at once
-        const int rot = GBS_KEYED_ROT ? (int)(((unsigned)r * 37u) % (unsigned)(nws > 0 ? nws : 1)) : 0;
-        auto pos = [&](int idx) { const int q = idx + rot; return q >= nws ? q - nws : q; };
         auto load = [&](int idx, KRaw<DT>& b) {
-            const u32 e = (u32)(lo + pos(idx) * KWSTEP + l * 4);
+            const u32 e = (u32)(lo + idx * KWSTEP + l * 4);
 #pragma unroll
             for (int j = 0; j < KGROUPS; ++j) {
                 if constexpr (DT == DT_F32) b.x[j] = __builtin_amdgcn_raw_buffer_load_b128(R, (e + j * KGS) * 4u, 0, 2);
@@ -403,7 +310,7 @@ __global__ void __launch_bounds__(KNT, 1) keyed_fast_k(const void* logits, long 
         };
         // the keys of one loaded wave-step (out of the chunk: key 0, not offered); `first` seeds the gate
         auto step = [&](KRaw<DT>& B, int idx, bool first, auto&& reload) __attribute__((always_inline)) {
-            const int e = lo + pos(idx) * KWSTEP + l * 4;
+            const int e = lo + idx * KWSTEP + l * 4;
             wt.apply_shared();
             wt.prefetch_shared();
             // f32 rows whose gate is a float at or above -inf test the gate with one float compare per element (NaN
@@ -459,15 +366,8 @@ __global__ void __launch_bounds__(KNT, 1) keyed_fast_k(const void* logits, long 
                 for (int i = 0; i < KGROUPS * 4; ++i) m = k[i] > m ? k[i] : m;
                 wt.seed(m);
                 __syncthreads();
-#if GBS_EXP_KTIMES
-                if (tid == 0) g_kdbg[(size_t)r * 8 + 1] = wall_clock64();
-#endif
                 wt.block_bound();
             }
-#if GBS_EXP_KBARE
-            for (int i = 0; i < KGROUPS * 4; ++i) bare_acc ^= k[i];
-            return;
-#endif
             const u32 g = wt.gate;
             bool any = false;
 #pragma unroll
@@ -483,7 +383,6 @@ __global__ void __launch_bounds__(KNT, 1) keyed_fast_k(const void* logits, long 
         };
         KRaw<DT> A, B;
         int ia = w;
-        (void)bare_acc;
         int ib = grab();
         if (ia < nws) load(ia, A);
         if (ib < nws) load(ib, B);
@@ -522,24 +421,6 @@ __global__ void __launch_bounds__(KNT, 1) keyed_fast_k(const void* logits, long 
     wt.prefetch_shared();
     wt.apply_shared();
     wt.flush(true);
-#if GBS_EXP_KTIMES
-    {
-        __shared__ u64 s_tw[KNW];
-        if (l == 0) s_tw[w] = wall_clock64();
-        __syncthreads();
-        if (tid == 0) {
-            u64 mn = ~0ull, mx = 0;
-            for (int o = 0; o < KNW; ++o) { mn = s_tw[o] < mn ? s_tw[o] : mn; mx = s_tw[o] > mx ? s_tw[o] : mx; }
-            g_kdbg[(size_t)r * 8 + 2] = mn;
-            g_kdbg[(size_t)r * 8 + 3] = mx;
-        }
-    }
-#endif
-#if GBS_EXP_KBARE
-    // the bare variant offers nothing: its lists hold no element, so it ends before the finish reads any
-    if (tid == 0) out_ids[r] = (int)bare_acc;
-    return;
-#endif
     u64 list = block_tree_merge<KNW>(wt.list, s_list);
     if (S > 1) {
         if (tid < WAVE) st_agent(&parts[((size_t)r * S + sp) * WAVE + tid], list);
@@ -547,9 +428,6 @@ __global__ void __launch_bounds__(KNT, 1) keyed_fast_k(const void* logits, long 
         list = block_merge_lists<KNW>(parts + (size_t)r * S * WAVE, S, s_list);
     }
     if (tid >= WAVE) return;
-#if GBS_EXP_KTIMES
-    if (tid == 0) g_kdbg[(size_t)r * 8 + 5] = wall_clock64();
-#endif
     int status = ok ? GBS_ROW_OK : GBS_ROW_INVALID_PARAMS;
     const u32 id = key_id(list);
     float v = 0.f;
@@ -559,9 +437,6 @@ __global__ void __launch_bounds__(KNT, 1) keyed_fast_k(const void* logits, long 
     }
     if (status == GBS_ROW_OK && ballot(l < count && v != v)) status = GBS_ROW_NAN_LOGIT;
     int pick = 0;
-#if GBS_EXP_KTIMES
-    if (tid == 0) g_kdbg[(size_t)r * 8 + 6] = wall_clock64();
-#endif
     if (status == GBS_ROW_OK && p.temperature > 0.0) {
         s_v[l] = v;
         s_id[l] = id;
@@ -575,17 +450,8 @@ __global__ void __launch_bounds__(KNT, 1) keyed_fast_k(const void* logits, long 
         out_ids[r] = status == GBS_ROW_OK ? (int)pid : -1;
         if (out_vals) out_vals[r] = status == GBS_ROW_OK ? pv : __uint_as_float(0x7fc00000u);
         if (out_status) out_status[r] = status;
-#if GBS_EXP_KTIMES
-        g_kdbg[(size_t)r * 8 + 4] = wall_clock64();
-#endif
     }
 }
-
-#if GBS_EXP_KTIMES
-}  // namespace
-GBS_EXPORT int gbs_debug_keyed_times(void* host) { return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_kdbg), sizeof(g_kdbg)); }
-namespace {
-#endif
 
 // ------------------------------------------------------------------------------------------------ accept steps
 
@@ -718,37 +584,21 @@ GBS_EXPORT int gbs_keyed_sample_rows(const void* logits, int dtype, int rows, in
     unsigned* counters = (unsigned*)ws;
     u64* parts = (u64*)((char*)ws + KEYED_CTL_BYTES);
     const KeyedRowDev* p = (const KeyedRowDev*)params;
-    if (KEYED_FAST) {
-        const int S = keyed_fast_splits(rows, valid);
-        int chunk = (valid + S - 1) / S;
-        chunk = (chunk + 3) / 4 * 4;
-        const size_t esz = dtype == GBS_DTYPE_F32 ? 4 : 2;
-        const bool vec = stride % 4 == 0 && aligned(logits, 4 * esz);
-        const dim3 grid(S, rows);
-        if (dtype == GBS_DTYPE_F32)
-            hipLaunchKernelGGL(keyed_fast_k<DT_F32>, grid, dim3(KNT), 0, to_stream(stream), logits, (long long)stride, valid, chunk, p,
-                               depth, vec, counters, parts, out_ids, out_vals, out_status);
-        else if (dtype == GBS_DTYPE_BF16)
-            hipLaunchKernelGGL(keyed_fast_k<DT_BF16>, grid, dim3(KNT), 0, to_stream(stream), logits, (long long)stride, valid, chunk, p,
-                               depth, vec, counters, parts, out_ids, out_vals, out_status);
-        else
-            hipLaunchKernelGGL(keyed_fast_k<DT_F16>, grid, dim3(KNT), 0, to_stream(stream), logits, (long long)stride, valid, chunk, p,
-                               depth, vec, counters, parts, out_ids, out_vals, out_status);
-        return launch_status();
-    }
-    const int S = keyed_splits(rows, valid);
+    const int S = keyed_fast_splits(rows, valid);
     int chunk = (valid + S - 1) / S;
     chunk = (chunk + 3) / 4 * 4;
+    const size_t esz = dtype == GBS_DTYPE_F32 ? 4 : 2;
+    const bool vec = stride % 4 == 0 && aligned(logits, 4 * esz);
     const dim3 grid(S, rows);
     if (dtype == GBS_DTYPE_F32)
-        hipLaunchKernelGGL(keyed_sample_k<DT_F32>, grid, dim3(NT), 0, to_stream(stream), logits, (long long)stride, valid, chunk, p,
-                           depth, counters, parts, out_ids, out_vals, out_status);
+        hipLaunchKernelGGL(keyed_fast_k<DT_F32>, grid, dim3(KNT), 0, to_stream(stream), logits, (long long)stride, valid, chunk, p,
+                           depth, vec, counters, parts, out_ids, out_vals, out_status);
     else if (dtype == GBS_DTYPE_BF16)
-        hipLaunchKernelGGL(keyed_sample_k<DT_BF16>, grid, dim3(NT), 0, to_stream(stream), logits, (long long)stride, valid, chunk, p,
-                           depth, counters, parts, out_ids, out_vals, out_status);
+        hipLaunchKernelGGL(keyed_fast_k<DT_BF16>, grid, dim3(KNT), 0, to_stream(stream), logits, (long long)stride, valid, chunk, p,
+                           depth, vec, counters, parts, out_ids, out_vals, out_status);
     else
-        hipLaunchKernelGGL(keyed_sample_k<DT_F16>, grid, dim3(NT), 0, to_stream(stream), logits, (long long)stride, valid, chunk, p,
-                           depth, counters, parts, out_ids, out_vals, out_status);
+        hipLaunchKernelGGL(keyed_fast_k<DT_F16>, grid, dim3(KNT), 0, to_stream(stream), logits, (long long)stride, valid, chunk, p,
+                           depth, vec, counters, parts, out_ids, out_vals, out_status);
     return launch_status();
 }
 

@@ -18,18 +18,6 @@ using namespace gbs::modeu;
 
 namespace {
 
-#ifndef GBS_EXP_NOATOM
-#define GBS_EXP_NOATOM 0
-#endif
-#ifndef GBS_EXP_FULLT
-#define GBS_EXP_FULLT 0
-#endif
-#if GBS_EXP_FULLT
-__device__ u64 g_fdbg[65536];
-#define FT(k) do { if (threadIdx.x == 0) g_fdbg[(size_t)blockIdx.x * 8 + (k)] = wall_clock64(); } while (0)
-#else
-#define FT(k) do { } while (0)
-#endif
 constexpr int NTF = 1024;
 constexpr int NWF = NTF / WAVE;
 constexpr int DB = 11;
@@ -350,23 +338,13 @@ __device__ bool binned_cut(const Row<DT, COUNTS, MASK>& R, float M, float c2, fl
     if (topp) {
         for (int i = tid; i < NBINS; i += NTF) sh.mass[i] = 0;
         __syncthreads();
-#if GBS_EXP_NOATOM
-        u64 fake = 0;
-#endif
         stream_tiles(R, [&](int, int, const float (&lv)[4]) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const u64 E = mass_fast(lv[q], M, c2);
-#if GBS_EXP_NOATOM
-                fake += E + bin_of(lv[q], M, c2);
-#else
                 if (E) atomicAdd((unsigned long long*)&sh.mass[bin_of(lv[q], M, c2)], (unsigned long long)E);
-#endif
             }
         });
-#if GBS_EXP_NOATOM
-        if (fake == 12345) sh.mass[0] = fake;
-#endif
         __syncthreads();
         if (tid < WAVE) {
             // lane i owns bins [32 i, 32 i + 32): the total, P, then the bin where the cumulative mass reaches P
@@ -392,7 +370,6 @@ __device__ bool binned_cut(const Row<DT, COUNTS, MASK>& R, float M, float c2, fl
             }
         }
         __syncthreads();
-        FT(2);
         bstar = (u32)sh.bc[0];
         above = sh.bc[1];
         P = sh.bc[2];
@@ -443,7 +420,6 @@ __device__ bool binned_cut(const Row<DT, COUNTS, MASK>& R, float M, float c2, fl
         sh.tile[t] = v;
     }
     __syncthreads();
-    FT(3);
     const u32 n = sh.ncol;
     if (n > (u32)CAP) return false;
     u64 kp = (u64)VALID_MIN_OK << 32;  // every valid key
@@ -460,7 +436,6 @@ __device__ bool binned_cut(const Row<DT, COUNTS, MASK>& R, float M, float c2, fl
             if (lo < P && P <= lo + sh.mass[i]) sh.bc[3] = ki;
         }
         __syncthreads();
-        FT(4);
         kp = sh.bc[3];
         // the kept tokens of bin b* (key >= the top-p key, mass >= Q) into their tiles
         for (u32 j = tid; j < n; j += NTF) {
@@ -508,7 +483,6 @@ __global__ void __launch_bounds__(NTF) sample_full_k(const void* __restrict__ lo
             if (out_status) out_status[r] = status;
         }
     };
-    FT(0);
     if (params_invalid(p, u)) {
         finish(-1, -1, GBS_ROW_INVALID_PARAMS, 0.f, 0.f);
         return;
@@ -542,7 +516,6 @@ __global__ void __launch_bounds__(NTF) sample_full_k(const void* __restrict__ lo
         sh.lse_m[w] = lse.m;
         sh.lse_s[w] = lse.s;
     }
-    FT(1);
     const u32 nan_any = (u32)block_sum((u64)nan, sh.red);
     const u64 n_allowed = block_sum((u64)nallowed, sh.red);
     const u64 top = block_max_u64(kmaxv, sh.red);
@@ -659,7 +632,6 @@ __global__ void __launch_bounds__(NTF) sample_full_k(const void* __restrict__ lo
     const u64 ec = sh.bc[6];
     const float lx = __uint_as_float((u32)sh.bc[7]);
     finish(id, greedy, GBS_ROW_OK, (float)((double)ec / (double)z), logprob_of(lx));
-    FT(5);
 }
 
 // ================================================================================================== the split path
@@ -1140,9 +1112,6 @@ __global__ void __launch_bounds__(NTF) fs_collect_k(const void* __restrict__ log
 
 }  // namespace
 
-#if GBS_EXP_FULLT
-GBS_EXPORT int gbs_debug_full_times(void* host) { return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_fdbg), sizeof(g_fdbg)); }
-#endif
 
 namespace gbs {
 

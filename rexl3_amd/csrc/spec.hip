@@ -29,26 +29,11 @@ namespace {
 #ifndef GBS_SPEC_U
 #define GBS_SPEC_U 4
 #endif
-#ifndef GBS_EXP_DRAW_NOCOMPUTE
-#define GBS_EXP_DRAW_NOCOMPUTE 0
-#endif
-#ifndef GBS_EXP_DRAW_NOTAIL
-#define GBS_EXP_DRAW_NOTAIL 0
-#endif
 #ifndef GBS_SPEC_AUX_FWD
 #define GBS_SPEC_AUX_FWD 2  // cache policy of the forward sweeps' loads (2: non-temporal)
 #endif
 #ifndef GBS_SPEC_AUX_REV
 #define GBS_SPEC_AUX_REV 2
-#endif
-#ifndef GBS_EXP_DRAWT
-#define GBS_EXP_DRAWT 0
-#endif
-#if GBS_EXP_DRAWT
-__device__ u64 g_dbg[65536];
-#define DBGT(k) do { if (threadIdx.x == 0) g_dbg[(size_t)seq * 8 + (k)] = wall_clock64(); } while (0)
-#else
-#define DBGT(k) do { } while (0)
 #endif
 #ifndef GBS_SPEC_PIPE
 #define GBS_SPEC_PIPE 1
@@ -708,11 +693,7 @@ __device__ __forceinline__ void draw_tiles(const float* tr, const float* dr, int
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const bool in = e + q < vocab;  // buffer loads past the row's end return 0, not -inf
-#if GBS_EXP_DRAW_NOCOMPUTE
-                part += (u128)__float_as_uint(t[j * 4 + q]) + __float_as_uint(d[j * 4 + q]) + (in ? 1u : 0u);
-#else
                 part += pair_weight<FAST>(MODE, in ? t[j * 4 + q] : -INFINITY, in ? d[j * 4 + q] : -INFINITY, Mp, Mq, c2, zp, zq);
-#endif
             }
             part = wave_sum_u128(part);
             if (l == 0) {
@@ -736,7 +717,6 @@ __global__ void __launch_bounds__(NT) spec_draw_k(const float* __restrict__ targ
     const int S = gridDim.x, sp = blockIdx.x, seq = blockIdx.y;
     const int tiles = (vocab + TILE - 1) / TILE;
     const int nsub = tiles * DU * NWD;
-    const u64 t_begin = wall_clock64();
     const SeqInfo si = load_seq(ws.seqs, seq);
     const bool drawing = si.status == GBS_ROW_OK && si.mode != 0;
     const float* tr = target + (size_t)si.row * vocab;
@@ -750,17 +730,9 @@ __global__ void __launch_bounds__(NT) spec_draw_k(const float* __restrict__ targ
         else if (fast) draw_tiles<2, true>(tr, dr, vocab, t0, t1, vec, si.Mp, si.Mq, si.c2, si.zp, si.zq, wp);
         else draw_tiles<2, false>(tr, dr, vocab, t0, t1, vec, si.Mp, si.Mq, si.c2, si.zp, si.zq, wp);
     }
-    const u64 t_streamed = wall_clock64();
     if (!arrive_last(&ws.draw_counters[seq], (unsigned)S, &s_flag)) return;
-#if GBS_EXP_DRAWT
-    if (threadIdx.x == 0) { g_dbg[(size_t)seq * 8 + 0] = t_begin; g_dbg[(size_t)seq * 8 + 1] = t_streamed; }
-#else
-    (void)t_begin;
-    (void)t_streamed;
-#endif
-    DBGT(2);
     int token = si.token;
-    if (drawing && !GBS_EXP_DRAW_NOTAIL) {
+    if (drawing) {
         const int tid = (int)threadIdx.x;
         if (tid == 0) {
             s_flag = (unsigned)nsub;  // a zero total selects no sub-tile
@@ -793,7 +765,6 @@ __global__ void __launch_bounds__(NT) spec_draw_k(const float* __restrict__ targ
             s_rem = t - before;
         }
         __syncthreads();
-        DBGT(3);
         const int p = (int)s_flag;
         const u128 rem = s_rem;
         // sub-tile p: one element per thread, coalesced; a block scan; the element whose range holds rem
@@ -803,13 +774,10 @@ __global__ void __launch_bounds__(NT) spec_draw_k(const float* __restrict__ targ
         const float de = (in && si.mode == 1) ? dr[e] : -INFINITY;
         const u128 we = fast ? pair_weight<true>(si.mode, te, de, si.Mp, si.Mq, si.c2, si.zp, si.zq)
                              : pair_weight(si.mode, te, de, si.Mp, si.Mq, si.c2, si.zp, si.zq);
-        DBGT(4);
         u128 sub_total;
         const u128 before = block_scan_u128(we, sub_total, s_wt);
-        DBGT(5);
         if (p < nsub && we != 0 && before <= rem && rem - before < we) s_tok = e;
         __syncthreads();
-        DBGT(6);
         token = s_tok;
     }
     if (threadIdx.x == 0) {
@@ -825,14 +793,10 @@ __global__ void __launch_bounds__(NT) spec_draw_k(const float* __restrict__ targ
             out_tokens[(size_t)seq * W1 + j] = v;
         }
     }
-    DBGT(7);
 }
 
 }  // namespace
 
-#if GBS_EXP_DRAWT
-GBS_EXPORT int gbs_debug_times(void* host) { return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_dbg), sizeof(g_dbg)); }
-#endif
 
 GBS_EXPORT size_t gbs_spec_verify_workspace_bytes(int n_seq, int width, int vocab) {
     if (n_seq <= 0 || width < 0 || vocab <= 0 || vocab > GBS_MAX_VOCAB) return 0;
