@@ -5,7 +5,7 @@ int32 counts, a u32 grammar bitmask, temperature, top-k 50 / top-p 0.9, fused ma
 inverse-CDF draw from one uniform per row -- at B=256, V=151,936 fp32, inputs resident in HBM. One step = one
 gbs_sample_rows launch over the batch. Prints one JSON line.
 
-    python bench.py [--steps K] [--warmup W] [--workload northstar|c1|c2|c4|c5|keyed] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--workload northstar|c1|c2|c3|c4|c5|keyed] [--no-cpu]
 """
 from __future__ import annotations
 
@@ -232,6 +232,18 @@ def main():
         kernel = "spec_rows_k + spec_draw_k" if R >= 192 else "spec_max_k + spec_mass_k + spec_draw_k"
         dtype = "f32 (integer masses)"
         workload = "config 5: speculative verification, 32 sequences x (7 drafts + 1 bonus), rejection + residual resampling"
+        if not args.no_cpu:
+            from oracle import oracle as O
+            t0 = time.perf_counter()
+            done = 0
+            while time.perf_counter() - t0 < args.cpu_seconds:
+                O.spec_verify(cfg["target"], cfg["draft"], n_seq, width, cfg["draft_ids"], cfg["temperatures"], cfg["u_accept"],
+                              cfg["u_resample"], threads=threads)
+                done += R
+            el = time.perf_counter() - t0
+            cpu = {"value": round(done / el, 1), "unit": "rows/s", "cores": threads, "kind": "port",
+                   "sample": f"the build's C oracle of the same verification on the same batch (its sequences over "
+                             f"{threads} threads), {done} rows in {el:.1f} s"}
     else:
         raise SystemExit(f"unknown workload {wl}")
 

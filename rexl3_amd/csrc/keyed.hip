@@ -228,7 +228,10 @@ constexpr int KGROUPS = GBS_KEYED_GROUPS;
 constexpr int KGS = WAVE * 4;           // elements between a lane's groups
 constexpr int KWSTEP = KGS * KGROUPS;   // elements of one wave-step
 constexpr int KBUF = WAVE * (4 + 1);  // < 64 keys left after a flush + one 4-element group per lane (flushed per group)
-constexpr int KF_TARGET_BLOCKS = 256;
+#ifndef GBS_KEYED_BLOCKS
+#define GBS_KEYED_BLOCKS 256
+#endif
+constexpr int KF_TARGET_BLOCKS = GBS_KEYED_BLOCKS;
 constexpr u32 NEG_INF_OK = 0x007FFFFFu;  // okey_f32(-inf)
 constexpr int KF_MIN_CHUNK = 4096;
 
