@@ -45,7 +45,8 @@ def profiled_traffic(workload):
     """HBM bytes per launch measured with rocprofv3 FETCH_SIZE + WRITE_SIZE (scaled by a plain copy of known size), as
     recorded in profiles/; None when no measurement of this workload is recorded."""
     import re
-    path = os.path.join(ROOT, "profiles", {"northstar": "sample_fast_k_northstar.md"}.get(workload, ""))
+    path = os.path.join(ROOT, "profiles", {"northstar": "sample_fast_k_northstar.md", "keyed": "keyed_fast_k_b256.md",
+                                           "c5": "spec_verify_config5.md", "c3": "sample_full_k_config3.md"}.get(workload, ""))
     if not os.path.isfile(path):
         return None
     m = re.search(r"traffic_bytes_per_launch:\s*(\d+)", open(path).read())
