@@ -128,6 +128,27 @@ int gb_ling_topk_f16(const void* logits, int rows, int stride, int valid, int co
                      size_t ws_bytes, void* stream);
 
 /*
+ * Replace crates/cuda/csrc/dflash2.cu:595-660 (gb_dflash_selector_walk_keyed / _ragged / gb_dflash_selector_walk): the
+ * draft head's selector chain walk, one sequence per block. Row i of a sequence scores its k (<= 64) candidates as
+ * topk_vals[c] + <pred_codebook[prev] * gate[row], succ_codebook[topk_ids[c]]> (f16 codebooks [V, rank]; gate bf16,
+ * or f32 when gate_is_f32) with the reference kernel's float arithmetic, and picks with the sequence's WalkSampling
+ * (48 bytes: u64 seed, u64 first_position, f64 temperature, top_p, min_p, i32 keyed; nullable = every sequence
+ * unkeyed): keyed = the device try_choose over all k at first_position + i (NaN scores last); unkeyed = the first
+ * maximum. anchor i32 [n_seq]; topk_ids i32 / topk_vals f32 [rows total, k]; out_tokens i32 and conf f32 (nullable,
+ * the pick's score) per row; margin (nullable, ragged form) the pick's lead over the runner-up. The ragged form takes
+ * row_off i32 [n_seq + 1] (sequence b owns rows row_off[b] .. row_off[b + 1]).
+ */
+int gb_dflash_selector_walk_keyed(const void* anchor, const void* topk_ids, const void* topk_vals, const void* gate, int gate_is_f32,
+                                  const void* pred_codebook, const void* succ_codebook, int n_seq, int rows, int k, int rank,
+                                  const void* sampling, void* out_tokens, void* conf, void* stream);
+int gb_dflash_selector_walk_ragged(const void* anchor, const void* topk_ids, const void* topk_vals, const void* gate, int gate_is_f32,
+                                   const void* pred_codebook, const void* succ_codebook, int n_seq, int k, int rank, const void* sampling,
+                                   const void* row_off, void* out_tokens, void* conf, void* margin, void* stream);
+int gb_dflash_selector_walk(const void* anchor, const void* topk_ids, const void* topk_vals, const void* gate, int gate_is_f32,
+                            const void* pred_codebook, const void* succ_codebook, int n_seq, int rows, int k, int rank,
+                            void* out_tokens, void* conf, void* stream);
+
+/*
  * Replaces crates/cuda/csrc/glm_mtp.cu:272-280 (gb_glm_keyed_pick). ids i32 / vals f32 [rows, count] sorted by
  * (value desc, id asc), count <= 64; params GbsKeyedRow[rows]. A keyed row with temperature > 0 takes
  * `try_choose` (crates/sampling/src/lib.rs:210-267) over its first min(top_k, count) candidates (top_k 0 = all) at

@@ -1073,3 +1073,130 @@ int gbo_batch_spec_verify(const float* target, const float* draft, int n_seq, in
     j.out_status = out_status;
     return run_threads(&j, n_seq, threads);
 }
+
+/* =====================================================================================================================
+ * The draft head's selector walk (crates/cuda/csrc/dflash2.cu:436-519, walk_kernel; its keyed choice is
+ * crates/cuda/csrc/keyed.cuh:50-112, keyed_choose).
+ * ===================================================================================================================== */
+
+/* keyed_choose: order the k <= 64 scored candidates by (score desc, id asc, NaN last) by insertion, then at temperature 0
+ * the first; otherwise try_choose's steps in double over all k (top_k = k) with the Gumbel argmax keyed on `position`.
+ * `margin` (nullable): the winner's lead over the runner-up in the maximised quantity, 30 with one candidate in play. */
+int gbo_keyed_choose(const float* scores, const int32_t* c_row, int k, uint64_t seed, double temperature, double top_p, double min_p,
+                     uint64_t position, float* margin) {
+    int ord[64];
+    for (int i = 0; i < k; ++i) {
+        int j = i;
+        while (j > 0) {
+            const float va = scores[ord[j - 1]], vb = scores[i];
+            const int before = (vb > va) || (vb == va && c_row[i] < c_row[ord[j - 1]]) || (va != va && vb == vb);
+            if (!before) break;
+            ord[j] = ord[j - 1];
+            --j;
+        }
+        ord[j] = i;
+    }
+    if (temperature == 0.0) {
+        if (margin) *margin = k > 1 ? scores[ord[0]] - scores[ord[1]] : 30.f;
+        return ord[0];
+    }
+    const double t = temperature > 1e-6 ? temperature : 1e-6;
+    double sc[64], pr[64] = {0};
+    int keep = k;
+    for (int i = 0; i < k; ++i) sc[i] = (double)scores[ord[i]] / t;
+    if (top_p > 0.0 && top_p < 1.0) {
+        const double mx = sc[0];
+        for (int i = 0; i < k; ++i) pr[i] = exp(sc[i] - mx);
+        const double total = gbo_pairwise_sum(pr, (size_t)k);
+        double c = 0.0;
+        int below = 0;
+        for (int i = 0; i < k; ++i) {
+            c += pr[i] / total;
+            if (c < top_p) ++below;
+        }
+        keep = below + 1 < k ? below + 1 : k;
+    }
+    if (min_p > 0.0) {
+        const double floor_v = sc[0] + log(min_p);
+        int n = 0;
+        for (int i = 0; i < keep; ++i)
+            if (sc[i] >= floor_v) ++n;
+        keep = n > 1 ? n : 1;
+    }
+    int best = 0;
+    double best_score = -INFINITY, second_score = -INFINITY;
+    for (int i = 0; i < keep; ++i) {
+        const double u = gbo_uniform(seed, position, (uint64_t)(uint32_t)c_row[ord[i]]);
+        const double score = sc[i] + (-log(-log(u)));
+        if (score > best_score) {
+            second_score = best_score;
+            best_score = score;
+            best = i;
+        } else if (score > second_score) {
+            second_score = score;
+        }
+    }
+    if (margin) *margin = keep > 1 ? (float)fmin(best_score - second_score, 30.0) : 30.f;
+    return ord[best];
+}
+
+/* walk_kernel, one sequence at a time. Row i of sequence b (rows base .. base + nrows): a_g[r] = f16 pred[prev][r] *
+ * gate[row][r] (f32); score[c] = unary[c] + dot, the dot summed as the kernel's 32 lanes do (lane l: fmaf over
+ * r = l, l + 32, ... in order; then the xor butterfly over offsets 16, 8, 4, 2, 1; lane 0's value); keyed rows take
+ * keyed_choose at first_position + i, the others the first maximum (strict >) with the gap to the runner-up. */
+void gbo_selector_walk(const int32_t* anchor, const int32_t* ids, const float* vals, const void* gate, int gate_f32,
+                       const uint16_t* pred_cb, const uint16_t* succ_cb, int n_seq, int rows, int k, int rank,
+                       const GboWalkSampling* ws, const int32_t* row_off, int32_t* out, float* conf, float* margin) {
+    float* a_g = (float*)malloc((size_t)rank * sizeof(float));
+    float scores[64];
+    for (int b = 0; b < n_seq; ++b) {
+        const int base = row_off ? row_off[b] : b * rows;
+        const int nrows = row_off ? row_off[b + 1] - base : rows;
+        int pred = anchor[b];
+        for (int i = 0; i < nrows; ++i) {
+            const size_t row = (size_t)(base + i);
+            for (int r = 0; r < rank; ++r) {
+                const float g = gate_f32 ? ((const float*)gate)[row * rank + r] : bf16_to_f32(((const uint16_t*)gate)[row * rank + r]);
+                a_g[r] = f16_to_f32(pred_cb[(size_t)pred * rank + r]) * g;
+            }
+            const int32_t* c_row = ids + row * k;
+            const float* u_row = vals + row * k;
+            for (int c = 0; c < k; ++c) {
+                const uint16_t* b_row = succ_cb + (size_t)c_row[c] * rank;
+                float lanes[32], nl[32];
+                for (int l = 0; l < 32; ++l) {
+                    float dot = 0.f;
+                    for (int r = l; r < rank; r += 32) dot = fmaf(a_g[r], f16_to_f32(b_row[r]), dot);
+                    lanes[l] = dot;
+                }
+                for (int o = 16; o > 0; o >>= 1) {
+                    for (int l = 0; l < 32; ++l) nl[l] = lanes[l] + lanes[l ^ o];
+                    memcpy(lanes, nl, sizeof(lanes));
+                }
+                scores[c] = u_row[c] + lanes[0];
+            }
+            int best = 0;
+            float bs = scores[0], mg = 30.f;
+            if (ws && ws[b].keyed) {
+                best = gbo_keyed_choose(scores, c_row, k, ws[b].seed, ws[b].temperature, ws[b].top_p, ws[b].min_p,
+                                        ws[b].first_position + (uint64_t)i, &mg);
+                bs = scores[best];
+            } else {
+                for (int c = 1; c < k; ++c)
+                    if (scores[c] > bs) {
+                        bs = scores[c];
+                        best = c;
+                    }
+                float second = -INFINITY;
+                for (int c = 0; c < k; ++c)
+                    if (c != best && scores[c] > second) second = scores[c];
+                mg = k > 1 ? fminf(bs - second, 30.f) : 30.f;
+            }
+            pred = c_row[best];
+            out[row] = pred;
+            if (conf) conf[row] = bs;
+            if (margin) margin[row] = mg;
+        }
+    }
+    free(a_g);
+}

@@ -97,6 +97,21 @@ int gbo_batch_spec_verify(const float* target, const float* draft, int n_seq, in
                           const float* temperatures, const float* u_accept, const float* u_resample, int32_t* out_accepted,
                           int32_t* out_tokens, int32_t* out_status, int threads);
 
+
+/* The draft head's selector walk (crates/cuda/csrc/dflash2.cu:436-519) and its keyed choice (crates/cuda/csrc/keyed.cuh:50-112).
+ * GboWalkSampling is the 48-byte WalkSampling record (dflash2.cu:436-441). */
+typedef struct {
+    uint64_t seed, first_position;
+    double temperature, top_p, min_p;
+    int32_t keyed;
+    int32_t pad;
+} GboWalkSampling;
+int gbo_keyed_choose(const float* scores, const int32_t* c_row, int k, uint64_t seed, double temperature, double top_p, double min_p,
+                     uint64_t position, float* margin);
+void gbo_selector_walk(const int32_t* anchor, const int32_t* ids, const float* vals, const void* gate, int gate_f32,
+                       const uint16_t* pred_cb, const uint16_t* succ_cb, int n_seq, int rows, int k, int rank,
+                       const GboWalkSampling* ws, const int32_t* row_off, int32_t* out, float* conf, float* margin);
+
 #ifdef __cplusplus
 }
 #endif

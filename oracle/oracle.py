@@ -106,6 +106,9 @@ def lib():
         L.gbo_batch_keyed_sample.argtypes = [P, C.c_int, C.c_int, C.c_int, C.c_int, P, C.c_int, P, C.c_int]
         L.gbo_batch_sample.restype = C.c_int
         L.gbo_batch_sample.argtypes = [P, C.c_int, C.c_int, C.c_int, C.c_int, P, P, P, P, P, P, P, P, P, C.c_int]
+        L.gbo_keyed_choose.restype = C.c_int
+        L.gbo_keyed_choose.argtypes = [P, P, C.c_int, C.c_uint64, C.c_double, C.c_double, C.c_double, C.c_uint64, C.POINTER(C.c_float)]
+        L.gbo_selector_walk.argtypes = [P, P, P, P, C.c_int, P, P, C.c_int, C.c_int, C.c_int, C.c_int, P, P, P, P, P]
         L.gbo_batch_spec_verify.restype = C.c_int
         L.gbo_batch_spec_verify.argtypes = [P, P, C.c_int, C.c_int, C.c_int, P, P, P, P, P, P, P, C.c_int]
         _lib = L
@@ -292,3 +295,38 @@ def spec_verify(target, draft, n_seq: int, width: int, draft_ids, temperatures, 
     lib().gbo_batch_spec_verify(_p(target), _p(draft), n_seq, width, vocab, _p(draft_ids), _p(temperatures), _p(u_accept),
                                 _p(u_resample), _p(acc), _p(toks), _p(st), threads)
     return acc, toks, st
+
+
+WALK_SAMPLING_DTYPE = np.dtype([("seed", "<u8"), ("first_position", "<u8"), ("temperature", "<f8"), ("top_p", "<f8"),
+                                ("min_p", "<f8"), ("keyed", "<i4"), ("pad", "<i4")])
+
+
+def keyed_choose(scores, ids, seed: int, temperature: float, top_p: float, min_p: float, position: int):
+    """crates/cuda/csrc/keyed.cuh:50-112 over k <= 64 scored candidates: (chosen index, margin)."""
+    scores = np.ascontiguousarray(scores, dtype=np.float32)
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    m = C.c_float(0.0)
+    i = lib().gbo_keyed_choose(_p(scores), _p(ids), scores.size, seed, temperature, top_p, min_p, position, C.byref(m))
+    return i, m.value
+
+
+def selector_walk(anchor, ids, vals, gate, gate_f32: bool, pred_cb, succ_cb, n_seq: int, rows: int, sampling=None, row_off=None):
+    """crates/cuda/csrc/dflash2.cu:436-519 (walk_kernel). ids / vals [rows total, k]; gate [rows total, rank] as f32 or
+    as bf16 bits (u16); codebooks as f16 bits (u16) [V, rank]. Returns (tokens, conf, margin) per row."""
+    anchor = np.ascontiguousarray(anchor, dtype=np.int32)
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    vals = np.ascontiguousarray(vals, dtype=np.float32)
+    gate = np.ascontiguousarray(gate, dtype=np.float32 if gate_f32 else np.uint16)
+    pred_cb = np.ascontiguousarray(pred_cb, dtype=np.uint16)
+    succ_cb = np.ascontiguousarray(succ_cb, dtype=np.uint16)
+    total, k = ids.shape
+    rank = gate.shape[-1]
+    ws = None if sampling is None else np.ascontiguousarray(sampling, dtype=WALK_SAMPLING_DTYPE)
+    ro = None if row_off is None else np.ascontiguousarray(row_off, dtype=np.int32)
+    out = np.zeros(total, np.int32)
+    conf = np.zeros(total, np.float32)
+    margin = np.zeros(total, np.float32)
+    lib().gbo_selector_walk(_p(anchor), _p(ids), _p(vals), _p(gate), 1 if gate_f32 else 0, _p(pred_cb), _p(succ_cb), n_seq, rows, k,
+                            rank, _p(ws), _p(ro), _p(out), _p(conf), _p(margin))
+    return out, conf, margin
+

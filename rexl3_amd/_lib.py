@@ -25,6 +25,9 @@ SIGNATURES = {
     "gb_glm_topk_f16": (I, [P, I, I, I, I, P, P, P, Z, P]),
     "gb_ling_topk_f16_workspace_bytes": (Z, [I, I, I]),
     "gb_ling_topk_f16": (I, [P, I, I, I, I, P, P, P, Z, P]),
+    "gb_dflash_selector_walk_keyed": (I, [P, P, P, P, I, P, P, I, I, I, I, P, P, P, P]),
+    "gb_dflash_selector_walk_ragged": (I, [P, P, P, P, I, P, P, I, I, I, P, P, P, P, P, P]),
+    "gb_dflash_selector_walk": (I, [P, P, P, P, I, P, P, I, I, I, I, P, P, P]),
     "gb_glm_keyed_pick": (I, [P, P, I, I, P, I, P, P, P]),
     "gb_qfn_greedy_gather": (I, [P, P, I, I, P, P, P]),
     "gbs_workspace_clear": (I, [P, Z, P]),

@@ -10,6 +10,8 @@
 //    leaves the device.
 //  - gbs_accept / gbs_accept_tree: crates/spec/src/lib.rs:30-35 and crates/spec/src/tree.rs:417-438.
 //  - gbs_tree_verify: a tree round on the device, keyed draws at each node's position then the accept walk.
+#include <hip/hip_fp16.h>
+
 #include "gbs_select.hpp"
 
 using namespace gbs;
@@ -456,6 +458,144 @@ __global__ void __launch_bounds__(KNT, 1) keyed_fast_k(const void* logits, long 
     }
 }
 
+// ------------------------------------------------------------------------------------------------ selector walk
+// The draft head's selector chain walk (crates/cuda/csrc/dflash2.cu:436-519, 595-660): per sequence, each draft row's
+// candidates are scored as unary[c] + <pred[prev] * gate[row], succ[c]> and the row's pick becomes the next row's
+// predecessor. One block of WT threads per sequence. The dot products follow the reference kernel's arithmetic (32-lane
+// groups: lane l sums r = l, l + 32, ... with fused multiply-adds, then an xor butterfly over offsets 16 .. 1), so a
+// score is the same float; half-waves play the 32-lane groups. The pick is `keyed_choose` (the reference's device
+// try_choose over all k candidates, NaN scores last, with the winner's margin) for a keyed sequence, else the first
+// maximum.
+
+struct WalkSamplingDev {
+    u64 seed, first_position;
+    double temperature, top_p, min_p;
+    int keyed, pad;
+};
+static_assert(sizeof(WalkSamplingDev) == 48, "WalkSampling is 48 bytes");
+
+constexpr int WT = 256;
+
+// crates/cuda/csrc/keyed.cuh:50-112, on one thread, in the reference's order of operations
+__device__ int keyed_choose_serial(const float* scores, const int* c_row, int k, u64 seed, double temperature, double top_p, double min_p,
+                                   u64 position, float* margin, double* pr) {
+    int ord[64];
+    for (int i = 0; i < k; ++i) {
+        int j = i;
+        while (j > 0) {
+            const float va = scores[ord[j - 1]], vb = scores[i];
+            const bool before = (vb > va) || (vb == va && c_row[i] < c_row[ord[j - 1]]) || (va != va && vb == vb);
+            if (!before) break;
+            ord[j] = ord[j - 1];
+            --j;
+        }
+        ord[j] = i;
+    }
+    if (temperature == 0.0) {
+        *margin = k > 1 ? scores[ord[0]] - scores[ord[1]] : 30.f;
+        return ord[0];
+    }
+    const double t = temperature > 1e-6 ? temperature : 1e-6;
+    int keep = k;
+    if (top_p > 0.0 && top_p < 1.0) {
+        const double mx = (double)scores[ord[0]] / t;
+        for (int i = 0; i < k; ++i) pr[i] = exp((double)scores[ord[i]] / t - mx);
+        const double total = pairwise_small(pr, k);
+        double c = 0.0;
+        int below = 0;
+        for (int i = 0; i < k; ++i) {
+            c += pr[i] / total;
+            if (c < top_p) ++below;
+        }
+        keep = below + 1 < k ? below + 1 : k;
+    }
+    if (min_p > 0.0) {
+        const double floor_v = (double)scores[ord[0]] / t + log(min_p);
+        int n = 0;
+        for (int i = 0; i < keep; ++i)
+            if ((double)scores[ord[i]] / t >= floor_v) ++n;
+        keep = n > 1 ? n : 1;
+    }
+    int best = 0;
+    double best_score = -INFINITY, second_score = -INFINITY;
+    for (int i = 0; i < keep; ++i) {
+        const double u = keyed_uniform(seed, position, (u64)(u32)c_row[ord[i]]);
+        const double score = (double)scores[ord[i]] / t + (-log(-log(u)));
+        if (score > best_score) {
+            second_score = best_score;
+            best_score = score;
+            best = i;
+        } else if (score > second_score) {
+            second_score = score;
+        }
+    }
+    *margin = keep > 1 ? (float)fmin(best_score - second_score, 30.0) : 30.f;
+    return ord[best];
+}
+
+__global__ void __launch_bounds__(WT) walk_k(const int* __restrict__ anchor, const int* __restrict__ ids, const float* __restrict__ vals,
+                                             const void* __restrict__ gate, int gate_f32, const __half* __restrict__ pred_cb,
+                                             const __half* __restrict__ succ_cb, int* __restrict__ out, float* __restrict__ conf, int rows,
+                                             int k, int rank, const WalkSamplingDev* __restrict__ ws, const int* __restrict__ row_off,
+                                             float* __restrict__ margin) {
+    extern __shared__ float smem[];
+    float* a_g = smem;            // [rank]
+    float* scores = smem + rank;  // [k]
+    __shared__ int s_pred;
+    __shared__ double s_pr[64];
+    const int b = blockIdx.x, t = threadIdx.x;
+    const int grp = t / 32, gl = t % 32;  // 32-lane groups (half-waves), as the reference's warps
+    const int base = row_off ? row_off[b] : b * rows;
+    const int nrows = row_off ? row_off[b + 1] - base : rows;
+    if (t == 0) s_pred = anchor[b];
+    __syncthreads();
+    for (int i = 0; i < nrows; ++i) {
+        const size_t row = (size_t)(base + i);
+        const __half* a_row = pred_cb + (size_t)s_pred * rank;
+        for (int r = t; r < rank; r += WT) {
+            const float g = gate_f32 ? ((const float*)gate)[row * rank + r]
+                                     : __uint_as_float((u32)((const u16*)gate)[row * rank + r] << 16);
+            a_g[r] = __half2float(a_row[r]) * g;
+        }
+        __syncthreads();
+        const int* c_row = ids + row * k;
+        const float* u_row = vals + row * k;
+        for (int c = grp; c < k; c += WT / 32) {
+            const __half* b_row = succ_cb + (size_t)c_row[c] * rank;
+            float dot = 0.f;
+            for (int r = gl; r < rank; r += 32) dot = fmaf(a_g[r], __half2float(b_row[r]), dot);
+#pragma unroll
+            for (int o = 16; o > 0; o >>= 1) dot += __shfl_xor(dot, o, 32);
+            if (gl == 0) scores[c] = u_row[c] + dot;
+        }
+        __syncthreads();
+        if (t == 0) {
+            int best = 0;
+            float bs = scores[0], mg = 30.f;
+            if (ws != nullptr && ws[b].keyed) {
+                best = keyed_choose_serial(scores, c_row, k, ws[b].seed, ws[b].temperature, ws[b].top_p, ws[b].min_p,
+                                           ws[b].first_position + (u64)i, &mg, s_pr);
+                bs = scores[best];
+            } else {
+                for (int c = 1; c < k; ++c)
+                    if (scores[c] > bs) {
+                        bs = scores[c];
+                        best = c;
+                    }
+                float second = -INFINITY;
+                for (int c = 0; c < k; ++c)
+                    if (c != best && scores[c] > second) second = scores[c];
+                mg = k > 1 ? fminf(bs - second, 30.f) : 30.f;
+            }
+            s_pred = c_row[best];
+            out[row] = s_pred;
+            if (conf) conf[row] = bs;
+            if (margin) margin[row] = mg;
+        }
+        __syncthreads();
+    }
+}
+
 // ------------------------------------------------------------------------------------------------ accept steps
 
 __global__ void accept_k(const int* __restrict__ drafts, const int* __restrict__ samples, int n_seq, int width, int* accepted) {
@@ -652,6 +792,45 @@ GBS_EXPORT int gbs_tree_verify(const void* logits, int dtype, int n_tree, int no
     hipLaunchKernelGGL(accept_tree_ok_k, dim3((n_tree + 63) / 64), dim3(64), 0, to_stream(stream), tokens, parents, out_samples, tst,
                        n_tree, nodes, out_path, out_path_len);
     return launch_status();
+}
+
+namespace {
+int launch_walk(const void* anchor, const void* topk_ids, const void* topk_vals, const void* gate, int gate_is_f32,
+                const void* pred_codebook, const void* succ_codebook, int n_seq, int rows, int k, int rank, const void* sampling,
+                const void* row_off, void* out_tokens, void* conf, void* margin, void* stream) {
+    const size_t smem = (size_t)(rank + k) * sizeof(float);
+    hipLaunchKernelGGL(walk_k, dim3(n_seq), dim3(WT), smem, to_stream(stream), (const int*)anchor, (const int*)topk_ids,
+                       (const float*)topk_vals, gate, gate_is_f32, (const __half*)pred_codebook, (const __half*)succ_codebook,
+                       (int*)out_tokens, (float*)conf, rows, k, rank, (const WalkSamplingDev*)sampling, (const int*)row_off,
+                       (float*)margin);
+    return launch_status();
+}
+}  // namespace
+
+GBS_EXPORT int gb_dflash_selector_walk_keyed(const void* anchor, const void* topk_ids, const void* topk_vals, const void* gate,
+                                             int gate_is_f32, const void* pred_codebook, const void* succ_codebook, int n_seq, int rows,
+                                             int k, int rank, const void* sampling, void* out_tokens, void* conf, void* stream) {
+    if (n_seq <= 0 || rows <= 0) return 0;
+    if (k < 1 || k > 64 || rank < 1 || rank > 8192) return GBS_ERR_INVALID;
+    return launch_walk(anchor, topk_ids, topk_vals, gate, gate_is_f32, pred_codebook, succ_codebook, n_seq, rows, k, rank, sampling,
+                       nullptr, out_tokens, conf, nullptr, stream);
+}
+
+GBS_EXPORT int gb_dflash_selector_walk_ragged(const void* anchor, const void* topk_ids, const void* topk_vals, const void* gate,
+                                              int gate_is_f32, const void* pred_codebook, const void* succ_codebook, int n_seq, int k,
+                                              int rank, const void* sampling, const void* row_off, void* out_tokens, void* conf,
+                                              void* margin, void* stream) {
+    if (n_seq <= 0) return 0;
+    if (k < 1 || k > 64 || rank < 1 || rank > 8192 || !row_off) return GBS_ERR_INVALID;
+    return launch_walk(anchor, topk_ids, topk_vals, gate, gate_is_f32, pred_codebook, succ_codebook, n_seq, 0, k, rank, sampling,
+                       row_off, out_tokens, conf, margin, stream);
+}
+
+GBS_EXPORT int gb_dflash_selector_walk(const void* anchor, const void* topk_ids, const void* topk_vals, const void* gate, int gate_is_f32,
+                                       const void* pred_codebook, const void* succ_codebook, int n_seq, int rows, int k, int rank,
+                                       void* out_tokens, void* conf, void* stream) {
+    return gb_dflash_selector_walk_keyed(anchor, topk_ids, topk_vals, gate, gate_is_f32, pred_codebook, succ_codebook, n_seq, rows, k,
+                                         rank, nullptr, out_tokens, conf, stream);
 }
 
 GBS_EXPORT const char* gbs_version(void) { return "gbsample-hip 0.1 (gfx950)"; }

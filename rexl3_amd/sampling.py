@@ -143,6 +143,36 @@ def topk_f16_single_launch(logits: torch.Tensor, count: int, valid: int | None =
     return ids, vals
 
 
+WALK_SAMPLING_DTYPE = np.dtype([("seed", "<u8"), ("first_position", "<u8"), ("temperature", "<f8"), ("top_p", "<f8"),
+                                ("min_p", "<f8"), ("keyed", "<i4"), ("pad", "<i4")])
+
+
+def selector_walk(anchor: torch.Tensor, topk_ids: torch.Tensor, topk_vals: torch.Tensor, gate: torch.Tensor,
+                  pred_codebook: torch.Tensor, succ_codebook: torch.Tensor, sampling: np.ndarray | None = None,
+                  row_off: torch.Tensor | None = None):
+    """The draft head's selector walk (gb_dflash_selector_walk_keyed, or _ragged when row_off is given;
+    crates/cuda/src/dflash2.rs). topk_ids / topk_vals [rows total, k]; gate [rows total, rank] bf16 or f32; codebooks
+    f16 [V, rank]; sampling: WALK_SAMPLING_DTYPE per sequence or None. Returns (tokens, conf, margin or None)."""
+    dev = topk_ids.device
+    n_seq = anchor.shape[0]
+    rows_total, k = topk_ids.shape
+    rank = gate.shape[-1]
+    out = torch.empty(rows_total, dtype=torch.int32, device=dev)
+    conf = torch.empty(rows_total, dtype=torch.float32, device=dev)
+    ws = None
+    if sampling is not None:
+        ws = torch.from_numpy(np.ascontiguousarray(sampling, dtype=WALK_SAMPLING_DTYPE).view(np.uint8)).to(dev)
+    g32 = 1 if gate.dtype == torch.float32 else 0
+    if row_off is None:
+        _lib.call("gb_dflash_selector_walk_keyed", _ptr(anchor), _ptr(topk_ids), _ptr(topk_vals), _ptr(gate), g32, _ptr(pred_codebook),
+                  _ptr(succ_codebook), n_seq, rows_total // n_seq, k, rank, _ptr(ws), _ptr(out), _ptr(conf), _stream(dev))
+        return out, conf, None
+    margin = torch.empty(rows_total, dtype=torch.float32, device=dev)
+    _lib.call("gb_dflash_selector_walk_ragged", _ptr(anchor), _ptr(topk_ids), _ptr(topk_vals), _ptr(gate), g32, _ptr(pred_codebook),
+              _ptr(succ_codebook), n_seq, k, rank, _ptr(ws), _ptr(row_off), _ptr(out), _ptr(conf), _ptr(margin), _stream(dev))
+    return out, conf, margin
+
+
 def keyed_rows(samplings, positions) -> np.ndarray:
     """KeyedRow records (crates/cuda/csrc/glm_mtp.cu:258-264) for a list of Sampling and absolute positions."""
     recs = np.zeros(len(samplings), dtype=KEYED_ROW_DTYPE)
