@@ -271,7 +271,7 @@ __device__ __forceinline__ u64 wave_max_u64(u64 v) {
 
 __device__ __forceinline__ u32 wave_or(u32 v) {
 #pragma unroll
-    for (int m = 1; m < WAVE; m <<= 1) v |= (u32)__shfl_xor((int)v, m, WAVE);
+    for (int m = 1; m < WAVE; m <<= 1) v |= xor_lane(v, m);
     return v;
 }
 

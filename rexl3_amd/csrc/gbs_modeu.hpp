@@ -162,5 +162,17 @@ __device__ __forceinline__ Lse lse_merge(Lse a, Lse b, float c) {
     return Lse{M, a.s * exp2f((a.m - M) * c) + b.s * exp2f((b.m - M) * c)};
 }
 
+// The wave's total of per-lane online log-sum-exp pairs, in every lane: the maximum first, then each lane's sum
+// rescaled to it once and summed (cross-lane moves by DPP and permlane swaps, no LDS). A lane at -inf adds 0.
+__device__ __forceinline__ Lse wave_lse(Lse a, float c) {
+    float M = a.m;
+#pragma unroll
+    for (int m = 1; m < WAVE; m <<= 1) M = fmaxf(M, __uint_as_float(xor_lane(__float_as_uint(M), m)));
+    float s = a.m == -INFINITY ? 0.0f : a.s * exp2f((a.m - M) * c);
+#pragma unroll
+    for (int m = 1; m < WAVE; m <<= 1) s += __uint_as_float(xor_lane(__float_as_uint(s), m));
+    return Lse{M, s};
+}
+
 }  // namespace modeu
 }  // namespace gbs

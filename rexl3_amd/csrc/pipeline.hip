@@ -581,24 +581,27 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
         return;
     }
     // block reduction: lists, LSE, NaN
-    if (LOGPROB) {
-#pragma unroll
-        for (int m = 1; m < WAVE; m <<= 1) {
-            Lse o{__shfl_xor(lse.m, m, WAVE), __shfl_xor(lse.s, m, WAVE)};
-            lse = lse_merge(lse, o, clp);
-        }
-    }
+    if (LOGPROB) lse = wave_lse(lse, clp);
     const bool wnan = ballot(nanv != 0u) != 0ull;
+    Lse rl{-INFINITY, 0.f};
+    unsigned rn = 0;
+    u64 list;
+#if GBS_EXP_TIMES
+    u64 t_bar = 0, t_merge = 0;
+#endif
     if (l == 0) {
         s_lse[w] = lse;
         s_nan[w] = wnan ? 1u : 0u;
     }
+#if GBS_EXP_TIMES
+    __syncthreads();
+    t_bar = wall_clock64();
+#endif
     wt.list = block_tree_merge<NW>(wt.list, s_list);  // also orders s_lse / s_nan before the reads below
-    Lse rl{-INFINITY, 0.f};
-    unsigned rn = 0;
-    u64 list;
+#if GBS_EXP_TIMES
+    t_merge = wall_clock64();
+#endif
     if (S == 1) {
-        // the whole row in this block: no hand-off through device memory
         if (w != 0) return;
         if (l < NW) {
             rl = s_lse[l];
@@ -631,14 +634,7 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
             rn |= ld_agent(&ws.nan[(size_t)r * S + o]);
         }
     }
-    if (LOGPROB) {
-        // only the first `span` lanes hold partial sums: a butterfly over them leaves the total in lane 0
-        const int span = S == 1 ? NW : (S < WAVE ? S : WAVE);
-        for (int m = 1; m < span; m <<= 1) {
-            Lse o{__shfl_xor(rl.m, m, WAVE), __shfl_xor(rl.s, m, WAVE)};
-            rl = lse_merge(rl, o, clp);
-        }
-    }
+    if (LOGPROB) rl = wave_lse(rl, clp);  // lanes without a partial hold (-inf, 0)
     rn = wave_or(rn);
 #if GBS_EXP_NOFINISH2
     if (l == 0) out_ids[r] = (int)(list >> 40) + (int)rn + (int)rl.s;
@@ -659,6 +655,7 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
         out_ids[r] = (int)(mn - t_start) | ((int)(s_tseed - t_start) << 16);
         out_probs[r] = (float)(mx - t_start);
         out_logprobs[r] = (float)(t_end - t_start);
+        out_status[r] = (int)(t_bar - t_start) | ((int)(t_merge - t_start) << 16);
 #endif
     }
 }

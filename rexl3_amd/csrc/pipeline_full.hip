@@ -508,10 +508,7 @@ __global__ void __launch_bounds__(NTF) sample_full_k(const void* __restrict__ lo
             }
         }
     });
-    for (int m = 1; m < WAVE; m <<= 1) {
-        const Lse o{__shfl_xor(lse.m, m, WAVE), __shfl_xor(lse.s, m, WAVE)};
-        lse = lse_merge(lse, o, clp);
-    }
+    lse = wave_lse(lse, clp);
     if (l == 0) {
         sh.lse_m[w] = lse.m;
         sh.lse_s[w] = lse.s;
@@ -786,10 +783,7 @@ __global__ void __launch_bounds__(NTF) fs_pass0_k(const void* __restrict__ logit
             }
         }
     });
-    for (int m = 1; m < WAVE; m <<= 1) {
-        const Lse o{__shfl_xor(lse.m, m, WAVE), __shfl_xor(lse.s, m, WAVE)};
-        lse = lse_merge(lse, o, clp);
-    }
+    lse = wave_lse(lse, clp);
     if (l == 0) {
         s_lm[w] = lse.m;
         s_ls[w] = lse.s;
