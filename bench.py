@@ -46,7 +46,7 @@ def profiled_traffic(workload):
     recorded in profiles/; None when no measurement of this workload is recorded."""
     import re
     path = os.path.join(ROOT, "profiles", {"northstar": "sample_fast_k_northstar.md", "keyed": "keyed_fast_k_b256.md",
-                                           "c5": "spec_verify_config5.md", "c3": "sample_full_k_config3.md"}.get(workload, ""))
+                                           "c5": "spec_verify_config5.md", "c3": "fs_split_kernels_config3.md"}.get(workload, ""))
     if not os.path.isfile(path):
         return None
     m = re.search(r"traffic_bytes_per_launch:\s*(\d+)", open(path).read())
@@ -145,7 +145,8 @@ def main():
 
         ms = time_launches(launch, args.steps, args.warmup)
         nbytes = algorithmic_bytes(rows, vocab, 2 if is_bf16 else 4, ct is not None, mt is not None)
-        kernel = "sample_full_k" if kmax == 0 else "sample_fast_k"
+        # the full path (kmax 0) runs split over fs_* launches when there are fewer rows than CUs
+        kernel = ("fs_pass0_k + fs_hist_k + fs_collect_k" if rows < 256 else "sample_full_k") if kmax == 0 else "sample_fast_k"
         dtype = "bf16->f32" if is_bf16 else "f32"
         workload = {"northstar": "extended pipeline: penalties (dense i32 counts) + u32 grammar mask + T 0.8 + top-k 50 / top-p 0.9"
                                  " + log-softmax + inverse-CDF draw",

@@ -113,6 +113,35 @@ struct Row {
 
 __device__ __forceinline__ bool valid_l(float v) { return v > -INFINITY; }  // false for NaN and -inf
 
+// Pass 0 of a lane, one 4-element group at a time: the largest allowed value and its lowest id (the row's greedy key;
+// -0 and +0 share a key, so float comparisons order values as the keys do), the NaN flag, the number of allowed tokens
+// and the online log-sum-exp in base 2 (rescaled once per group, at the group's maximum).
+struct Pass0Acc {
+    float bv = -INFINITY;
+    u32 bid = 0, nan = 0, nallowed = 0;
+    Lse lse{-INFINITY, 0.f};
+
+    __device__ __forceinline__ void add(const float (&l)[4], int e, float c) {
+        nan |= (__builtin_isunordered(l[0], l[1]) | __builtin_isunordered(l[2], l[3])) ? 1u : 0u;
+        nallowed += (u32)valid_l(l[0]) + (u32)valid_l(l[1]) + (u32)valid_l(l[2]) + (u32)valid_l(l[3]);
+        const float gm = fmaxf(fmaxf(l[0], l[1]), fmaxf(l[2], l[3]));  // NaN only when all four are NaN
+        if (gm > bv) {  // strictly: on a tie the earlier (lower) id stays
+            bv = gm;
+            bid = (u32)e + (l[0] == gm ? 0u : l[1] == gm ? 1u : l[2] == gm ? 2u : 3u);
+        }
+        if (gm > lse.m) {
+            lse.s = lse.m == -INFINITY ? 0.f : lse.s * __builtin_amdgcn_exp2f((lse.m - gm) * c);
+            lse.m = gm;
+        }
+        if (lse.m != -INFINITY) {
+            const float mc = lse.m * c;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) lse.s += __builtin_amdgcn_exp2f(__builtin_fmaf(l[q], c, -mc));
+        }
+    }
+    __device__ __forceinline__ u64 key() const { return bv > -INFINITY ? make_key(okey_f32(bv), bid) : 0ull; }
+};
+
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t full_rsrc(const void* base, u32 bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
@@ -449,16 +478,11 @@ __device__ bool binned_cut(const Row<DT, COUNTS, MASK>& R, float M, float c2, fl
 }
 
 template <int DT, bool COUNTS, bool MASK>
-__global__ void __launch_bounds__(NTF) sample_full_k(const void* __restrict__ logits, long long stride, int vocab,
-                                                     const int* __restrict__ counts, const u32* __restrict__ mask,
-                                                     const RowParamsDev* __restrict__ params, const float* __restrict__ uniforms, bool vec,
-                                                     int* __restrict__ out_ids, int* __restrict__ out_greedy, float* __restrict__ out_probs,
-                                                     float* __restrict__ out_logprobs, int* __restrict__ out_status,
-                                                     const FsRow* __restrict__ only_radix) {
-    __shared__ Shared sh;
-    const int r = blockIdx.x;
-    // after the split path: only the rows it handed to the radix path
-    if (only_radix && ld_agent(&only_radix[r].state) != FS_RADIX) return;
+__device__ __forceinline__ void full_row(const void* __restrict__ logits, long long stride, int vocab, const int* __restrict__ counts,
+                                         const u32* __restrict__ mask, const RowParamsDev* __restrict__ params,
+                                         const float* __restrict__ uniforms, bool vec, int* __restrict__ out_ids,
+                                         int* __restrict__ out_greedy, float* __restrict__ out_probs, float* __restrict__ out_logprobs,
+                                         int* __restrict__ out_status, int r, Shared& sh) {
     const int tid = threadIdx.x, w = tid / WAVE, l = lane_id();
     const RowParamsDev p = params[r];
     const float u = uniforms[r];
@@ -489,26 +513,11 @@ __global__ void __launch_bounds__(NTF) sample_full_k(const void* __restrict__ lo
     }
 
     // ---- pass 0: maximum, NaN, allowed count, log-sum-exp
-    u64 kmaxv = 0;
-    u32 nan = 0, nallowed = 0;
-    Lse lse{-INFINITY, 0.f};
-    stream_tiles(R, [&](int, int e, const float (&lv)[4]) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            nan |= lv[q] != lv[q];
-            if (valid_l(lv[q])) {
-                ++nallowed;
-                const u64 k = make_key(okey_f32(lv[q]), (u32)(e + q));
-                kmaxv = k > kmaxv ? k : kmaxv;
-                if (lv[q] > lse.m) {
-                    lse.s = lse.m == -INFINITY ? 0.f : lse.s * exp2f((lse.m - lv[q]) * clp);
-                    lse.m = lv[q];
-                }
-                lse.s += exp2f((lv[q] - lse.m) * clp);
-            }
-        }
-    });
-    lse = wave_lse(lse, clp);
+    Pass0Acc acc;
+    stream_tiles(R, [&](int, int e, const float (&lv)[4]) { acc.add(lv, e, clp); });
+    const u64 kmaxv = acc.key();
+    const u32 nan = acc.nan, nallowed = acc.nallowed;
+    const Lse lse = wave_lse(acc.lse, clp);
     if (l == 0) {
         sh.lse_m[w] = lse.m;
         sh.lse_s[w] = lse.s;
@@ -631,6 +640,18 @@ __global__ void __launch_bounds__(NTF) sample_full_k(const void* __restrict__ lo
     finish(id, greedy, GBS_ROW_OK, (float)((double)ec / (double)z), logprob_of(lx));
 }
 
+// One block of NTF threads per row: the whole row in one block (batches of at least as many rows as CUs).
+template <int DT, bool COUNTS, bool MASK>
+__global__ void __launch_bounds__(NTF) sample_full_k(const void* __restrict__ logits, long long stride, int vocab,
+                                                     const int* __restrict__ counts, const u32* __restrict__ mask,
+                                                     const RowParamsDev* __restrict__ params, const float* __restrict__ uniforms, bool vec,
+                                                     int* __restrict__ out_ids, int* __restrict__ out_greedy, float* __restrict__ out_probs,
+                                                     float* __restrict__ out_logprobs, int* __restrict__ out_status) {
+    __shared__ Shared sh;
+    full_row<DT, COUNTS, MASK>(logits, stride, vocab, counts, mask, params, uniforms, vec, out_ids, out_greedy, out_probs, out_logprobs,
+                               out_status, (int)blockIdx.x, sh);
+}
+
 // ================================================================================================== the split path
 // Batches with fewer rows than CUs: S blocks per row, block sp over whole tiles [sp * tpb, (sp + 1) * tpb). Three
 // launches, each with a last-block hand-off per row (agent-scope stores and loads, an arrival counter):
@@ -640,8 +661,9 @@ __global__ void __launch_bounds__(NTF) sample_full_k(const void* __restrict__ lo
 //   fs_hist_k     the binned cut's mass histogram (rows with top-p); the last block sums the blocks' histograms and
 //                 finds the crossing bin
 //   fs_collect_k  kept masses per tile and the crossing bin's tokens; the last block finds the exact top-p key, the
-//                 tile that holds the draw, and the token
-// then sample_full_k for the rows marked for the radix path (and rows whose crossing bin held more than CAP tokens).
+//                 tile that holds the draw, and the token. A row marked for the radix path is taken by its first block
+//                 (the single-block path, full_row), and so is a row whose crossing bin held more than CAP tokens, by its
+//                 last block.
 constexpr int FS_TARGET_BLOCKS = 256;
 constexpr int FS_MAX_SPLITS = 128;
 
@@ -764,26 +786,11 @@ __global__ void __launch_bounds__(NTF) fs_pass0_k(const void* __restrict__ logit
     const float clp = fs_clp(p);
     const int ntiles = (vocab + TILE - 1) / TILE;
     const int t0 = sp * tpb, t1 = min(ntiles, t0 + tpb);
-    u64 kmaxv = 0;
-    u32 nan = 0, nallowed = 0;
-    Lse lse{-INFINITY, 0.f};
-    stream_tiles(R, t0, t1, [&](int, int e, const float (&lv)[4]) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            nan |= lv[q] != lv[q];
-            if (valid_l(lv[q])) {
-                ++nallowed;
-                const u64 k = make_key(okey_f32(lv[q]), (u32)(e + q));
-                kmaxv = k > kmaxv ? k : kmaxv;
-                if (lv[q] > lse.m) {
-                    lse.s = lse.m == -INFINITY ? 0.f : lse.s * exp2f((lse.m - lv[q]) * clp);
-                    lse.m = lv[q];
-                }
-                lse.s += exp2f((lv[q] - lse.m) * clp);
-            }
-        }
-    });
-    lse = wave_lse(lse, clp);
+    Pass0Acc acc;
+    stream_tiles(R, t0, t1, [&](int, int e, const float (&lv)[4]) { acc.add(lv, e, clp); });
+    const u64 kmaxv = acc.key();
+    const u32 nan = acc.nan, nallowed = acc.nallowed;
+    const Lse lse = wave_lse(acc.lse, clp);
     if (l == 0) {
         s_lm[w] = lse.m;
         s_ls[w] = lse.s;
@@ -929,18 +936,30 @@ __global__ void __launch_bounds__(NTF) fs_collect_k(const void* __restrict__ log
                                                     bool vec, int tpb, FsWs ws, int* __restrict__ out_ids, int* __restrict__ out_greedy,
                                                     float* __restrict__ out_probs, float* __restrict__ out_logprobs,
                                                     int* __restrict__ out_status) {
-    __shared__ u64 s_key[CAP], s_mass[CAP];
-    __shared__ u64 s_tilew[MAX_TILES][NWF];
-    __shared__ u64 s_tile[MAX_TILES];
-    __shared__ u64 s_red[NWF];
-    __shared__ u64 s_bc[4];
-    __shared__ u32 s_ncol, s_off[FS_MAX_SPLITS + 1];
+    // the collection's arrays live in the radix path's LDS record (the two never run at the same time)
+    __shared__ Shared sh;
+    u64* const s_key = sh.maxk;
+    u64* const s_mass = sh.mass;
+    u64 (*const s_tilew)[NWF] = sh.tilew;
+    u64* const s_tile = sh.tile;
+    u64* const s_red = sh.red;
+    u64* const s_bc = sh.bc;
+    u32& s_ncol = sh.ncol;
+    __shared__ u32 s_off[FS_MAX_SPLITS + 1];
     __shared__ unsigned s_flag;
     const int S = gridDim.x, sp = blockIdx.x, r = blockIdx.y;
     const int tid = threadIdx.x, w = tid / WAVE, l = lane_id();
     const RowParamsDev p = params[r];
     const FsRow* row = &ws.rows[r];
-    if (ld_agent(&row->state) != FS_CUT) return;
+    const u32 state0 = ld_agent(&row->state);
+    if (state0 == FS_RADIX) {
+        // marked by pass 0 (top-k with a cut, an infinite maximum or 1/T): the row's first block takes the radix path
+        if (sp == 0)
+            full_row<DT, COUNTS, MASK>(logits, stride, vocab, counts, mask, params, uniforms, vec, out_ids, out_greedy, out_probs,
+                                       out_logprobs, out_status, r, sh);
+        return;
+    }
+    if (state0 != FS_CUT) return;
     const Row<DT, COUNTS, MASK> R = make_row<DT, COUNTS, MASK>(logits, stride, vocab, counts, mask, p, vec, r);
     const u64 top = ld_agent(&row->top);
     const float M = okey_to_f32(key_ok(top));
@@ -1014,7 +1033,9 @@ __global__ void __launch_bounds__(NTF) fs_collect_k(const void* __restrict__ log
     __syncthreads();
     const u32 n = s_off[S];
     if (n > (u32)CAP) {  // every block's count is at most the total: no block overflowed unless the total did
-        if (tid == 0) st_agent(&ws.rows[r].state, (u32)FS_RADIX);
+        // more tokens in the crossing bin than the collection holds: this block takes the radix path for the row
+        full_row<DT, COUNTS, MASK>(logits, stride, vocab, counts, mask, params, uniforms, vec, out_ids, out_greedy, out_probs,
+                                   out_logprobs, out_status, r, sh);
         return;
     }
     for (int o = 0; o < S; ++o) {
@@ -1125,7 +1146,6 @@ int launch_sample_full(const void* logits, int dtype, int rows, int stride, int 
     const bool split = pl.S >= 2;
     if (split && (!ws || !aligned(ws, 256) || ws_bytes < pl.bytes)) return GBS_ERR_INVALID;
     const FsWs w = split ? fs_carve(ws, rows, pl) : FsWs{};
-    const FsRow* only = split ? w.rows : nullptr;
     auto run = [&]<int D, bool C, bool Mk>() {
         if (split) {
             const dim3 grid(pl.S, rows);
@@ -1136,8 +1156,9 @@ int launch_sample_full(const void* logits, int dtype, int rows, int stride, int 
             hipLaunchKernelGGL((fs_collect_k<D, C, Mk>), grid, dim3(NTF), 0, st, logits, (long long)stride, vocab, counts, mask, p,
                                uniforms, vec, pl.tpb, w, out_ids, out_greedy, out_probs, out_logprobs, out_status);
         }
-        hipLaunchKernelGGL((sample_full_k<D, C, Mk>), dim3(rows), dim3(NTF), 0, st, logits, (long long)stride, vocab, counts, mask, p,
-                           uniforms, vec, out_ids, out_greedy, out_probs, out_logprobs, out_status, only);
+        else
+            hipLaunchKernelGGL((sample_full_k<D, C, Mk>), dim3(rows), dim3(NTF), 0, st, logits, (long long)stride, vocab, counts, mask,
+                               p, uniforms, vec, out_ids, out_greedy, out_probs, out_logprobs, out_status);
     };
     const bool c = counts != nullptr, m = mask != nullptr;
     if (dtype == GBS_DTYPE_F32) {
