@@ -358,9 +358,8 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
                 lse.m = gm;
             }
             if (lse.m != -INFINITY) {
-                const float mc = lse.m * lse_c;
 #pragma unroll
-                for (int q = 0; q < 4; ++q) lse.s += __builtin_amdgcn_exp2f(__builtin_fmaf(lv[q], lse_c, -mc));
+                for (int q = 0; q < 4; ++q) lse.s += __builtin_amdgcn_exp2f((lv[q] - lse.m) * lse_c);
             }
         }
     };
@@ -444,9 +443,10 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
                 }
                 // a half that is -inf on every lane adds exactly 0
                 if (lse.m != -INFINITY && ballot(gm != -INFINITY)) {
-                    const float mc = lse.m * lse_c;
+                    // the difference first: exact for values near the maximum at any magnitude (a product l * c
+                    // rounded at |l| ~ 1e6 would shift every exponent by up to ulp(l * c))
 #pragma unroll
-                    for (int i = 0; i < NE; ++i) lse.s += __builtin_amdgcn_exp2f(__builtin_fmaf(lv[i], lse_c, -mc));
+                    for (int i = 0; i < NE; ++i) lse.s += __builtin_amdgcn_exp2f((lv[i] - lse.m) * lse_c);
                 }
             }
         };

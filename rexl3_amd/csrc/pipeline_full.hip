@@ -134,9 +134,9 @@ struct Pass0Acc {
             lse.m = gm;
         }
         if (lse.m != -INFINITY) {
-            const float mc = lse.m * c;
+            // the difference first: exact near the maximum at any magnitude
 #pragma unroll
-            for (int q = 0; q < 4; ++q) lse.s += __builtin_amdgcn_exp2f(__builtin_fmaf(l[q], c, -mc));
+            for (int q = 0; q < 4; ++q) lse.s += __builtin_amdgcn_exp2f((l[q] - lse.m) * c);
         }
     }
     __device__ __forceinline__ u64 key() const { return bv > -INFINITY ? make_key(okey_f32(bv), bid) : 0ull; }
@@ -1022,13 +1022,16 @@ __global__ void __launch_bounds__(NTF) fs_collect_k(const void* __restrict__ log
     }
     if (!arrive_last(&ws.cnt2[r], (unsigned)S, &s_flag)) return;
     // ---- the row's last block: gather the collected tokens (or hand the row to the radix path)
+    // the blocks' counts (one load per thread), then their offsets
+    if (tid < S) s_off[tid + 1] = ld_agent(&ws.ccount[(size_t)r * S + tid]);
+    __syncthreads();
     if (tid == 0) {
         u32 off = 0;
+        s_off[0] = 0;
         for (int o = 0; o < S; ++o) {
-            s_off[o] = off;
-            off += ld_agent(&ws.ccount[(size_t)r * S + o]);
+            off += s_off[o + 1];
+            s_off[o + 1] = off;
         }
-        s_off[S] = off;
     }
     __syncthreads();
     const u32 n = s_off[S];
@@ -1052,11 +1055,24 @@ __global__ void __launch_bounds__(NTF) fs_collect_k(const void* __restrict__ log
         // the collected token with above + G < P <= above + G + E, G the mass of the collected tokens with larger keys
         const u64 above = ld_agent(&row->above), P = ld_agent(&row->P);
         if (tid == 0) s_bc[0] = kp;
+        for (u32 j = n + tid; j < ((n + 7u) & ~7u); j += NTF) {  // pad to whole groups of 8: keys 0 never count
+            s_key[j] = 0ull;
+            s_mass[j] = 0ull;
+        }
         __syncthreads();
         for (u32 i = tid; i < n; i += NTF) {
             const u64 ki = s_key[i];
             u64 g = 0;
-            for (u32 j = 0; j < n; ++j) g += s_key[j] > ki ? s_mass[j] : 0ull;
+            for (u32 j = 0; j < n; j += 8) {  // 8 independent LDS reads in flight (broadcast: every lane reads j)
+                u64 kk[8], mm[8];
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    kk[q] = s_key[j + q];
+                    mm[q] = s_mass[j + q];
+                }
+#pragma unroll
+                for (int q = 0; q < 8; ++q) g += kk[q] > ki ? mm[q] : 0ull;
+            }
             const u64 lo = above + g;
             if (lo < P && P <= lo + s_mass[i]) s_bc[0] = ki;
         }

@@ -173,6 +173,58 @@ def test_full_path_large_top_k_ties_and_min_p():
     compare(g, w, "ties")
 
 
+
+def test_log_probabilities_at_huge_magnitudes():
+    """Logits around 1e6 and -1e5: the log-sum-exp takes each difference to the running maximum before scaling by 1/T,
+    which is exact near the maximum at any magnitude (both paths, one block per row and split)."""
+    need_gpu()
+    rng = np.random.default_rng(31)
+    for rows in (4, 300):
+        V = 20_000
+        x = (rng.standard_normal((rows, V)) * 1.5).astype(np.float32)
+        x[0::4] *= 1e6
+        x[1::4] -= 1e5
+        x[2::4] += 3e4
+        p = S.row_params(rows, temperature=0.8, top_p=0.9, top_k=40)
+        cfg = dict(logits=x, dtype="f32", params=p, uniforms=W.uniforms_f32(31, rows), counts=None, mask=None)
+        for kmax in (64, 0):
+            log(f"huge magnitudes rows={rows} kmax={kmax}")
+            g, w = run_both(cfg, kmax=kmax)
+            compare(g, w, f"huge magnitudes rows={rows} kmax={kmax}")
+
+
+def test_full_path_split_rows_with_extreme_shapes():
+    """The split full path (19 blocks per row) on rows with extreme shapes: a maximum far above the rest, leading tiles
+    and a whole block without an allowed token, a crossing bin of far more than 2048 tokens (the single-block path
+    takes the row inside the collection launch), one allowed token, huge magnitudes, sharp and flat temperatures."""
+    need_gpu()
+    rng = np.random.default_rng(23)
+    B, V = 12, 154_880                         # 19 blocks of 2 tiles per row
+    x = (rng.standard_normal((B, V)) * 1.5).astype(np.float32)
+    words = (V + 31) // 32
+    mask = np.full((B, words), 0xFFFFFFFF, dtype=np.uint32)
+    counts = rng.integers(0, 2, (B, V)).astype(np.int32)
+    p = S.row_params(B, temperature=0.8, top_p=0.9, min_p=0.0, top_k=0, repetition=1.1, presence=0.5, frequency=0.3)
+    x[1, 8191] = 60.0                           # a maximum far above every other value
+    mask[2, : 8192 // 32] = 0                   # block 0 of row 2: no allowed token
+    mask[2, 8192 // 32: (8192 + 4096) // 32] = 0  # block 1: its first tile without an allowed token
+    x[3] = (rng.standard_normal(V) * 1e-4).astype(np.float32)  # flat: far more than 2048 tokens in the crossing bin
+    counts[3] = 0
+    p[4]["top_p"] = 0.01
+    p[5]["top_p"] = 0.999
+    p[6]["min_p"] = 0.2
+    mask[7] = 0
+    mask[7, 4000] = 1 << 5                      # one allowed token
+    x[8] = x[8] * 1e6                           # huge magnitudes
+    x[9] = x[9] - 1e5
+    p[10]["temperature"] = 0.05                 # sharp
+    p[11]["temperature"] = 5.0                  # flat-ish
+    cfg = dict(logits=x, dtype="f32", params=p, uniforms=W.uniforms_f32(29, B), counts=counts, mask=mask)
+    log("full path extreme rows: 12 x 154880")
+    g, w = run_both(cfg, kmax=0)
+    compare(g, w, "extreme rows")
+
+
 # ---------------------------------------------------------------- full batches (one block per row)
 
 def test_northstar_full_size_and_repeated_launches():
