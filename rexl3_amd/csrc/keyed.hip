@@ -55,39 +55,54 @@ __device__ double pairwise_small(const double* a, int n) {
     return res;
 }
 
+__device__ __forceinline__ double readlane_f64(double v, int lane) {
+    return __longlong_as_double((long long)readlane64((u64)__double_as_longlong(v), lane));
+}
+
+// numpy's float64 pairwise sum for n <= 64 of a[i] held on lane i (the same order as pairwise_small), read lane by
+// lane into scalar registers: no LDS round trip per term
+__device__ __forceinline__ double pairwise_lanes(double a, int n) {
+    if (n < 8) {
+        double r = 0.0;
+        for (int i = 0; i < n; ++i) r += readlane_f64(a, i);
+        return r;
+    }
+    double r[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r[j] = readlane_f64(a, j);
+    int i = 8;
+    for (; i < n - (n % 8); i += 8) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) r[j] += readlane_f64(a, i + j);
+    }
+    double res = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
+    for (; i < n; ++i) res += readlane_f64(a, i);
+    return res;
+}
+
 // `try_choose` over vals[0..k), ids[0..k) (LDS, already in (value desc, id asc) order, no NaN), temperature > 0.
-// Returns the chosen index (wave-uniform). s_tmp: 64 doubles of LDS.
+// Returns the chosen index (wave-uniform). The sums run in the reference's order on values read lane by lane (every
+// lane computes the same scalar sequence); cross-lane moves are readlanes and DPP/permlane swaps, not LDS.
 __device__ int keyed_choose_wave(const float* vals, const u32* ids, int k, u64 seed, double temperature, double top_p, double min_p,
-                                 u64 position, double* s_tmp) {
+                                 u64 position) {
     const int l = lane_id();
     const double t = temperature > 1e-6 ? temperature : 1e-6;
     const double sc = l < k ? (double)vals[l] / t : 0.0;
-    const double sc0 = __shfl(sc, 0, WAVE);
+    const double sc0 = readlane_f64(sc, 0);
     int keep = k;
     if (top_p > 0.0 && top_p < 1.0) {
         // the maximum of `scaled` is its first entry: the values are sorted and t > 0
-        s_tmp[l] = l < k ? exp(sc - sc0) : 0.0;
-        wave_lds_sync();
-        int kp = 0;
-        // the quotients probs[i] / total on their own lanes (the same IEEE divisions), the running sum on lane 0
-        double total = 0.0;
-        if (l == 0) total = pairwise_small(s_tmp, k);
-        total = __shfl(total, 0, WAVE);
-        const double q = l < k ? s_tmp[l] / total : 0.0;
-        wave_lds_sync();
-        s_tmp[l] = q;
-        wave_lds_sync();
-        if (l == 0) {
-            double c = 0.0;
-            int below = 0;
-            for (int i = 0; i < k; ++i) {
-                c += s_tmp[i];
-                if (c < top_p) ++below;
-            }
-            kp = below + 1 < k ? below + 1 : k;
+        const double e = l < k ? exp(sc - sc0) : 0.0;
+        const double total = pairwise_lanes(e, k);
+        // the quotients probs[i] / total on their own lanes (the same IEEE divisions), then the running sum in order
+        const double q = l < k ? e / total : 0.0;
+        double c = 0.0;
+        int below = 0;
+        for (int i = 0; i < k; ++i) {
+            c += readlane_f64(q, i);
+            below += c < top_p ? 1 : 0;
         }
-        keep = __shfl(kp, 0, WAVE);
-        wave_lds_sync();
+        keep = below + 1 < k ? below + 1 : k;
     }
     if (min_p > 0.0) {
         const double floor_v = sc0 + log(min_p);
@@ -103,7 +118,8 @@ __device__ int keyed_choose_wave(const float* vals, const u32* ids, int k, u64 s
     const bool live = score > -INFINITY;  // false for NaN
     double best = live ? score : -INFINITY;
 #pragma unroll
-    for (int m = 1; m < WAVE; m <<= 1) best = fmax(best, __shfl_xor(best, m, WAVE));
+    for (int m = 1; m < WAVE; m <<= 1)
+        best = fmax(best, __longlong_as_double((long long)xor_lane64((u64)__double_as_longlong(best), m)));
     const u64 hit = ballot(live && score == best);
     return hit ? (int)__builtin_ctzll(hit) : 0;
 }
@@ -132,7 +148,6 @@ __global__ void __launch_bounds__(256) keyed_pick_k(const int* __restrict__ ids,
     __shared__ float s_v[4][64];
     __shared__ u32 s_i[4][64];
     __shared__ u32 s_tid[4][64];
-    __shared__ double s_tmp[4][64];
     const int w = threadIdx.x / WAVE, l = lane_id();
     const int r = blockIdx.x * 4 + w;
     if (r >= rows) return;
@@ -164,7 +179,7 @@ __global__ void __launch_bounds__(256) keyed_pick_k(const int* __restrict__ ids,
             if (l < k) s_tid[w][l] = (u32)c_row[s_i[w][l]];
             wave_lds_sync();
             const int b = keyed_choose_wave(s_v[w], s_tid[w], k, p.seed, p.temperature, p.top_p, p.min_p,
-                                            p.first_position + (u64)depth, s_tmp[w]);
+                                            p.first_position + (u64)depth);
             pick = (int)s_i[w][b];
         }
     }
@@ -270,7 +285,6 @@ __global__ void __launch_bounds__(KNT, 1) keyed_fast_k(const void* logits, long 
     __shared__ u64 s_list[KNW][WAVE];
     __shared__ float s_v[WAVE];
     __shared__ u32 s_id[WAVE];
-    __shared__ double s_tmp[WAVE];
     __shared__ unsigned s_flag;
     __shared__ u64 s_thr;
     __shared__ u32 s_top[KNW * WaveTop<KBUF>::TOPN];
@@ -447,7 +461,7 @@ __global__ void __launch_bounds__(KNT, 1) keyed_fast_k(const void* logits, long 
         s_id[l] = id;
         wave_lds_sync();
         const int k = min(p.top_k, count);
-        pick = keyed_choose_wave(s_v, s_id, k, p.seed, p.temperature, p.top_p, p.min_p, p.first_position + (u64)depth, s_tmp);
+        pick = keyed_choose_wave(s_v, s_id, k, p.seed, p.temperature, p.top_p, p.min_p, p.first_position + (u64)depth);
     }
     const u32 pid = readlane32(id, pick);
     const float pv = __uint_as_float(readlane32(__float_as_uint(v), pick));
