@@ -149,6 +149,22 @@ int gb_dflash_selector_walk(const void* anchor, const void* topk_ids, const void
                             void* out_tokens, void* conf, void* stream);
 
 /*
+ * Replace crates/cuda/csrc/dsv4_mtp_gpu.cu:1662-1718 (gb_dsv4_mtp_markov_walk_fast_bf16 / _keyed_bf16; Rust bindings
+ * crates/cuda/src/dsv4_mtp_gpu.rs:55-67): the DSV4 draft head's Markov walk over walk_rows rows of logits f32
+ * [walk_rows, vocab] (vocab >= 1024). Row k's 1024 candidates are each of 256 threads' 4 largest logits of
+ * v = t, t + 256, ...; each gains <embed[ids[k]], head[v]> (bf16 [vocab, 256], rank must be 256) in place, with the
+ * reference kernel's float arithmetic; ids[k + 1] is their maximum (fast) or the keyed choose over their top cand_k
+ * (1..64) at base_pos + k, conf[k] (nullable) = 1 / (1 + exp(-margin)). ids i32 [walk_rows + 1], ids[0] the input
+ * token. Workspaces: cand_ids_ws i32 [walk_rows, 1024], cand_scores_ws f32 [1024] (16-byte aligned, like embed and
+ * head). Two launches per row after one for the candidates; each row's pick sorts its 1024 keys in registers.
+ */
+int gb_dsv4_mtp_markov_walk_fast_bf16(void* logits, int* ids, const void* embed, const void* head, void* cand_ids_ws,
+                                      void* cand_scores_ws, int walk_rows, int vocab, int rank, void* stream);
+int gb_dsv4_mtp_markov_walk_keyed_bf16(void* logits, int* ids, float* conf, const void* embed, const void* head, void* cand_ids_ws,
+                                       void* cand_scores_ws, int walk_rows, int vocab, int rank, int cand_k, unsigned long long seed,
+                                       double temperature, double top_p, double min_p, unsigned long long base_pos, void* stream);
+
+/*
  * Replaces crates/cuda/csrc/glm_mtp.cu:272-280 (gb_glm_keyed_pick). ids i32 / vals f32 [rows, count] sorted by
  * (value desc, id asc), count <= 64; params GbsKeyedRow[rows]. A keyed row with temperature > 0 takes
  * `try_choose` (crates/sampling/src/lib.rs:210-267) over its first min(top_k, count) candidates (top_k 0 = all) at

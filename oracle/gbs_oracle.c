@@ -1200,3 +1200,115 @@ void gbo_selector_walk(const int32_t* anchor, const int32_t* ids, const float* v
     }
     free(a_g);
 }
+
+/* ------------------------------------------------------------------------------------------------ DSV4 Markov walk
+ * crates/cuda/csrc/dsv4_mtp_gpu.cu: candidates :1233-1262 (thread t of 256 keeps the 4 largest of v = t, t + 256, ...,
+ * strict >), bias :1264-1311 (per candidate, lane j of 32 sums e[8j + q] * h[8j + q] for q = 0..7 by fmaf in order, the
+ * 32 partial sums reduced by the butterfly xor 16, 8, 4, 2, 1 as lane 0 sees it; the logit gains the sum in place),
+ * picks :1313-1462 (non-finite scores become -inf with id 0x7fffffff; order value desc, id asc). */
+static float bf16f(uint16_t h) {
+    union { uint32_t u; float f; } c;
+    c.u = (uint32_t)h << 16;
+    return c.f;
+}
+
+static int mw_before(float va, int ia, float vb, int ib) { return va > vb || (va == vb && ia < ib); }
+
+void gbo_markov_walk(float* logits, int32_t* ids, float* conf, const uint16_t* embed, const uint16_t* head, int walk_rows, int vocab,
+                     int keyed, int cand_k, uint64_t seed, double temperature, double top_p, double min_p, uint64_t base_pos) {
+    enum { NC = 1024, RANK = 256, NONE = 0x7fffffff };
+    int32_t* cand = (int32_t*)malloc(sizeof(int32_t) * (size_t)walk_rows * NC);
+    for (int r = 0; r < walk_rows; ++r) {
+        const float* lr = logits + (size_t)r * vocab;
+        for (int t = 0; t < 256; ++t) {
+            float b[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+            int bi[4] = {0, 0, 0, 0};
+            for (int v = t; v < vocab; v += 256) {
+                const float x = lr[v];
+                if (!(x > b[3])) continue;
+                int pos = 3;
+                while (pos > 0 && x > b[pos - 1]) {
+                    b[pos] = b[pos - 1];
+                    bi[pos] = bi[pos - 1];
+                    --pos;
+                }
+                b[pos] = x;
+                bi[pos] = v;
+            }
+            for (int q = 0; q < 4; ++q) cand[(size_t)r * NC + t * 4 + q] = bi[q];
+        }
+    }
+    float sc[NC];
+    int sid[NC];
+    for (int k = 0; k < walk_rows; ++k) {
+        float* lr = logits + (size_t)k * vocab;
+        const int tok = ids[k];
+        const int ok = (unsigned)tok < (unsigned)vocab;
+        for (int idx = 0; idx < NC; ++idx) {
+            const int v = cand[(size_t)k * NC + idx];
+            if ((unsigned)v >= (unsigned)vocab) {
+                sc[idx] = -INFINITY;
+                continue;
+            }
+            float part[32];
+            for (int j = 0; j < 32; ++j) {
+                float a = 0.0f;
+                for (int q = 0; q < 8; ++q) {
+                    const float e = ok ? bf16f(embed[(size_t)tok * RANK + j * 8 + q]) : 0.0f;
+                    a = fmaf(e, bf16f(head[(size_t)v * RANK + j * 8 + q]), a);
+                }
+                part[j] = a;
+            }
+            for (int m = 16; m >= 1; m >>= 1) {
+                float nx[32];
+                for (int j = 0; j < 32; ++j) nx[j] = part[j] + part[j ^ m];
+                memcpy(part, nx, sizeof(part));
+            }
+            lr[v] = lr[v] + part[0];
+            sc[idx] = lr[v];
+        }
+        /* (value desc, id asc) order of the 1024 candidates */
+        int ord[NC];
+        float vv[NC];
+        for (int i = 0; i < NC; ++i) {
+            const int fin = isfinite(sc[i]);
+            vv[i] = fin ? sc[i] : -INFINITY;
+            sid[i] = fin ? cand[(size_t)k * NC + i] : NONE;
+            ord[i] = i;
+        }
+        for (int i = 1; i < NC; ++i) { /* insertion sort: 1024 keys, a test oracle */
+            const int x = ord[i];
+            int j = i;
+            while (j > 0 && mw_before(vv[x], sid[x], vv[ord[j - 1]], sid[ord[j - 1]])) {
+                ord[j] = ord[j - 1];
+                --j;
+            }
+            ord[j] = x;
+        }
+        if (!keyed) {
+            const int b = sid[ord[0]];
+            ids[k + 1] = b != NONE ? b : 0;
+            continue;
+        }
+        const int kk = cand_k < 1 ? 1 : (cand_k > 64 ? 64 : cand_k);
+        float ts[64];
+        int32_t ti[64];
+        int valid = 0;
+        for (int i = 0; i < kk; ++i) {
+            ts[i] = vv[ord[i]];
+            ti[i] = sid[ord[i]];
+        }
+        while (valid < kk && isfinite(ts[valid]) && ti[valid] != NONE) ++valid;
+        if (valid == 0) {
+            ids[k + 1] = 0;
+            if (conf) conf[k] = 0.0f;
+            continue;
+        }
+        float margin = 30.0f;
+        const int ch = gbo_keyed_choose(ts, ti, valid, seed, temperature, top_p, min_p, base_pos + (uint64_t)k, &margin);
+        if (!isfinite(margin)) margin = -30.0f;
+        ids[k + 1] = ti[ch] != NONE ? ti[ch] : 0;
+        if (conf) conf[k] = 1.0f / (1.0f + expf(-margin));
+    }
+    free(cand);
+}

@@ -112,6 +112,13 @@ void gbo_selector_walk(const int32_t* anchor, const int32_t* ids, const float* v
                        const uint16_t* pred_cb, const uint16_t* succ_cb, int n_seq, int rows, int k, int rank,
                        const GboWalkSampling* ws, const int32_t* row_off, int32_t* out, float* conf, float* margin);
 
+/* The DSV4 draft head's Markov walk (crates/cuda/csrc/dsv4_mtp_gpu.cu:1233-1480, 1662-1718). logits f32
+ * [walk_rows, vocab] (the candidates' logits gain their bias in place); ids i32 [walk_rows + 1] (ids[0] in, ids[1..]
+ * out); embed / head bf16 bits [vocab, 256]; keyed = 0: argmax, 1: keyed choose over the top cand_k (conf: the
+ * sigmoid of its margin, nullable). */
+void gbo_markov_walk(float* logits, int32_t* ids, float* conf, const uint16_t* embed, const uint16_t* head, int walk_rows, int vocab,
+                     int keyed, int cand_k, uint64_t seed, double temperature, double top_p, double min_p, uint64_t base_pos);
+
 #ifdef __cplusplus
 }
 #endif

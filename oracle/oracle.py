@@ -109,6 +109,9 @@ def lib():
         L.gbo_keyed_choose.restype = C.c_int
         L.gbo_keyed_choose.argtypes = [P, P, C.c_int, C.c_uint64, C.c_double, C.c_double, C.c_double, C.c_uint64, C.POINTER(C.c_float)]
         L.gbo_selector_walk.argtypes = [P, P, P, P, C.c_int, P, P, C.c_int, C.c_int, C.c_int, C.c_int, P, P, P, P, P]
+        L.gbo_markov_walk.restype = None
+        L.gbo_markov_walk.argtypes = [P, P, P, P, P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_uint64, C.c_double, C.c_double,
+                                      C.c_double, C.c_uint64]
         L.gbo_batch_spec_verify.restype = C.c_int
         L.gbo_batch_spec_verify.argtypes = [P, P, C.c_int, C.c_int, C.c_int, P, P, P, P, P, P, P, C.c_int]
         _lib = L
@@ -308,6 +311,22 @@ def keyed_choose(scores, ids, seed: int, temperature: float, top_p: float, min_p
     m = C.c_float(0.0)
     i = lib().gbo_keyed_choose(_p(scores), _p(ids), scores.size, seed, temperature, top_p, min_p, position, C.byref(m))
     return i, m.value
+
+
+def markov_walk(logits, first_id: int, embed, head, walk_rows: int, keyed: bool = False, cand_k: int = 1, seed: int = 0,
+                temperature: float = 1.0, top_p: float = 1.0, min_p: float = 0.0, base_pos: int = 0):
+    """crates/cuda/csrc/dsv4_mtp_gpu.cu:1233-1480 / 1662-1718: the DSV4 draft head's Markov walk. logits f32
+    [walk_rows, vocab]; embed / head bf16 bits (u16) [vocab, 256]. Returns (ids [walk_rows + 1], conf [walk_rows],
+    logits after the in-place bias)."""
+    lg = np.array(logits, dtype=np.float32, order="C", copy=True)
+    embed = np.ascontiguousarray(embed, dtype=np.uint16)
+    head = np.ascontiguousarray(head, dtype=np.uint16)
+    ids = np.zeros(walk_rows + 1, np.int32)
+    ids[0] = first_id
+    conf = np.zeros(walk_rows, np.float32)
+    lib().gbo_markov_walk(_p(lg), _p(ids), _p(conf), _p(embed), _p(head), walk_rows, lg.shape[1], 1 if keyed else 0, cand_k, seed,
+                          temperature, top_p, min_p, base_pos)
+    return ids, conf, lg
 
 
 def selector_walk(anchor, ids, vals, gate, gate_f32: bool, pred_cb, succ_cb, n_seq: int, rows: int, sampling=None, row_off=None):

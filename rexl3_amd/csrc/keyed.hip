@@ -697,6 +697,177 @@ __global__ void clear_k(uint4* p, size_t n16, unsigned char* tail, size_t ntail)
     if (i < ntail) tail[i] = 0;
 }
 
+// ------------------------------------------------------------------------------------------------ DSV4 Markov walk
+// The DSV4 draft head's keyed Markov walk (crates/cuda/csrc/dsv4_mtp_gpu.cu:1233-1480 kernels, 1662-1718 entry
+// points). Per walk row k, 1024 candidates: thread t of 256 keeps the 4 largest logits of v = t, t + 256, ... Then,
+// from the previous token p = ids[k], each candidate's logit gains <embed[p], head[v]> (bf16 tables [vocab, 256]) and the
+// logits row keeps the sum. The next token is the argmax of the candidates, or the keyed choose (the device
+// try_choose with its margin) over their top cand_k. Row k + 1's bias needs token k + 1, so each row is a launch of
+// the bias kernel and a launch of the pick (the caller's workspace leaves no room for a hand-off counter).
+
+constexpr int MW_CAND = 1024;
+constexpr int MW_RANK = 256;
+constexpr int MW_NT = 256;
+constexpr u32 MW_NONE = 0x7fffffffu;
+
+// thread t's 4 largest of logits[v], v = t + 256 i, in descending order; strict > so the first of equal values stays,
+// a NaN never enters and an unfilled slot keeps id 0 (reference :1233-1262)
+__global__ void __launch_bounds__(MW_NT) mw_cands_k(const float* __restrict__ logits, int* __restrict__ cand_ids, int vocab) {
+    const int row = blockIdx.x, t = threadIdx.x;
+    const float* lr = logits + (size_t)row * vocab;
+    float b0 = -INFINITY, b1 = -INFINITY, b2 = -INFINITY, b3 = -INFINITY;
+    int i0 = 0, i1 = 0, i2 = 0, i3 = 0;
+    for (int v = t; v < vocab; v += MW_NT) {
+        const float x = lr[v];
+        if (!(x > b3)) continue;
+        if (x > b0) {
+            b3 = b2; i3 = i2; b2 = b1; i2 = i1; b1 = b0; i1 = i0; b0 = x; i0 = v;
+        } else if (x > b1) {
+            b3 = b2; i3 = i2; b2 = b1; i2 = i1; b1 = x; i1 = v;
+        } else if (x > b2) {
+            b3 = b2; i3 = i2; b2 = x; i2 = v;
+        } else {
+            b3 = x; i3 = v;
+        }
+    }
+    int* o = cand_ids + (size_t)row * MW_CAND + t * 4;
+    o[0] = i0;
+    o[1] = i1;
+    o[2] = i2;
+    o[3] = i3;
+}
+
+// One walk row's bias: 32 blocks of 256 threads; each half-wave (32 lanes, lane j owning dimensions 8j .. 8j + 7)
+// scores 4 candidates: 8 fused multiply-adds in order, then a butterfly over the 32 lanes (xor 16, 8, 4, 2, 1) whose
+// lane-0 total is added to the logit (reference :1264-1311).
+__global__ void __launch_bounds__(MW_NT) mw_bias_k(float* __restrict__ logits, const int* __restrict__ token,
+                                                   const u16* __restrict__ embed, const u16* __restrict__ head,
+                                                   const int* __restrict__ cand_ids, float* __restrict__ cand_scores, int vocab) {
+    const int t = *token;
+    const bool ok = (unsigned)t < (unsigned)vocab;
+    const int hw = threadIdx.x >> 5, j = threadIdx.x & 31;
+    const int c_base = ((int)blockIdx.x * (MW_NT / 32) + hw) * 4;
+    float e[8];
+    if (ok) {
+        const uint4 eu = *reinterpret_cast<const uint4*>(embed + (size_t)t * MW_RANK + j * 8);
+        const u32 w[4] = {eu.x, eu.y, eu.z, eu.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            e[2 * q] = __uint_as_float(w[q] << 16);
+            e[2 * q + 1] = __uint_as_float(w[q] & 0xFFFF0000u);
+        }
+    } else {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) e[q] = 0.0f;
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const int idx = c_base + c;
+        const int v = cand_ids[idx];
+        if ((unsigned)v < (unsigned)vocab) {  // uniform over the half-wave
+            const uint4 hu = *reinterpret_cast<const uint4*>(head + (size_t)v * MW_RANK + j * 8);
+            const u32 w[4] = {hu.x, hu.y, hu.z, hu.w};
+            float acc = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                acc = __builtin_fmaf(e[2 * q], __uint_as_float(w[q] << 16), acc);
+                acc = __builtin_fmaf(e[2 * q + 1], __uint_as_float(w[q] & 0xFFFF0000u), acc);
+            }
+#pragma unroll
+            for (int m = 16; m >= 1; m >>= 1) acc += __shfl_xor(acc, m, 32);
+            if (j == 0) {
+                const float sc = logits[v] + acc;
+                logits[v] = sc;
+                cand_scores[idx] = sc;
+            }
+        } else if (j == 0) {
+            cand_scores[idx] = -INFINITY;
+        }
+    }
+}
+
+// One walk row's pick over the 1024 candidate scores (a non-finite score counts as -inf with id 0x7fffffff). Keys
+// order (value desc, id asc), -0 tying +0 as the reference's float compares do. KEYED: the exact top min(cand_k, 64)
+// by a register sort and merge of the 1024 keys, then the keyed choose over the leading finite ones (reference
+// :1363-1462); otherwise their maximum (:1313-1361).
+template <bool KEYED>
+__global__ void __launch_bounds__(MW_NT) mw_pick_k(const float* __restrict__ cand_scores, const int* __restrict__ cand_ids,
+                                                   int* __restrict__ out_id, float* __restrict__ out_conf, int cand_k, u64 seed,
+                                                   double temperature, double top_p, double min_p, u64 position) {
+    __shared__ u64 s_list[MW_NT / WAVE][WAVE];
+    __shared__ float s_sc[64];
+    __shared__ int s_id[64];
+    __shared__ double s_pr[64];
+    const int tid = threadIdx.x, l = lane_id();
+    auto key_of = [&](float v, int id) -> u64 {
+        const bool fin = __builtin_isfinite(v);
+        const u32 ok = okey_f32(fin ? v : -INFINITY);
+        const u32 i = fin ? (u32)id : MW_NONE;
+        return ((u64)ok << 32) | (u64)(0xFFFFFFFFu - i);
+    };
+    // this wave's best 64 of its 256 keys: four lanes-wide lists sorted and merged
+    u64 acc = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int c = tid * 4 + q;
+        const u64 k = wave_sort_desc(key_of(cand_scores[c], cand_ids[c]));
+        acc = q == 0 ? k : wave_merge_desc(acc, k);
+    }
+    const u64 top = block_tree_merge<MW_NT / WAVE>(acc, s_list);  // wave 0: the block's best 64, descending
+    if (tid >= WAVE) return;
+    const float v = okey_to_f32((u32)(top >> 32));
+    const u32 id = 0xFFFFFFFFu - (u32)top;
+    if (!KEYED) {
+        if (l == 0) out_id[0] = id != MW_NONE ? (int)id : 0;
+        return;
+    }
+    const int k = cand_k < 1 ? 1 : (cand_k > 64 ? 64 : cand_k);
+    // the leading candidates with a finite score and a real id
+    const u64 bad = ballot(l < k && (!__builtin_isfinite(v) || id == MW_NONE)) | (k < 64 ? ~0ull << k : 0ull);
+    const int valid_k = bad ? (int)__builtin_ctzll(bad) : 64;
+    if (l < k) {
+        s_sc[l] = v;
+        s_id[l] = (int)id;
+    }
+    wave_lds_sync();
+    if (l == 0) {
+        if (valid_k == 0) {
+            out_id[0] = 0;
+            if (out_conf) out_conf[0] = 0.0f;
+        } else {
+            float margin = 30.0f;
+            const int chosen = keyed_choose_serial(s_sc, s_id, valid_k, seed, temperature, top_p, min_p, position, &margin, s_pr);
+            if (!__builtin_isfinite(margin)) margin = -30.0f;
+            out_id[0] = (u32)s_id[chosen] != MW_NONE ? s_id[chosen] : 0;
+            if (out_conf) out_conf[0] = 1.0f / (1.0f + expf(-margin));
+        }
+    }
+}
+
+int launch_markov_walk(void* logits, int* ids, float* conf, const void* embed, const void* head, void* cand_ids_ws,
+                       void* cand_scores_ws, int walk_rows, int vocab, int rank, bool keyed, int cand_k, u64 seed, double temperature,
+                       double top_p, double min_p, u64 base_pos, void* stream) {
+    if (!logits || !ids || !embed || !head || !cand_ids_ws || !cand_scores_ws) return GBS_ERR_INVALID;
+    if (walk_rows <= 0 || vocab < MW_CAND || rank != MW_RANK || (keyed && cand_k < 1)) return GBS_ERR_INVALID;
+    if (!aligned(embed, 16) || !aligned(head, 16) || !aligned(cand_ids_ws, 16) || !aligned(cand_scores_ws, 16)) return GBS_ERR_INVALID;
+    const hipStream_t st = to_stream(stream);
+    float* lg = (float*)logits;
+    int* cids = (int*)cand_ids_ws;
+    float* cs = (float*)cand_scores_ws;
+    hipLaunchKernelGGL(mw_cands_k, dim3(walk_rows), dim3(MW_NT), 0, st, (const float*)lg, cids, vocab);
+    for (int k = 0; k < walk_rows; ++k) {
+        hipLaunchKernelGGL(mw_bias_k, dim3(MW_CAND / ((MW_NT / 32) * 4)), dim3(MW_NT), 0, st, lg + (size_t)k * vocab, (const int*)(ids + k),
+                           (const u16*)embed, (const u16*)head, (const int*)(cids + (size_t)k * MW_CAND), cs, vocab);
+        if (keyed)
+            hipLaunchKernelGGL(mw_pick_k<true>, dim3(1), dim3(MW_NT), 0, st, (const float*)cs, (const int*)(cids + (size_t)k * MW_CAND),
+                               ids + k + 1, conf ? conf + k : nullptr, cand_k, seed, temperature, top_p, min_p, base_pos + (u64)k);
+        else
+            hipLaunchKernelGGL(mw_pick_k<false>, dim3(1), dim3(MW_NT), 0, st, (const float*)cs, (const int*)(cids + (size_t)k * MW_CAND),
+                               ids + k + 1, (float*)nullptr, 1, (u64)0, 0.0, 0.0, 0.0, (u64)0);
+    }
+    return launch_status();
+}
+
 }  // namespace
 
 GBS_EXPORT int gb_glm_keyed_pick(const int* ids, const float* vals, int count, int rows, const void* params, int depth, int* out_ids,
@@ -845,6 +1016,20 @@ GBS_EXPORT int gb_dflash_selector_walk(const void* anchor, const void* topk_ids,
                                        void* out_tokens, void* conf, void* stream) {
     return gb_dflash_selector_walk_keyed(anchor, topk_ids, topk_vals, gate, gate_is_f32, pred_codebook, succ_codebook, n_seq, rows, k,
                                          rank, nullptr, out_tokens, conf, stream);
+}
+
+GBS_EXPORT int gb_dsv4_mtp_markov_walk_fast_bf16(void* logits, int* ids, const void* embed, const void* head, void* cand_ids_ws,
+                                                 void* cand_scores_ws, int walk_rows, int vocab, int rank, void* stream) {
+    return launch_markov_walk(logits, ids, nullptr, embed, head, cand_ids_ws, cand_scores_ws, walk_rows, vocab, rank, false, 1, 0, 0.0,
+                              0.0, 0.0, 0, stream);
+}
+
+GBS_EXPORT int gb_dsv4_mtp_markov_walk_keyed_bf16(void* logits, int* ids, float* conf, const void* embed, const void* head,
+                                                  void* cand_ids_ws, void* cand_scores_ws, int walk_rows, int vocab, int rank,
+                                                  int cand_k, unsigned long long seed, double temperature, double top_p, double min_p,
+                                                  unsigned long long base_pos, void* stream) {
+    return launch_markov_walk(logits, ids, conf, embed, head, cand_ids_ws, cand_scores_ws, walk_rows, vocab, rank, true, cand_k, seed,
+                              temperature, top_p, min_p, base_pos, stream);
 }
 
 GBS_EXPORT const char* gbs_version(void) { return "gbsample-hip 0.1 (gfx950)"; }

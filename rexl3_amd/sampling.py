@@ -173,6 +173,29 @@ def selector_walk(anchor: torch.Tensor, topk_ids: torch.Tensor, topk_vals: torch
     return out, conf, margin
 
 
+def markov_walk(logits: torch.Tensor, ids: torch.Tensor, embed: torch.Tensor, head: torch.Tensor, keyed: bool = False,
+                cand_k: int = 1, seed: int = 0, temperature: float = 1.0, top_p: float = 1.0, min_p: float = 0.0,
+                base_pos: int = 0):
+    """The DSV4 draft head's Markov walk (gb_dsv4_mtp_markov_walk_fast_bf16 / _keyed_bf16; crates/cuda/src/dsv4_mtp_gpu.rs).
+    logits f32 [walk_rows, vocab], biased in place; ids i32 [walk_rows + 1] (ids[0] in, the rest written); embed / head
+    bf16 [vocab, 256]. Returns conf f32 [walk_rows] for the keyed walk, else None."""
+    walk_rows, vocab = logits.shape
+    rank = embed.shape[-1]
+    dev = logits.device
+    if ids.shape[0] != walk_rows + 1 or embed.shape[0] < vocab or head.shape[0] < vocab or head.shape[-1] != rank:
+        raise ValueError("markov_walk: shapes")
+    cand = torch.empty((walk_rows, 1024), dtype=torch.int32, device=dev)
+    scores = torch.empty(1024, dtype=torch.float32, device=dev)
+    if not keyed:
+        _lib.call("gb_dsv4_mtp_markov_walk_fast_bf16", _ptr(logits), _ptr(ids), _ptr(embed), _ptr(head), _ptr(cand), _ptr(scores),
+                  walk_rows, vocab, rank, _stream(dev))
+        return None
+    conf = torch.empty(walk_rows, dtype=torch.float32, device=dev)
+    _lib.call("gb_dsv4_mtp_markov_walk_keyed_bf16", _ptr(logits), _ptr(ids), _ptr(conf), _ptr(embed), _ptr(head), _ptr(cand),
+              _ptr(scores), walk_rows, vocab, rank, cand_k, seed, temperature, top_p, min_p, base_pos, _stream(dev))
+    return conf
+
+
 def keyed_rows(samplings, positions) -> np.ndarray:
     """KeyedRow records (crates/cuda/csrc/glm_mtp.cu:258-264) for a list of Sampling and absolute positions."""
     recs = np.zeros(len(samplings), dtype=KEYED_ROW_DTYPE)
