@@ -163,6 +163,12 @@ int gb_dsv4_mtp_markov_walk_fast_bf16(void* logits, int* ids, const void* embed,
 int gb_dsv4_mtp_markov_walk_keyed_bf16(void* logits, int* ids, float* conf, const void* embed, const void* head, void* cand_ids_ws,
                                        void* cand_scores_ws, int walk_rows, int vocab, int rank, int cand_k, unsigned long long seed,
                                        double temperature, double top_p, double min_p, unsigned long long base_pos, void* stream);
+/* The same keyed walk with cand_k, seed, temperature, top_p, min_p and base_pos read on the device from params, a
+ * DEVICE pointer to the 72-byte Dsv4MtpRoundParams (crates/cuda/src/dsv4_mtp_gpu.rs:2683-2701; the reference's
+ * gb_dsv4_mtp_markov_walk_keyed_bf16_params, dsv4_mtp_gpu.cu:1720-1760). */
+int gb_dsv4_mtp_markov_walk_keyed_bf16_params(void* logits, int* ids, float* conf, const void* embed, const void* head,
+                                              void* cand_ids_ws, void* cand_scores_ws, int walk_rows, int vocab, int rank,
+                                              const void* params, void* stream);
 
 /*
  * Replaces crates/cuda/csrc/glm_mtp.cu:272-280 (gb_glm_keyed_pick). ids i32 / vals f32 [rows, count] sorted by

@@ -31,6 +31,7 @@ SIGNATURES = {
     "gb_dsv4_mtp_markov_walk_fast_bf16": (I, [P, P, P, P, P, P, I, I, I, P]),
     "gb_dsv4_mtp_markov_walk_keyed_bf16": (I, [P, P, P, P, P, P, P, I, I, I, I, C.c_ulonglong, C.c_double, C.c_double, C.c_double,
                                                 C.c_ulonglong, P]),
+    "gb_dsv4_mtp_markov_walk_keyed_bf16_params": (I, [P, P, P, P, P, P, P, I, I, I, P, P]),
     "gb_glm_keyed_pick": (I, [P, P, I, I, P, I, P, P, P]),
     "gb_qfn_greedy_gather": (I, [P, P, I, I, P, P, P]),
     "gbs_workspace_clear": (I, [P, Z, P]),

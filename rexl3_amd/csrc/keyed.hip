@@ -710,6 +710,15 @@ constexpr int MW_RANK = 256;
 constexpr int MW_NT = 256;
 constexpr u32 MW_NONE = 0x7fffffffu;
 
+// The 72-byte Dsv4MtpRoundParams record (crates/cuda/src/dsv4_mtp_gpu.rs:2683-2701); the walk reads cand_k and the
+// sampling fields on the device, so a captured graph replays with new values.
+struct Dsv4RoundDev {
+    int anchor, start_pos, reach, n_kv, window, block_size, cand_k, pad;
+    u64 seed, base_pos;
+    double temperature, top_p, min_p;
+};
+static_assert(sizeof(Dsv4RoundDev) == 72, "Dsv4MtpRoundParams is 72 bytes");
+
 // thread t's 4 largest of logits[v], v = t + 256 i, in descending order; strict > so the first of equal values stays,
 // a NaN never enters and an unfilled slot keeps id 0 (reference :1233-1262)
 __global__ void __launch_bounds__(MW_NT) mw_cands_k(const float* __restrict__ logits, int* __restrict__ cand_ids, int vocab) {
@@ -793,8 +802,17 @@ __global__ void __launch_bounds__(MW_NT) mw_bias_k(float* __restrict__ logits, c
 template <bool KEYED>
 __global__ void __launch_bounds__(MW_NT) mw_pick_k(const float* __restrict__ cand_scores, const int* __restrict__ cand_ids,
                                                    int* __restrict__ out_id, float* __restrict__ out_conf, int cand_k, u64 seed,
-                                                   double temperature, double top_p, double min_p, u64 position) {
+                                                   double temperature, double top_p, double min_p, u64 position,
+                                                   const Dsv4RoundDev* __restrict__ rp) {
     __shared__ u64 s_list[MW_NT / WAVE][WAVE];
+    if (KEYED && rp) {  // the device-params form: position = base_pos + step, the step passed in `position`
+        cand_k = rp->cand_k;
+        seed = rp->seed;
+        temperature = rp->temperature;
+        top_p = rp->top_p;
+        min_p = rp->min_p;
+        position += rp->base_pos;
+    }
     __shared__ float s_sc[64];
     __shared__ int s_id[64];
     __shared__ double s_pr[64];
@@ -846,9 +864,11 @@ __global__ void __launch_bounds__(MW_NT) mw_pick_k(const float* __restrict__ can
 
 int launch_markov_walk(void* logits, int* ids, float* conf, const void* embed, const void* head, void* cand_ids_ws,
                        void* cand_scores_ws, int walk_rows, int vocab, int rank, bool keyed, int cand_k, u64 seed, double temperature,
-                       double top_p, double min_p, u64 base_pos, void* stream) {
+                       double top_p, double min_p, u64 base_pos, const void* params, void* stream) {
     if (!logits || !ids || !embed || !head || !cand_ids_ws || !cand_scores_ws) return GBS_ERR_INVALID;
-    if (walk_rows <= 0 || vocab < MW_CAND || rank != MW_RANK || (keyed && cand_k < 1)) return GBS_ERR_INVALID;
+    if (walk_rows <= 0 || vocab < MW_CAND || rank != MW_RANK || (keyed && !params && cand_k < 1)) return GBS_ERR_INVALID;
+    if (params && !aligned(params, 8)) return GBS_ERR_INVALID;
+    const Dsv4RoundDev* rp = (const Dsv4RoundDev*)params;  // a device pointer: read only by the kernels
     if (!aligned(embed, 16) || !aligned(head, 16) || !aligned(cand_ids_ws, 16) || !aligned(cand_scores_ws, 16)) return GBS_ERR_INVALID;
     const hipStream_t st = to_stream(stream);
     float* lg = (float*)logits;
@@ -860,10 +880,11 @@ int launch_markov_walk(void* logits, int* ids, float* conf, const void* embed, c
                            (const u16*)embed, (const u16*)head, (const int*)(cids + (size_t)k * MW_CAND), cs, vocab);
         if (keyed)
             hipLaunchKernelGGL(mw_pick_k<true>, dim3(1), dim3(MW_NT), 0, st, (const float*)cs, (const int*)(cids + (size_t)k * MW_CAND),
-                               ids + k + 1, conf ? conf + k : nullptr, cand_k, seed, temperature, top_p, min_p, base_pos + (u64)k);
+                               ids + k + 1, conf ? conf + k : nullptr, cand_k, seed, temperature, top_p, min_p,
+                               (rp ? 0ull : base_pos) + (u64)k, rp);
         else
             hipLaunchKernelGGL(mw_pick_k<false>, dim3(1), dim3(MW_NT), 0, st, (const float*)cs, (const int*)(cids + (size_t)k * MW_CAND),
-                               ids + k + 1, (float*)nullptr, 1, (u64)0, 0.0, 0.0, 0.0, (u64)0);
+                               ids + k + 1, (float*)nullptr, 1, (u64)0, 0.0, 0.0, 0.0, (u64)0, (const Dsv4RoundDev*)nullptr);
     }
     return launch_status();
 }
@@ -1021,7 +1042,7 @@ GBS_EXPORT int gb_dflash_selector_walk(const void* anchor, const void* topk_ids,
 GBS_EXPORT int gb_dsv4_mtp_markov_walk_fast_bf16(void* logits, int* ids, const void* embed, const void* head, void* cand_ids_ws,
                                                  void* cand_scores_ws, int walk_rows, int vocab, int rank, void* stream) {
     return launch_markov_walk(logits, ids, nullptr, embed, head, cand_ids_ws, cand_scores_ws, walk_rows, vocab, rank, false, 1, 0, 0.0,
-                              0.0, 0.0, 0, stream);
+                              0.0, 0.0, 0, nullptr, stream);
 }
 
 GBS_EXPORT int gb_dsv4_mtp_markov_walk_keyed_bf16(void* logits, int* ids, float* conf, const void* embed, const void* head,
@@ -1029,7 +1050,15 @@ GBS_EXPORT int gb_dsv4_mtp_markov_walk_keyed_bf16(void* logits, int* ids, float*
                                                   int cand_k, unsigned long long seed, double temperature, double top_p, double min_p,
                                                   unsigned long long base_pos, void* stream) {
     return launch_markov_walk(logits, ids, conf, embed, head, cand_ids_ws, cand_scores_ws, walk_rows, vocab, rank, true, cand_k, seed,
-                              temperature, top_p, min_p, base_pos, stream);
+                              temperature, top_p, min_p, base_pos, nullptr, stream);
+}
+
+GBS_EXPORT int gb_dsv4_mtp_markov_walk_keyed_bf16_params(void* logits, int* ids, float* conf, const void* embed, const void* head,
+                                                         void* cand_ids_ws, void* cand_scores_ws, int walk_rows, int vocab, int rank,
+                                                         const void* params, void* stream) {
+    if (!params) return GBS_ERR_INVALID;
+    return launch_markov_walk(logits, ids, conf, embed, head, cand_ids_ws, cand_scores_ws, walk_rows, vocab, rank, true, 1, 0, 0.0, 0.0,
+                              0.0, 0, params, stream);
 }
 
 GBS_EXPORT const char* gbs_version(void) { return "gbsample-hip 0.1 (gfx950)"; }

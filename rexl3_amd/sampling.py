@@ -173,10 +173,16 @@ def selector_walk(anchor: torch.Tensor, topk_ids: torch.Tensor, topk_vals: torch
     return out, conf, margin
 
 
+DSV4_ROUND_PARAMS_DTYPE = np.dtype([("anchor", "<i4"), ("start_pos", "<i4"), ("reach", "<i4"), ("n_kv", "<i4"), ("window", "<i4"),
+                                    ("block_size", "<i4"), ("cand_k", "<i4"), ("pad", "<i4"), ("seed", "<u8"), ("base_pos", "<u8"),
+                                    ("temperature", "<f8"), ("top_p", "<f8"), ("min_p", "<f8")])
+
+
 def markov_walk(logits: torch.Tensor, ids: torch.Tensor, embed: torch.Tensor, head: torch.Tensor, keyed: bool = False,
                 cand_k: int = 1, seed: int = 0, temperature: float = 1.0, top_p: float = 1.0, min_p: float = 0.0,
-                base_pos: int = 0):
-    """The DSV4 draft head's Markov walk (gb_dsv4_mtp_markov_walk_fast_bf16 / _keyed_bf16; crates/cuda/src/dsv4_mtp_gpu.rs).
+                base_pos: int = 0, params: torch.Tensor | None = None):
+    """The DSV4 draft head's Markov walk (gb_dsv4_mtp_markov_walk_fast_bf16 / _keyed_bf16 / _keyed_bf16_params;
+    crates/cuda/src/dsv4_mtp_gpu.rs).
     logits f32 [walk_rows, vocab], biased in place; ids i32 [walk_rows + 1] (ids[0] in, the rest written); embed / head
     bf16 [vocab, 256]. Returns conf f32 [walk_rows] for the keyed walk, else None."""
     walk_rows, vocab = logits.shape
@@ -191,6 +197,12 @@ def markov_walk(logits: torch.Tensor, ids: torch.Tensor, embed: torch.Tensor, he
                   walk_rows, vocab, rank, _stream(dev))
         return None
     conf = torch.empty(walk_rows, dtype=torch.float32, device=dev)
+    if params is not None:  # the device-params form: a 72-byte DSV4_ROUND_PARAMS_DTYPE record in device memory
+        if params.numel() * params.element_size() != 72:
+            raise ValueError("markov_walk: params must be one 72-byte record")
+        _lib.call("gb_dsv4_mtp_markov_walk_keyed_bf16_params", _ptr(logits), _ptr(ids), _ptr(conf), _ptr(embed), _ptr(head), _ptr(cand),
+                  _ptr(scores), walk_rows, vocab, rank, _ptr(params), _stream(dev))
+        return conf
     _lib.call("gb_dsv4_mtp_markov_walk_keyed_bf16", _ptr(logits), _ptr(ids), _ptr(conf), _ptr(embed), _ptr(head), _ptr(cand),
               _ptr(scores), walk_rows, vocab, rank, cand_k, seed, temperature, top_p, min_p, base_pos, _stream(dev))
     return conf

@@ -72,3 +72,22 @@ def test_walk_from_an_out_of_range_token_and_ties():
         g_ids, _, g_lg = run(logits, V + 5, embed, head, rows, **kw)
         w_ids, _, w_lg = O.markov_walk(logits, V + 5, embed, head, rows, keyed, 16, 5, 0.0 if keyed else 1.0, 1.0, 0.0, 0)
         assert np.array_equal(g_ids, w_ids) and np.array_equal(g_lg, w_lg)
+
+
+def test_keyed_walk_with_device_params_equals_the_scalar_form():
+    """gb_dsv4_mtp_markov_walk_keyed_bf16_params reads cand_k and the sampling fields from a 72-byte device record."""
+    need_gpu()
+    rng = np.random.default_rng(41)
+    V, rows = 3000, 5
+    logits = (rng.standard_normal((rows, V)) * 2).astype(np.float32)
+    embed = bf16_bits(rng.standard_normal((V, 256)) * 0.1)
+    head = bf16_bits(rng.standard_normal((V, 256)) * 0.1)
+    rec = np.zeros(1, dtype=S.DSV4_ROUND_PARAMS_DTYPE)
+    rec[0]["cand_k"], rec[0]["seed"], rec[0]["base_pos"] = 24, 2024, 500
+    rec[0]["temperature"], rec[0]["top_p"], rec[0]["min_p"] = 0.9, 0.8, 0.02
+    params = torch.from_numpy(rec.view(np.uint8).copy()).cuda()
+    log("markov keyed, device params")
+    g_ids, g_conf, g_lg = run(logits, 9, embed, head, rows, keyed=True, params=params)
+    w_ids, w_conf, w_lg = O.markov_walk(logits, 9, embed, head, rows, True, 24, 2024, 0.9, 0.8, 0.02, 500)
+    assert np.array_equal(g_ids, w_ids) and np.array_equal(g_lg, w_lg)
+    np.testing.assert_allclose(g_conf, w_conf, rtol=1e-6)
