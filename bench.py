@@ -5,7 +5,7 @@ int32 counts, a u32 grammar bitmask, temperature, top-k 50 / top-p 0.9, fused ma
 inverse-CDF draw from one uniform per row -- at B=256, V=151,936 fp32, inputs resident in HBM. One step = one
 gbs_sample_rows launch over the batch. Prints one JSON line.
 
-    python bench.py [--steps K] [--warmup W] [--workload northstar|c1|c2|c3|c4|c5|keyed] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--workload northstar|c1|c2|c3|c4|c5|keyed|markov] [--no-cpu]
 """
 from __future__ import annotations
 
@@ -246,6 +246,49 @@ def main():
             cpu = {"value": round(done / el, 1), "unit": "rows/s", "cores": threads, "kind": "port",
                    "sample": f"the build's C oracle of the same verification on the same batch (its sequences over "
                              f"{threads} threads), {done} rows in {el:.1f} s"}
+    elif wl == "markov":
+        # the DSV4 draft head's keyed Markov walk: 8 walk rows over V = 129,280 (bf16 embed / head [V, 256])
+        walk_rows, vocab = 8, 129_280
+        rng = np.random.default_rng(8)
+        x = (rng.standard_normal((walk_rows, vocab)) * 2).astype(np.float32)
+        tab = lambda: torch.from_numpy(((rng.standard_normal((vocab, 256)) * 0.1).astype(np.float32).view(np.uint32) >> 16)  # noqa: E731
+                                       .astype(np.uint16).view(np.int16)).to(dev).view(torch.bfloat16)
+        emb, hed = tab(), tab()
+        lg = torch.from_numpy(x).to(dev)
+        ids = torch.zeros(walk_rows + 1, dtype=torch.int32, device=dev)
+        ids[0] = 17
+        cand = torch.empty((walk_rows, 1024), dtype=torch.int32, device=dev)
+        scores = torch.empty(1024, dtype=torch.float32, device=dev)
+        conf = torch.empty(walk_rows, dtype=torch.float32, device=dev)
+        P = lambda t: C.c_void_p(t.data_ptr())  # noqa: E731
+        fn = lib.gb_dsv4_mtp_markov_walk_keyed_bf16
+        argv = (P(lg), P(ids), P(conf), P(emb), P(hed), P(cand), P(scores), walk_rows, vocab, 256, 16, 1234, 0.8, 0.9, 0.0, 100,
+                stream)
+
+        def launch():
+            rc = fn(*argv)
+            if rc:
+                raise RuntimeError(f"gb_dsv4_mtp_markov_walk_keyed_bf16 returned {rc}")
+
+        ms = time_launches(launch, args.steps, args.warmup)
+        rows = walk_rows
+        # the logits once (candidates), then per row 1024 head rows and one embedding row of 512 B
+        nbytes = walk_rows * vocab * 4 + walk_rows * (1024 + 1) * 512
+        kernel = "mw_cands_k + 8 x (mw_bias_k + mw_pick_k<true>)"
+        dtype = "f32 bias from bf16 tables (choose in f64)"
+        workload = "DSV4 draft head's keyed Markov walk: 8 walk rows, V 129,280, rank 256, top-16 keyed choose (launch-bound)"
+        if not args.no_cpu:
+            from oracle import oracle as O
+            eb = (emb.view(torch.int16).cpu().numpy()).view(np.uint16)
+            hb = (hed.view(torch.int16).cpu().numpy()).view(np.uint16)
+            t0 = time.perf_counter()
+            done = 0
+            while time.perf_counter() - t0 < min(args.cpu_seconds, 10.0):
+                O.markov_walk(x, 17, eb, hb, walk_rows, True, 16, 1234, 0.8, 0.9, 0.0, 100)
+                done += walk_rows
+            el = time.perf_counter() - t0
+            cpu = {"value": round(done / el, 1), "unit": "walk rows/s", "cores": 1, "kind": "port",
+                   "sample": f"the build's C oracle of the same walk (one thread), {done} walk rows in {el:.1f} s"}
     else:
         raise SystemExit(f"unknown workload {wl}")
 

@@ -84,7 +84,7 @@ __device__ __forceinline__ double pairwise_lanes(double a, int n) {
 // Returns the chosen index (wave-uniform). The sums run in the reference's order on values read lane by lane (every
 // lane computes the same scalar sequence); cross-lane moves are readlanes and DPP/permlane swaps, not LDS.
 __device__ int keyed_choose_wave(const float* vals, const u32* ids, int k, u64 seed, double temperature, double top_p, double min_p,
-                                 u64 position) {
+                                 u64 position, float* margin = nullptr) {
     const int l = lane_id();
     const double t = temperature > 1e-6 ? temperature : 1e-6;
     const double sc = l < k ? (double)vals[l] / t : 0.0;
@@ -121,7 +121,16 @@ __device__ int keyed_choose_wave(const float* vals, const u32* ids, int k, u64 s
     for (int m = 1; m < WAVE; m <<= 1)
         best = fmax(best, __longlong_as_double((long long)xor_lane64((u64)__double_as_longlong(best), m)));
     const u64 hit = ballot(live && score == best);
-    return hit ? (int)__builtin_ctzll(hit) : 0;
+    const int chosen = hit ? (int)__builtin_ctzll(hit) : 0;
+    if (margin) {
+        // keyed.cuh's margin: the chosen score's lead over the best other kept score, at most 30 (30 with one kept)
+        double second = (live && l != chosen) ? score : -INFINITY;
+#pragma unroll
+        for (int m = 1; m < WAVE; m <<= 1)
+            second = fmax(second, __longlong_as_double((long long)xor_lane64((u64)__double_as_longlong(second), m)));
+        *margin = keep > 1 ? (float)fmin(best - second, 30.0) : 30.f;
+    }
+    return chosen;
 }
 
 // ------------------------------------------------------------------------------------------------ gb_glm_keyed_pick
@@ -719,31 +728,90 @@ struct Dsv4RoundDev {
 };
 static_assert(sizeof(Dsv4RoundDev) == 72, "Dsv4MtpRoundParams is 72 bytes");
 
-// thread t's 4 largest of logits[v], v = t + 256 i, in descending order; strict > so the first of equal values stays,
-// a NaN never enters and an unfilled slot keeps id 0 (reference :1233-1262)
-__global__ void __launch_bounds__(MW_NT) mw_cands_k(const float* __restrict__ logits, int* __restrict__ cand_ids, int vocab) {
-    const int row = blockIdx.x, t = threadIdx.x;
-    const float* lr = logits + (size_t)row * vocab;
-    float b0 = -INFINITY, b1 = -INFINITY, b2 = -INFINITY, b3 = -INFINITY;
-    int i0 = 0, i1 = 0, i2 = 0, i3 = 0;
-    for (int v = t; v < vocab; v += MW_NT) {
-        const float x = lr[v];
-        if (!(x > b3)) continue;
-        if (x > b0) {
-            b3 = b2; i3 = i2; b2 = b1; i2 = i1; b1 = b0; i1 = i0; b0 = x; i0 = v;
-        } else if (x > b1) {
-            b3 = b2; i3 = i2; b2 = b1; i2 = i1; b1 = x; i1 = v;
-        } else if (x > b2) {
-            b3 = b2; i3 = i2; b2 = x; i2 = v;
-        } else {
-            b3 = x; i3 = v;
+// Thread t's 4 largest of logits[v], v = t + 256 i, in descending order. The reference inserts with a strict > in
+// increasing v, which is the order (value desc, v asc); a NaN or -inf never enters and an unfilled slot keeps
+// (-inf, id 0) (reference :1233-1262). Here 512 threads per row: thread (g, j) of 8 x 64 loads the 4 values
+// v = 256 i + 4j .. + 3 (slices t = 4j .. 4j + 3) for i = g, g + 8, ..., keeping a top-4 per slice; the 8 groups'
+// lists of each slice are then merged in LDS.
+constexpr int MW_CT = 512;
+constexpr int MW_CG = MW_CT / 64;
+
+struct Top4 {
+    float v[4];
+    int id[4];
+    __device__ __forceinline__ void init() {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            v[q] = -INFINITY;
+            id[q] = 0;
         }
     }
-    int* o = cand_ids + (size_t)row * MW_CAND + t * 4;
-    o[0] = i0;
-    o[1] = i1;
-    o[2] = i2;
-    o[3] = i3;
+    // (x, i) after every entry that ranks before it (a larger value, or an equal one with a smaller id), by a
+    // compare-and-select network: no run-time index, so the lists stay in registers
+    __device__ __forceinline__ void insert(float x, int i) {
+        bool b[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) b[q] = x > v[q] || (x == v[q] && i < id[q]);
+#pragma unroll
+        for (int q = 3; q >= 1; --q) {
+            v[q] = b[q - 1] ? v[q - 1] : (b[q] ? x : v[q]);
+            id[q] = b[q - 1] ? id[q - 1] : (b[q] ? i : id[q]);
+        }
+        v[0] = b[0] ? x : v[0];
+        id[0] = b[0] ? i : id[0];
+    }
+};
+
+__global__ void __launch_bounds__(MW_CT) mw_cands_k(const float* __restrict__ logits, int* __restrict__ cand_ids, int vocab) {
+    __shared__ float s_v[MW_CG][256][4];
+    __shared__ int s_i[MW_CG][256][4];
+    const int row = blockIdx.x, g = threadIdx.x / 64, j = threadIdx.x % 64;
+    const float* lr = logits + (size_t)row * vocab;
+    Top4 t4[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) t4[q].init();
+    const bool vec = (vocab & 3) == 0 && (((uintptr_t)lr) & 15) == 0;
+    // MW_CU strides' loads in flight before any is ranked (the insert order does not matter: ties rank by id)
+    constexpr int MW_CU = 8;
+    for (int i0 = g; 256 * i0 < vocab; i0 += MW_CG * MW_CU) {
+        float x[MW_CU][4];
+#pragma unroll
+        for (int u = 0; u < MW_CU; ++u) {
+            const int v0 = 256 * (i0 + u * MW_CG) + 4 * j;
+            if (vec && v0 + 4 <= vocab) {
+                const float4 f = *reinterpret_cast<const float4*>(lr + v0);
+                x[u][0] = f.x; x[u][1] = f.y; x[u][2] = f.z; x[u][3] = f.w;
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) x[u][q] = v0 + q < vocab ? lr[v0 + q] : -INFINITY;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < MW_CU; ++u) {
+            const int v0 = 256 * (i0 + u * MW_CG) + 4 * j;
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                if (x[u][q] > -INFINITY) t4[q].insert(x[u][q], v0 + q);  // false for NaN and -inf, as the reference's x > -inf
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            s_v[g][4 * j + q][r] = t4[q].v[r];
+            s_i[g][4 * j + q][r] = t4[q].id[r];
+        }
+    __syncthreads();
+    if (threadIdx.x >= 256) return;
+    const int t = threadIdx.x;
+    Top4 m;
+    m.init();
+    for (int gg = 0; gg < MW_CG; ++gg)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            if (s_v[gg][t][r] > -INFINITY) m.insert(s_v[gg][t][r], s_i[gg][t][r]);
+    int4* o = reinterpret_cast<int4*>(cand_ids + (size_t)row * MW_CAND + t * 4);
+    *o = make_int4(m.id[0], m.id[1], m.id[2], m.id[3]);
 }
 
 // One walk row's bias: 32 blocks of 256 threads; each half-wave (32 lanes, lane j owning dimensions 8j .. 8j + 7)
@@ -815,7 +883,6 @@ __global__ void __launch_bounds__(MW_NT) mw_pick_k(const float* __restrict__ can
     }
     __shared__ float s_sc[64];
     __shared__ int s_id[64];
-    __shared__ double s_pr[64];
     const int tid = threadIdx.x, l = lane_id();
     auto key_of = [&](float v, int id) -> u64 {
         const bool fin = __builtin_isfinite(v);
@@ -848,17 +915,23 @@ __global__ void __launch_bounds__(MW_NT) mw_pick_k(const float* __restrict__ can
         s_id[l] = (int)id;
     }
     wave_lds_sync();
-    if (l == 0) {
-        if (valid_k == 0) {
+    if (valid_k == 0) {
+        if (l == 0) {
             out_id[0] = 0;
             if (out_conf) out_conf[0] = 0.0f;
-        } else {
-            float margin = 30.0f;
-            const int chosen = keyed_choose_serial(s_sc, s_id, valid_k, seed, temperature, top_p, min_p, position, &margin, s_pr);
-            if (!__builtin_isfinite(margin)) margin = -30.0f;
-            out_id[0] = (u32)s_id[chosen] != MW_NONE ? s_id[chosen] : 0;
-            if (out_conf) out_conf[0] = 1.0f / (1.0f + expf(-margin));
         }
+        return;
+    }
+    // the device keyed choose over the sorted candidates (keyed.cuh:50-112): greedy with the first two's gap at T = 0,
+    // otherwise try_choose on the wave with the margin of the chosen Gumbel score
+    float margin = 30.0f;
+    int chosen = 0;
+    if (temperature == 0.0) margin = valid_k > 1 ? s_sc[0] - s_sc[1] : 30.f;
+    else chosen = keyed_choose_wave(s_sc, (const u32*)s_id, valid_k, seed, temperature, top_p, min_p, position, &margin);
+    if (!__builtin_isfinite(margin)) margin = -30.0f;
+    if (l == 0) {
+        out_id[0] = (u32)s_id[chosen] != MW_NONE ? s_id[chosen] : 0;
+        if (out_conf) out_conf[0] = 1.0f / (1.0f + expf(-margin));
     }
 }
 
@@ -874,7 +947,7 @@ int launch_markov_walk(void* logits, int* ids, float* conf, const void* embed, c
     float* lg = (float*)logits;
     int* cids = (int*)cand_ids_ws;
     float* cs = (float*)cand_scores_ws;
-    hipLaunchKernelGGL(mw_cands_k, dim3(walk_rows), dim3(MW_NT), 0, st, (const float*)lg, cids, vocab);
+    hipLaunchKernelGGL(mw_cands_k, dim3(walk_rows), dim3(MW_CT), 0, st, (const float*)lg, cids, vocab);
     for (int k = 0; k < walk_rows; ++k) {
         hipLaunchKernelGGL(mw_bias_k, dim3(MW_CAND / ((MW_NT / 32) * 4)), dim3(MW_NT), 0, st, lg + (size_t)k * vocab, (const int*)(ids + k),
                            (const u16*)embed, (const u16*)head, (const int*)(cids + (size_t)k * MW_CAND), cs, vocab);
