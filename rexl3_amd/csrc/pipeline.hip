@@ -25,9 +25,6 @@ namespace {
 #ifndef GBS_FAST_THREADS
 #define GBS_FAST_THREADS 512
 #endif
-#ifndef GBS_FAST_BUFS
-#define GBS_FAST_BUFS 2  // wave-steps in flight per wave
-#endif
 constexpr int NT = GBS_FAST_THREADS;
 constexpr int NW = NT / WAVE;
 #ifndef GBS_EXP_NOPEN
@@ -294,17 +291,28 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
     u64 t_stream = 0;
     __shared__ u64 s_tseed;
 #endif
-    __shared__ int s_next;
-    if (tid == 0) {
-        s_thr = 0;
-        s_next = NW;
-    }
-    if (tid < NW * WaveTop<BUF>::TOPN) s_top[tid] = 0;
-    __syncthreads();
     const size_t esz = DT == GBS_DTYPE_F32 ? 4 : 2;
     const void* row = (const char*)logits + (size_t)r * (size_t)stride * esz;
     const int* crow = COUNTS ? counts + (size_t)r * vocab : nullptr;
     const u32* mrow = MASK ? mask + (size_t)r * ((vocab + 31) / 32) : nullptr;
+    const int lo = sp * chunk;
+    const int hi = min(vocab, lo + chunk);
+    // Wave-steps of WSTEP contiguous elements: wave w's first two (w and NW + w) are fixed, so their loads go out at
+    // once, before the block's first barrier and the row's parameters; later ones come from an LDS counter.
+    const int nws = vec ? (hi - lo + WSTEP - 1) / WSTEP : 0;
+    const RowRsrc R{rsrc(row, (u32)vocab * (u32)esz), rsrc(crow, COUNTS ? (u32)vocab * 4u : 0u),
+                    rsrc(mrow, MASK ? (u32)((vocab + 31) / 32) * 4u : 0u)};
+    auto wstep_e = [&](int idx) { return lo + idx * WSTEP + l * 4; };
+    RawStep<DT> A, B;
+    if (w < nws) load_step<DT, COUNTS, MASK>(R, (u32)wstep_e(w), A);
+    if (NW + w < nws) load_step<DT, COUNTS, MASK>(R, (u32)wstep_e(NW + w), B);
+    __shared__ int s_next;
+    if (tid == 0) {
+        s_thr = 0;
+        s_next = 2 * NW;
+    }
+    if (tid < NW * WaveTop<BUF>::TOPN) s_top[tid] = 0;
+    __syncthreads();
     const RowParamsDev p = params[r];
     const float u = uniforms[r];
     const bool invalid = params_invalid(p, u) || p.top_k < 1 || p.top_k > kmax;
@@ -312,8 +320,6 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
     const float rinv = 1.0f / p.repetition;
     const float rep = p.repetition, freq = p.frequency, pres = p.presence;  // plain scalars for the element loop
     const float clp = p.temperature > 0.0f ? temp_scale(p.temperature) : 1.44269504088896340736f;
-    const int lo = sp * chunk;
-    const int hi = min(vocab, lo + chunk);
 
     WaveTop<BUF> wt;
     wt.init(s_buf[w], count, FLOOR_KEY, &s_thr);
@@ -372,10 +378,6 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
         // the memory system serves late do not hold the block. The last wave-step may run past the chunk: its loads
         // stay inside the row (the buffer resource returns zeros past the row's end) and its out-of-chunk groups are
         // masked to -inf.
-        const int nws = (hi - lo + WSTEP - 1) / WSTEP;
-        const u32 esz = DT == GBS_DTYPE_F32 ? 4u : 2u;
-        const RowRsrc R{rsrc(row, (u32)vocab * esz), rsrc(crow, COUNTS ? (u32)vocab * 4u : 0u),
-                        rsrc(mrow, MASK ? (u32)((vocab + 31) / 32) * 4u : 0u)};
         constexpr int NE = HALF * 4;
         auto penal_fn = [&](RawStep<DT>& B, int h, int e, bool guard, float (&lv)[NE]) __attribute__((always_inline)) {
 #pragma unroll
@@ -487,7 +489,6 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
             reload();
             rank_fn(lv, e);
         };
-        auto wstep_e = [&](int idx) { return lo + idx * WSTEP + l * 4; };
         // Two wave-steps in flight per wave: A and B alternate; a buffer is reloaded with the next wave-step as soon
         // as it is ranked. A wave-step index at or past nws loads nothing and ends the loop.
         auto grab = [&]() {
@@ -495,21 +496,8 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
             if (l == 0) t = __hip_atomic_fetch_add(&s_next, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             return __builtin_amdgcn_readfirstlane(t);
         };
-#if GBS_FAST_BUFS == 3
-        RawStep<DT> A, B, C;
-        int ia = w;
-        int ib = grab();
-        int ic = grab();
-        if (ia < nws) load_step<DT, COUNTS, MASK>(R, (u32)wstep_e(ia), A);
-        if (ib < nws) load_step<DT, COUNTS, MASK>(R, (u32)wstep_e(ib), B);
-        if (ic < nws) load_step<DT, COUNTS, MASK>(R, (u32)wstep_e(ic), C);
-#else
-        RawStep<DT> A, B;
-        int ia = w;
-        int ib = grab();
-        if (ia < nws) load_step<DT, COUNTS, MASK>(R, (u32)wstep_e(ia), A);
-        if (ib < nws) load_step<DT, COUNTS, MASK>(R, (u32)wstep_e(ib), B);
-#endif
+        int ia = w;       // loaded at the kernel's start
+        int ib = NW + w;  // likewise
         if (ia >= nws) {
             // no wave-step of its own: take part in the block's seeding barrier
             wt.seed(0u);
@@ -528,12 +516,6 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
                 if (ib >= nws) break;
                 step_fn(B, wstep_e(ib), ib, false, [&]() { refill(B, nb); });
                 ib = nb;
-#if GBS_FAST_BUFS == 3
-                if (ic >= nws) break;
-                int nc = 0;
-                step_fn(C, wstep_e(ic), ic, false, [&]() { refill(C, nc); });
-                ic = nc;
-#endif
                 if (ia >= nws) break;
             }
         }
