@@ -300,37 +300,42 @@ __global__ void __launch_bounds__(KNT, 1) keyed_fast_k(const void* logits, long 
     __shared__ int s_next;
     const int S = gridDim.x, sp = blockIdx.x, r = blockIdx.y;
     const int tid = threadIdx.x, w = tid / WAVE, l = lane_id();
+    const size_t esz = DT == DT_F32 ? 4 : 2;
+    const void* row = (const char*)logits + (size_t)r * (size_t)stride * esz;
+    const int lo = sp * chunk;
+    const int hi = min(valid, lo + chunk);
+    // loads past the row's valid columns (rounded up to a whole group, inside the row) return zeros; the last
+    // wave-step's elements at or past `hi` are not offered
+    const u32 nbytes = (u32)((valid + 3) / 4 * 4) * (u32)esz;
+    const __amdgpu_buffer_rsrc_t R = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(row), (short)0, (int)nbytes, 0x00020000);
+    const int nws = vec ? (hi - lo + KWSTEP - 1) / KWSTEP : 0;
+    auto load = [&](int idx, KRaw<DT>& b) {
+        const u32 e = (u32)(lo + idx * KWSTEP + l * 4);
+#pragma unroll
+        for (int j = 0; j < KGROUPS; ++j) {
+            if constexpr (DT == DT_F32) b.x[j] = __builtin_amdgcn_raw_buffer_load_b128(R, (e + j * KGS) * 4u, 0, 2);
+            else b.x[j] = __builtin_amdgcn_raw_buffer_load_b64(R, (e + j * KGS) * 2u, 0, 2);
+        }
+    };
+    // wave w's first two wave-steps (w and KNW + w) are fixed: their loads go out before the block's first barrier and
+    // the row's parameters; later ones come from an LDS counter
+    KRaw<DT> A, B;
+    if (w < nws) load(w, A);
+    if (KNW + w < nws) load(KNW + w, B);
     if (tid == 0) {
         s_thr = 0;
-        s_next = KNW;
+        s_next = 2 * KNW;
     }
     if (tid < KNW * WaveTop<KBUF>::TOPN) s_top[tid] = 0;
     __syncthreads();
-    const size_t esz = DT == DT_F32 ? 4 : 2;
-    const void* row = (const char*)logits + (size_t)r * (size_t)stride * esz;
     const KeyedRowDev p = params[r];
     const bool ok = keyed_params_ok(p);
     const int count = ok ? min(p.top_k + 8, valid) : min(WAVE, valid);
-    const int lo = sp * chunk;
-    const int hi = min(valid, lo + chunk);
     WaveTop<KBUF> wt;
     wt.init(s_buf[w], count, 0ull, &s_thr);
     wt.set_top(s_top, w, KNW);
     int e0 = lo;
     if (vec) {
-        // loads past the row's valid columns (rounded up to a whole group, inside the row) return zeros; the last
-        // wave-step's elements at or past `hi` are not offered
-        const u32 nbytes = (u32)((valid + 3) / 4 * 4) * (u32)esz;
-        const __amdgpu_buffer_rsrc_t R = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(row), (short)0, (int)nbytes, 0x00020000);
-        const int nws = (hi - lo + KWSTEP - 1) / KWSTEP;
-        auto load = [&](int idx, KRaw<DT>& b) {
-            const u32 e = (u32)(lo + idx * KWSTEP + l * 4);
-#pragma unroll
-            for (int j = 0; j < KGROUPS; ++j) {
-                if constexpr (DT == DT_F32) b.x[j] = __builtin_amdgcn_raw_buffer_load_b128(R, (e + j * KGS) * 4u, 0, 2);
-                else b.x[j] = __builtin_amdgcn_raw_buffer_load_b64(R, (e + j * KGS) * 2u, 0, 2);
-            }
-        };
         auto grab = [&]() {
             int t = 0;
             if (l == 0) t = __hip_atomic_fetch_add(&s_next, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -409,11 +414,8 @@ __global__ void __launch_bounds__(KNT, 1) keyed_fast_k(const void* logits, long 
                 }
             }
         };
-        KRaw<DT> A, B;
-        int ia = w;
-        int ib = grab();
-        if (ia < nws) load(ia, A);
-        if (ib < nws) load(ib, B);
+        int ia = w;        // loaded at the kernel's start
+        int ib = KNW + w;  // likewise
         if (ia >= nws) {
             // no wave-step of its own: take part in the block's seeding barrier
             wt.seed(0u);
