@@ -69,7 +69,10 @@ constexpr int BUF = WAVE * (FLUSH_GROUPS * 4 + 1);
 constexpr u64 FLOOR_KEY = ((u64)NEG_INF_KEY << 32) | 0xFFFFFFFFull;  // every -inf key is at or below it
 
 constexpr int FAST_TARGET_BLOCKS = GBS_FAST_BLOCKS;
-constexpr int FAST_MIN_CHUNK = 4096;
+#ifndef GBS_FAST_MIN_CHUNK
+#define GBS_FAST_MIN_CHUNK 8192
+#endif
+constexpr int FAST_MIN_CHUNK = GBS_FAST_MIN_CHUNK;  // elements: a row is split into chunks of at least this many
 
 size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
