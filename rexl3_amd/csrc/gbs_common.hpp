@@ -184,6 +184,23 @@ __device__ __forceinline__ u64 wave_sort_asc(u64 v) {
     return v;
 }
 
+// ascending bitonic sort of one u32 per lane (lane 0 ends with the smallest)
+__device__ __forceinline__ u32 wave_sort_asc32(u32 v) {
+    const int l = lane_id();
+#pragma unroll
+    for (int k = 2; k <= WAVE; k <<= 1) {
+#pragma unroll
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            const u32 o = xor_lane(v, j);
+            const bool lower = (l & j) == 0;
+            const bool asc = (l & k) == 0;
+            const bool keep_min = (lower == asc);
+            v = keep_min ? (v < o ? v : o) : (v > o ? v : o);
+        }
+    }
+    return v;
+}
+
 // descending bitonic clean-up of a bitonic sequence
 __device__ __forceinline__ u64 wave_bitonic_desc(u64 v) {
     const int l = lane_id();

@@ -202,7 +202,7 @@ __device__ RowOut finish_row(u64 list, const RowParamsDev& p, float u, bool inva
         o.prob = 1.0f;
     } else {
         const float c2 = temp_scale(p.temperature);
-        const u64 E = valid ? mass(lval, M, c2) : 0ull;
+        const u64 E = valid ? (mass_fast_ok(M, c2) ? mass_fast(lval, M, c2) : mass(lval, M, c2)) : 0ull;
         const u64 C = wave_scan_u64(E);
         const u64 zk = readlane64(C, WAVE - 1);
         int keep = kn;
@@ -243,16 +243,18 @@ __device__ RowOut finish_row(u64 list, const RowParamsDev& p, float u, bool inva
             o.id = (int)best;
             o.prob = (float)((double)readlane64(E, f) / (double)z);
         } else {
-            // kept tokens in ascending id order: sort (id, rank) pairs
-            const u64 sk = wave_sort_asc(kept ? (((u64)key_id(list) << 32) | (u64)l) : ~0ull);
-            const bool skept = sk != ~0ull;
-            const int rank = (int)(u32)sk;
+            // kept tokens in ascending id order: sort (id << 6 | rank) in 32 bits (ids below 2^25, ranks below 64)
+            static_assert(GBS_MAX_VOCAB <= (1 << 25), "ids fit in 26 bits beside a 6-bit rank");
+            const u32 sk = wave_sort_asc32(kept ? ((key_id(list) << 6) | (u32)l) : 0xFFFFFFFFu);
+            const bool skept = sk != 0xFFFFFFFFu;
+            const int rank = (int)(sk & 63u);
             const u64 Es = shfl64(E, skept ? rank : 0);
             const u64 cum = wave_scan_u64(skept ? Es : 0ull);
             const u64 hit = ballot(skept && cum > t);
             const int f = hit ? (int)__builtin_ctzll(hit) : 0;
-            chosen_rank = (int)(u32)readlane64(sk, f);
-            o.id = (int)(readlane64(sk, f) >> 32);
+            const u32 skf = (u32)__builtin_amdgcn_readlane((int)sk, f);
+            chosen_rank = (int)(skf & 63u);
+            o.id = (int)(skf >> 6);
             const u64 ec = readlane64(Es, f);
             o.prob = (float)((double)ec / (double)z);
         }
