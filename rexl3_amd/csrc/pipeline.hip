@@ -27,6 +27,10 @@ namespace {
 #endif
 constexpr int NT = GBS_FAST_THREADS;
 constexpr int NW = NT / WAVE;
+// GBS_EXP_*: measurement variants, all off in the product build. Each drops or instruments one stage, to measure
+// its cost with the loads kept live (NOPEN penalties, NOSEL selection, NOLSE log-sum-exp, NOFINISH / NOFINISH2 the
+// block merge and row finish, BARE everything but the loads, TIMES per-row wall-clock stamps, STATS gate and merge
+// counts, ORACLE_GATE a gate seeded from the row's true threshold).
 #ifndef GBS_EXP_NOPEN
 #define GBS_EXP_NOPEN 0
 #endif
