@@ -55,6 +55,9 @@ constexpr int NW = NT / WAVE;
 #ifndef GBS_EXP_ORACLE_GATE
 #define GBS_EXP_ORACLE_GATE 0
 #endif
+#ifndef GBS_FAST_LATE_B
+#define GBS_FAST_LATE_B 1  // the second buffer's first load: 0 at the start, 1 once the first's data has arrived, 2 after the seeding barrier
+#endif
 #ifndef GBS_FAST_GROUPS
 #define GBS_FAST_GROUPS 4
 #endif
@@ -314,7 +317,10 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
     auto wstep_e = [&](int idx) { return lo + idx * WSTEP + l * 4; };
     RawStep<DT> A, B;
     if (w < nws) load_step<DT, COUNTS, MASK>(R, (u32)wstep_e(w), A);
-    if (NW + w < nws) load_step<DT, COUNTS, MASK>(R, (u32)wstep_e(NW + w), B);
+    if (!GBS_FAST_LATE_B && NW + w < nws) load_step<DT, COUNTS, MASK>(R, (u32)wstep_e(NW + w), B);
+    auto late_b = [&](int when) {
+        if (GBS_FAST_LATE_B == when && NW + w < nws) load_step<DT, COUNTS, MASK>(R, (u32)wstep_e(NW + w), B);
+    };
     __shared__ int s_next;
     if (tid == 0) {
         s_thr = 0;
@@ -474,6 +480,7 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
             if (guard) penal_fn(B, 0, e, true, lv);
             else penal_fn(B, 0, e, false, lv);
             if (first) {
+                late_b(1);  // after this wave-step's data has arrived
                 // the gate starts from the lanes' maxima of the first wave-step: the wave's count-th largest of
                 // them, then the block bound of every wave's best ones
                 u32 m = 0;
@@ -484,6 +491,7 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
                 }
                 wt.seed(m);
                 __syncthreads();
+                late_b(2);
 #if GBS_EXP_TIMES
                 if (tid == 0) s_tseed = wall_clock64();
 #endif
