@@ -242,6 +242,9 @@ __device__ __forceinline__ bool keyed_params_ok(const KeyedRowDev& p) {
 // 4-element groups per lane) are handed out through an LDS counter, two in flight per wave; each wave keeps its gated
 // top-64 list, the gate raised by the block bound of every wave's best keys. With one block per row the block merges
 // its wave lists and draws; otherwise the blocks hand their lists to the row's last block.
+#ifndef GBS_KEYED_LATE_B
+#define GBS_KEYED_LATE_B 1  // each wave's second wave-step issued once its first has arrived (0: at the start)
+#endif
 #ifndef GBS_KEYED_NT
 #define GBS_KEYED_NT 1024
 #endif
@@ -317,11 +320,13 @@ __global__ void __launch_bounds__(KNT, 1) keyed_fast_k(const void* logits, long 
             else b.x[j] = __builtin_amdgcn_raw_buffer_load_b64(R, (e + j * KGS) * 2u, 0, 2);
         }
     };
-    // wave w's first two wave-steps (w and KNW + w) are fixed: their loads go out before the block's first barrier and
-    // the row's parameters; later ones come from an LDS counter
+    // wave w's first two wave-steps (w and KNW + w) are fixed: the first's loads go out before the block's first barrier
+    // and the row's parameters, the second's once the first has arrived (a lighter queue ahead of the seeding barrier);
+    // later ones come from an LDS counter
     KRaw<DT> A, B;
+    KRaw<DT>& B0 = B;  // the second buffer, under a name the step lambda's parameter does not hide
     if (w < nws) load(w, A);
-    if (KNW + w < nws) load(KNW + w, B);
+    if (!GBS_KEYED_LATE_B && KNW + w < nws) load(KNW + w, B);
     if (tid == 0) {
         s_thr = 0;
         s_next = 2 * KNW;
@@ -392,6 +397,7 @@ __global__ void __launch_bounds__(KNT, 1) keyed_fast_k(const void* logits, long 
                     k[j * 4 + q] = in[j * 4 + q] ? kj[q] : 0u;
                 }
             }
+            if (first && GBS_KEYED_LATE_B && KNW + w < nws) load(KNW + w, B0);  // once this wave-step has arrived
             reload();
             if (first) {
                 u32 m = 0;
