@@ -27,7 +27,7 @@ namespace {
 #define GBS_SPEC_BLOCKS 1024
 #endif
 #ifndef GBS_SPEC_U
-#define GBS_SPEC_U 4
+#define GBS_SPEC_U 2  // 4-element groups in flight per thread (config 5: 2 -> 127 us, 4 -> 130.5 us, 6 -> 195 us)
 #endif
 #ifndef GBS_SPEC_AUX_FWD
 #define GBS_SPEC_AUX_FWD 2  // cache policy of the forward sweeps' loads (2: non-temporal)
