@@ -149,7 +149,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t full_rsrc(const void* base, u3
 // Streams the row tile by tile (tile t: elements [t * TILE, (t + 1) * TILE), thread tid the group at t * TILE + 4 tid),
 // calling f(t, e, l) with the group's penalised, masked logits; every thread calls f for every tile, so f may hold
 // block barriers. Rows that allow 16-byte loads keep the loads of DEPTH tiles in flight.
-constexpr int DEPTH = 4;
+#ifndef GBS_FULL_DEPTH
+#define GBS_FULL_DEPTH 2  // tiles in flight per thread (config 3: 1 -> 115.7 us, 2 -> 116.8, 3 -> 119, 4 -> 120.9)
+#endif
+constexpr int DEPTH = GBS_FULL_DEPTH;
 template <int DT, bool COUNTS, bool MASK, class F>
 __device__ __forceinline__ void stream_tiles(const Row<DT, COUNTS, MASK>& R, int t0, int t1, F&& f) {
     const int tid = threadIdx.x;
