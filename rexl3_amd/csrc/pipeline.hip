@@ -2,8 +2,8 @@
 // one caller uniform per row), exact in integer masses. The definition of every step is in gbs_modeu.hpp and in the
 // comment of sample_fast_k.
 //
-// Single-pass kernel (kmax in [1, 64]): grid (splits, rows) x 1024 threads; at 256 rows and more one block per row.
-// One read of the row's logits, counts and mask words, in wave-steps of 2048 contiguous elements handed out through an
+// Single-pass kernel (kmax in [1, 64]): grid (splits, rows) x 512 threads (8 waves); at 256 rows and more one block per row.
+// One read of the row's logits, counts and mask words, in wave-steps of 1024 contiguous elements handed out through an
 // LDS counter. Per element a lane computes the penalised, masked logit, the NaN flag and the online log-sum-exp, and
 // offers the order key to its wave's gated top-64 list. The waves' lists are merged by a tree in LDS; with one block per
 // row wave 0 then finishes the row (masses of the <= 64 candidates, the exact top-p cut and min-p filter, the draw in
