@@ -467,7 +467,6 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
                 }
             }
         };
-        // rank one loaded wave-step (idx: its index; the last one is guarded; the first of each wave seeds the gate)
         // rank one loaded wave-step (idx: its index; the last one is guarded; the first of each wave seeds the gate).
         // `reload` runs as soon as the step's logits are computed: the buffer's registers are free from there on, so
         // the next load is in flight while this step is ranked.
