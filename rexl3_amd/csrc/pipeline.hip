@@ -26,6 +26,14 @@ namespace {
 #define GBS_FAST_THREADS 512
 #endif
 constexpr int NT = GBS_FAST_THREADS;
+#ifndef GBS_FAST_LOAD_AUX
+#define GBS_FAST_LOAD_AUX 2
+#endif
+constexpr int LOAD_AUX = GBS_FAST_LOAD_AUX;  // cache-policy bits of the logits and counts loads (2: non-temporal)
+#ifndef GBS_FAST_MASK_AUX
+#define GBS_FAST_MASK_AUX 0
+#endif
+constexpr int MASK_AUX = GBS_FAST_MASK_AUX;  // cache-policy bits of the mask-word loads
 constexpr int NW = NT / WAVE;
 // GBS_EXP_*: measurement variants, all off in the product build. Each drops or instruments one stage, to measure
 // its cost with the loads kept live (NOPEN penalties, NOSEL selection, NOLSE log-sum-exp, NOFINISH / NOFINISH2 the
@@ -149,10 +157,10 @@ __device__ __forceinline__ void load_step(const RowRsrc& R, u32 e, RawStep<DT>& 
 #pragma unroll
     for (int j = 0; j < GROUPS; ++j) {
         // logits and counts are read once: non-temporal loads (cache policy bit 1)
-        if constexpr (DT == GBS_DTYPE_F32) r.x[j] = __builtin_amdgcn_raw_buffer_load_b128(R.x, (e + j * GS) * ESZ, 0, 2);
-        else r.x[j] = __builtin_amdgcn_raw_buffer_load_b64(R.x, (e + j * GS) * ESZ, 0, 2);
-        if constexpr (COUNTS) r.c[j] = __builtin_amdgcn_raw_buffer_load_b128(R.c, (e + j * GS) * 4u, 0, 2);
-        if constexpr (MASK) r.m[j] = __builtin_amdgcn_raw_buffer_load_b32(R.m, ((e >> 5) + j * (GS / 32)) * 4u, 0, 0);
+        if constexpr (DT == GBS_DTYPE_F32) r.x[j] = __builtin_amdgcn_raw_buffer_load_b128(R.x, (e + j * GS) * ESZ, 0, LOAD_AUX);
+        else r.x[j] = __builtin_amdgcn_raw_buffer_load_b64(R.x, (e + j * GS) * ESZ, 0, LOAD_AUX);
+        if constexpr (COUNTS) r.c[j] = __builtin_amdgcn_raw_buffer_load_b128(R.c, (e + j * GS) * 4u, 0, LOAD_AUX);
+        if constexpr (MASK) r.m[j] = __builtin_amdgcn_raw_buffer_load_b32(R.m, ((e >> 5) + j * (GS / 32)) * 4u, 0, MASK_AUX);
     }
 }
 
