@@ -38,23 +38,6 @@ __device__ __forceinline__ double keyed_uniform(u64 seed, u64 position, u64 id) 
     return u < below_one ? u : below_one;
 }
 
-// numpy's float64 pairwise sum for n <= 128 (crates/sampling/src/lib.rs:152-173)
-__device__ double pairwise_small(const double* a, int n) {
-    if (n < 8) {
-        double r = 0.0;
-        for (int i = 0; i < n; ++i) r += a[i];
-        return r;
-    }
-    double r[8];
-    for (int j = 0; j < 8; ++j) r[j] = a[j];
-    int i = 8;
-    for (; i < n - (n % 8); i += 8)
-        for (int j = 0; j < 8; ++j) r[j] += a[i + j];
-    double res = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
-    for (; i < n; ++i) res += a[i];
-    return res;
-}
-
 __device__ __forceinline__ double readlane_f64(double v, int lane) {
     return __longlong_as_double((long long)readlane64((u64)__double_as_longlong(v), lane));
 }
@@ -490,13 +473,24 @@ __global__ void __launch_bounds__(KNT, 1) keyed_fast_k(const void* logits, long 
 }
 
 // ------------------------------------------------------------------------------------------------ selector walk
-// The draft head's selector chain walk (crates/cuda/csrc/dflash2.cu:436-519, 595-660): per sequence, each draft row's
-// candidates are scored as unary[c] + <pred[prev] * gate[row], succ[c]> and the row's pick becomes the next row's
-// predecessor. One block of WT threads per sequence. The dot products follow the reference kernel's arithmetic (32-lane
-// groups: lane l sums r = l, l + 32, ... with fused multiply-adds, then an xor butterfly over offsets 16 .. 1), so a
-// score is the same float; half-waves play the 32-lane groups. The pick is `keyed_choose` (the reference's device
-// try_choose over all k candidates, NaN scores last, with the winner's margin) for a keyed sequence, else the first
-// maximum.
+// The draft head's selector chain walk (crates/cuda/csrc/dflash2.cu:436-519 kernel, 595-660 entry points): per
+// sequence, each draft row's k <= 64 candidates are scored as unary[c] + <pred[prev] * gate[row], succ[c]>, and the
+// row's pick becomes the next row's predecessor.
+//
+// Layout: one block of WALK_NW waves per sequence, one candidate per lane. The score's float value is fixed by the
+// reference: the dot product is 32 partial sums, partial j a chain of fused multiply-adds over r = j, j + 32, ...
+// (ascending), combined by an xor butterfly over offsets 16, 8, 4, 2, 1. Here wave w computes partials
+// 8w .. 8w + 7 of every candidate (lane c reads 8 consecutive f16 of succ[c] per 32-element slice: one 16-byte load),
+// the partials meet in LDS, and wave 0 replays the butterfly inside each lane: at offset o, s[j] += s[j + o] for j < o
+// (IEEE addition commutes, so this is the value every lane of the butterfly ends with).
+//
+// The pick, on wave 0:
+//  - unkeyed: the first maximum in candidate order (strict >; a NaN first score stays the pick), with the gap to the
+//    runner-up capped at 30;
+//  - keyed (crates/cuda/csrc/keyed.cuh:50-112 semantics): each lane's place in the order (score desc, id asc, NaN
+//    last, ties in candidate order) is counted against the other lanes' (score, id) pairs, the candidates are placed
+//    in that order in LDS, then keyed_choose_wave runs try_choose over all k. Temperature 0 takes the first in order,
+//    with the raw score gap to the second as its margin.
 
 struct WalkSamplingDev {
     u64 seed, first_position;
@@ -505,123 +499,161 @@ struct WalkSamplingDev {
 };
 static_assert(sizeof(WalkSamplingDev) == 48, "WalkSampling is 48 bytes");
 
-constexpr int WT = 256;
+constexpr int WALK_NW = 4;                 // waves per sequence
+constexpr int WALK_NT = WALK_NW * WAVE;    // threads per sequence
+constexpr int WALK_PW = 32 / WALK_NW;      // partial sums per wave
+constexpr int WALK_MAX_RANK = 8192;
+static_assert(WALK_PW == 8, "one 16-byte f16 load feeds a wave's partials of one 32-element slice");
 
-// crates/cuda/csrc/keyed.cuh:50-112, on one thread, in the reference's order of operations
-__device__ int keyed_choose_serial(const float* scores, const int* c_row, int k, u64 seed, double temperature, double top_p, double min_p,
-                                   u64 position, float* margin, double* pr) {
-    int ord[64];
-    for (int i = 0; i < k; ++i) {
-        int j = i;
-        while (j > 0) {
-            const float va = scores[ord[j - 1]], vb = scores[i];
-            const bool before = (vb > va) || (vb == va && c_row[i] < c_row[ord[j - 1]]) || (va != va && vb == vb);
-            if (!before) break;
-            ord[j] = ord[j - 1];
-            --j;
-        }
-        ord[j] = i;
-    }
-    if (temperature == 0.0) {
-        *margin = k > 1 ? scores[ord[0]] - scores[ord[1]] : 30.f;
-        return ord[0];
-    }
-    const double t = temperature > 1e-6 ? temperature : 1e-6;
-    int keep = k;
-    if (top_p > 0.0 && top_p < 1.0) {
-        const double mx = (double)scores[ord[0]] / t;
-        for (int i = 0; i < k; ++i) pr[i] = exp((double)scores[ord[i]] / t - mx);
-        const double total = pairwise_small(pr, k);
-        double c = 0.0;
-        int below = 0;
-        for (int i = 0; i < k; ++i) {
-            c += pr[i] / total;
-            if (c < top_p) ++below;
-        }
-        keep = below + 1 < k ? below + 1 : k;
-    }
-    if (min_p > 0.0) {
-        const double floor_v = (double)scores[ord[0]] / t + log(min_p);
-        int n = 0;
-        for (int i = 0; i < keep; ++i)
-            if ((double)scores[ord[i]] / t >= floor_v) ++n;
-        keep = n > 1 ? n : 1;
-    }
-    int best = 0;
-    double best_score = -INFINITY, second_score = -INFINITY;
-    for (int i = 0; i < keep; ++i) {
-        const double u = keyed_uniform(seed, position, (u64)(u32)c_row[ord[i]]);
-        const double score = (double)scores[ord[i]] / t + (-log(-log(u)));
-        if (score > best_score) {
-            second_score = best_score;
-            best_score = score;
-            best = i;
-        } else if (score > second_score) {
-            second_score = score;
-        }
-    }
-    *margin = keep > 1 ? (float)fmin(best_score - second_score, 30.0) : 30.f;
-    return ord[best];
+__device__ __forceinline__ float walk_gate(const void* gate, bool gate_f32, size_t at) {
+    return gate_f32 ? ((const float*)gate)[at] : __uint_as_float((u32)((const u16*)gate)[at] << 16);
 }
 
-__global__ void __launch_bounds__(WT) walk_k(const int* __restrict__ anchor, const int* __restrict__ ids, const float* __restrict__ vals,
-                                             const void* __restrict__ gate, int gate_f32, const __half* __restrict__ pred_cb,
-                                             const __half* __restrict__ succ_cb, int* __restrict__ out, float* __restrict__ conf, int rows,
-                                             int k, int rank, const WalkSamplingDev* __restrict__ ws, const int* __restrict__ row_off,
-                                             float* __restrict__ margin) {
-    extern __shared__ float smem[];
-    float* a_g = smem;            // [rank]
-    float* scores = smem + rank;  // [k]
-    __shared__ int s_pred;
-    __shared__ double s_pr[64];
-    const int b = blockIdx.x, t = threadIdx.x;
-    const int grp = t / 32, gl = t % 32;  // 32-lane groups (half-waves), as the reference's warps
-    const int base = row_off ? row_off[b] : b * rows;
-    const int nrows = row_off ? row_off[b + 1] - base : rows;
-    if (t == 0) s_pred = anchor[b];
+// true when candidate (vb, ib, pb) comes before (va, ia, pa): score desc, id asc, NaN after every number, otherwise
+// candidate order
+__device__ __forceinline__ bool walk_before(float vb, int ib, int pb, float va, int ia, int pa) {
+    const bool nb = vb != vb, na = va != va;
+    if (nb || na) return na && !nb ? true : (nb && na ? pb < pa : false);
+    if (vb != va) return vb > va;
+    if (ib != ia) return ib < ia;
+    return pb < pa;
+}
+
+__global__ void __launch_bounds__(WALK_NT) walk_k(const int* __restrict__ anchor, const int* __restrict__ cand_ids,
+                                                  const float* __restrict__ unary, const void* __restrict__ gate, int gate_f32,
+                                                  const __half* __restrict__ pred_cb, const __half* __restrict__ succ_cb,
+                                                  int* __restrict__ out, float* __restrict__ conf, int rows, int k, int rank,
+                                                  const WalkSamplingDev* __restrict__ samp, const int* __restrict__ row_off,
+                                                  float* __restrict__ margin) {
+    extern __shared__ float s_ag[];                // [rank]: pred[prev] * gate[row]
+    __shared__ float s_part[32][WAVE];             // partial sums, [partial][candidate]
+    __shared__ float s_sorted_v[WAVE];
+    __shared__ u32 s_sorted_id[WAVE];
+    __shared__ int s_sorted_c[WAVE];
+    __shared__ int s_prev;
+    const int seq = blockIdx.x, w = threadIdx.x / WAVE, c = lane_id();
+    const int first = row_off ? row_off[seq] : seq * rows;
+    const int n_rows = row_off ? row_off[seq + 1] - first : rows;
+    const bool keyed = samp != nullptr && samp[seq].keyed != 0;
+    // 16-byte loads of 8 f16 need 16-byte aligned codebook rows
+    const bool vec = (rank % 8) == 0 && aligned(succ_cb, 16);
+    if (threadIdx.x == 0) s_prev = anchor[seq];
     __syncthreads();
-    for (int i = 0; i < nrows; ++i) {
-        const size_t row = (size_t)(base + i);
-        const __half* a_row = pred_cb + (size_t)s_pred * rank;
-        for (int r = t; r < rank; r += WT) {
-            const float g = gate_f32 ? ((const float*)gate)[row * rank + r]
-                                     : __uint_as_float((u32)((const u16*)gate)[row * rank + r] << 16);
-            a_g[r] = __half2float(a_row[r]) * g;
-        }
+    for (int i = 0; i < n_rows; ++i) {
+        const size_t row = (size_t)(first + i);
+        const __half* prow = pred_cb + (size_t)s_prev * rank;
+        for (int r = threadIdx.x; r < rank; r += WALK_NT) s_ag[r] = __half2float(prow[r]) * walk_gate(gate, gate_f32 != 0, row * rank + r);
         __syncthreads();
-        const int* c_row = ids + row * k;
-        const float* u_row = vals + row * k;
-        for (int c = grp; c < k; c += WT / 32) {
-            const __half* b_row = succ_cb + (size_t)c_row[c] * rank;
-            float dot = 0.f;
-            for (int r = gl; r < rank; r += 32) dot = fmaf(a_g[r], __half2float(b_row[r]), dot);
+        // partials 8w .. 8w + 7 of candidate c
+        float p[WALK_PW];
 #pragma unroll
-            for (int o = 16; o > 0; o >>= 1) dot += __shfl_xor(dot, o, 32);
-            if (gl == 0) scores[c] = u_row[c] + dot;
-        }
-        __syncthreads();
-        if (t == 0) {
-            int best = 0;
-            float bs = scores[0], mg = 30.f;
-            if (ws != nullptr && ws[b].keyed) {
-                best = keyed_choose_serial(scores, c_row, k, ws[b].seed, ws[b].temperature, ws[b].top_p, ws[b].min_p,
-                                           ws[b].first_position + (u64)i, &mg, s_pr);
-                bs = scores[best];
-            } else {
-                for (int c = 1; c < k; ++c)
-                    if (scores[c] > bs) {
-                        bs = scores[c];
-                        best = c;
+        for (int j = 0; j < WALK_PW; ++j) p[j] = 0.f;
+        if (c < k) {
+            const __half* srow = succ_cb + (size_t)cand_ids[row * k + c] * rank;
+            const int j0 = w * WALK_PW;
+            if (vec) {
+                const uint4* s16 = reinterpret_cast<const uint4*>(srow + j0);
+                const int slices = rank / 32;
+                int m = 0;
+                for (; m + 4 <= slices; m += 4) {
+                    uint4 q[4];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) q[u] = s16[(size_t)(m + u) * 4];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const __half* h = reinterpret_cast<const __half*>(&q[u]);
+                        const float* a = s_ag + (m + u) * 32 + j0;
+#pragma unroll
+                        for (int j = 0; j < WALK_PW; ++j) p[j] = fmaf(a[j], __half2float(h[j]), p[j]);
                     }
-                float second = -INFINITY;
-                for (int c = 0; c < k; ++c)
-                    if (c != best && scores[c] > second) second = scores[c];
-                mg = k > 1 ? fminf(bs - second, 30.f) : 30.f;
+                }
+                for (; m < slices; ++m) {
+                    const uint4 q = s16[(size_t)m * 4];
+                    const __half* h = reinterpret_cast<const __half*>(&q);
+                    const float* a = s_ag + m * 32 + j0;
+#pragma unroll
+                    for (int j = 0; j < WALK_PW; ++j) p[j] = fmaf(a[j], __half2float(h[j]), p[j]);
+                }
+                // rank % 8 == 0: the last partial slice has whole groups of 8, each owned by one wave
+                const int r0 = slices * 32 + j0;
+                if (r0 < rank) {
+                    const uint4 q = *reinterpret_cast<const uint4*>(srow + r0);
+                    const __half* h = reinterpret_cast<const __half*>(&q);
+#pragma unroll
+                    for (int j = 0; j < WALK_PW; ++j) p[j] = fmaf(s_ag[r0 + j], __half2float(h[j]), p[j]);
+                }
+            } else {
+                for (int base = j0; base < rank; base += 32) {
+#pragma unroll
+                    for (int j = 0; j < WALK_PW; ++j)
+                        if (base + j < rank) p[j] = fmaf(s_ag[base + j], __half2float(srow[base + j]), p[j]);
+                }
             }
-            s_pred = c_row[best];
-            out[row] = s_pred;
-            if (conf) conf[row] = bs;
-            if (margin) margin[row] = mg;
+        }
+#pragma unroll
+        for (int j = 0; j < WALK_PW; ++j) s_part[w * WALK_PW + j][c] = p[j];
+        __syncthreads();
+        if (w == 0) {
+            // the butterfly, in lane
+            float s[32];
+#pragma unroll
+            for (int j = 0; j < 32; ++j) s[j] = s_part[j][c];
+#pragma unroll
+            for (int o = 16; o > 0; o >>= 1) {
+#pragma unroll
+                for (int j = 0; j < o; ++j) s[j] = s[j] + s[j + o];
+            }
+            const int cid = c < k ? cand_ids[row * k + c] : 0x7fffffff;
+            const float score = c < k ? unary[row * k + c] + s[0] : -INFINITY;
+            int pick;       // candidate index
+            float mg;
+            if (!keyed) {
+                const float s0 = __shfl(score, 0);
+                if (s0 != s0) {
+                    pick = 0;
+                } else {
+                    float mx = (c < k && score == score) ? score : -INFINITY;
+#pragma unroll
+                    for (int m = 1; m < WAVE; m <<= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
+                    pick = (int)__builtin_ctzll(ballot(c < k && score == mx));
+                }
+                float second = (c < k && c != pick && score == score) ? score : -INFINITY;
+#pragma unroll
+                for (int m = 1; m < WAVE; m <<= 1) second = fmaxf(second, __shfl_xor(second, m));
+                const float best = __shfl(score, pick);
+                mg = k > 1 ? fminf(best - second, 30.f) : 30.f;
+            } else {
+                // place in the order: the lanes before this one, counted over (score, id) broadcasts
+                int place = 0;
+                for (int o = 0; o < k; ++o) {
+                    const float vo = __shfl(score, o);
+                    const int io = __shfl(cid, o);
+                    place += (o != c && walk_before(vo, io, o, score, cid, c)) ? 1 : 0;
+                }
+                if (c < k) {
+                    s_sorted_v[place] = score;
+                    s_sorted_id[place] = (u32)cid;
+                    s_sorted_c[place] = c;
+                }
+                wave_lds_sync();
+                const WalkSamplingDev sp = samp[seq];
+                if (sp.temperature == 0.0) {
+                    pick = s_sorted_c[0];
+                    mg = k > 1 ? s_sorted_v[0] - s_sorted_v[1] : 30.f;
+                } else {
+                    float m_out = 30.f;
+                    const int at = keyed_choose_wave(s_sorted_v, s_sorted_id, k, sp.seed, sp.temperature, sp.top_p, sp.min_p,
+                                                     sp.first_position + (u64)i, &m_out);
+                    pick = s_sorted_c[at];
+                    mg = m_out;
+                }
+            }
+            if (c == pick) {
+                s_prev = cid;
+                out[row] = cid;
+                if (conf) conf[row] = score;
+                if (margin) margin[row] = mg;
+            }
         }
         __syncthreads();
     }
@@ -1085,8 +1117,8 @@ namespace {
 int launch_walk(const void* anchor, const void* topk_ids, const void* topk_vals, const void* gate, int gate_is_f32,
                 const void* pred_codebook, const void* succ_codebook, int n_seq, int rows, int k, int rank, const void* sampling,
                 const void* row_off, void* out_tokens, void* conf, void* margin, void* stream) {
-    const size_t smem = (size_t)(rank + k) * sizeof(float);
-    hipLaunchKernelGGL(walk_k, dim3(n_seq), dim3(WT), smem, to_stream(stream), (const int*)anchor, (const int*)topk_ids,
+    const size_t smem = (size_t)rank * sizeof(float);
+    hipLaunchKernelGGL(walk_k, dim3(n_seq), dim3(WALK_NT), smem, to_stream(stream), (const int*)anchor, (const int*)topk_ids,
                        (const float*)topk_vals, gate, gate_is_f32, (const __half*)pred_codebook, (const __half*)succ_codebook,
                        (int*)out_tokens, (float*)conf, rows, k, rank, (const WalkSamplingDev*)sampling, (const int*)row_off,
                        (float*)margin);
@@ -1098,7 +1130,7 @@ GBS_EXPORT int gb_dflash_selector_walk_keyed(const void* anchor, const void* top
                                              int gate_is_f32, const void* pred_codebook, const void* succ_codebook, int n_seq, int rows,
                                              int k, int rank, const void* sampling, void* out_tokens, void* conf, void* stream) {
     if (n_seq <= 0 || rows <= 0) return 0;
-    if (k < 1 || k > 64 || rank < 1 || rank > 8192) return GBS_ERR_INVALID;
+    if (k < 1 || k > 64 || rank < 1 || rank > WALK_MAX_RANK) return GBS_ERR_INVALID;
     return launch_walk(anchor, topk_ids, topk_vals, gate, gate_is_f32, pred_codebook, succ_codebook, n_seq, rows, k, rank, sampling,
                        nullptr, out_tokens, conf, nullptr, stream);
 }
@@ -1108,7 +1140,7 @@ GBS_EXPORT int gb_dflash_selector_walk_ragged(const void* anchor, const void* to
                                               int rank, const void* sampling, const void* row_off, void* out_tokens, void* conf,
                                               void* margin, void* stream) {
     if (n_seq <= 0) return 0;
-    if (k < 1 || k > 64 || rank < 1 || rank > 8192 || !row_off) return GBS_ERR_INVALID;
+    if (k < 1 || k > 64 || rank < 1 || rank > WALK_MAX_RANK || !row_off) return GBS_ERR_INVALID;
     return launch_walk(anchor, topk_ids, topk_vals, gate, gate_is_f32, pred_codebook, succ_codebook, n_seq, 0, k, rank, sampling,
                        row_off, out_tokens, conf, margin, stream);
 }

@@ -67,20 +67,29 @@ def _require_cuda(t: torch.Tensor, name: str):
 
 
 class Workspace:
-    """Zero-initialised device workspaces, one per (device, purpose), grown on demand. The gbs_* entry points leave their
-    counters at zero after every call, so a workspace is cleared once when it is allocated."""
+    """Zero-initialised device workspaces, one per (device, stream, purpose), grown on demand. The gbs_* entry points
+    leave their arrival counters at zero after every call, so a workspace is cleared once when it is allocated.
+
+    Calls that share a workspace must not overlap; keying on the stream gives calls on different streams different
+    buffers. A buffer is allocated while its stream is current, so the caching allocator hands a replaced buffer's
+    memory only to later work on that same stream: the kernels still using it finish first."""
 
     def __init__(self):
         self._bufs = {}
 
     def get(self, device: torch.device, purpose: str, nbytes: int) -> torch.Tensor:
-        key = (str(device), purpose)
+        stream = torch.cuda.current_stream(device)
+        key = (str(device), stream.cuda_stream, purpose)
         buf = self._bufs.get(key)
         if buf is None or buf.numel() < nbytes:
-            buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
-            _lib.call("gbs_workspace_clear", _ptr(buf), buf.numel(), _stream(device))
+            with torch.cuda.stream(stream):
+                buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+            _lib.call("gbs_workspace_clear", _ptr(buf), buf.numel(), C.c_void_p(stream.cuda_stream))
             self._bufs[key] = buf
         return buf
+
+    def keys(self):
+        return list(self._bufs)
 
 
 WORKSPACE = Workspace()
@@ -330,15 +339,34 @@ def row_params(rows: int, temperature=1.0, top_p=1.0, min_p=0.0, repetition=1.0,
     return p
 
 
+def _check(t, name: str, dtype, shape: tuple, device):
+    if t is None:
+        return
+    dtypes = dtype if isinstance(dtype, tuple) else (dtype,)
+    if t.dtype not in dtypes or tuple(t.shape) != shape or not t.is_contiguous() or t.device != device:
+        raise ValueError(f"{name} must be a contiguous {dtype} tensor of shape {shape} on {device}, got {t.dtype} "
+                         f"{tuple(t.shape)} on {t.device}")
+
+
 def sample_rows(logits: torch.Tensor, params: np.ndarray | torch.Tensor, uniforms: torch.Tensor, counts: torch.Tensor | None = None,
-                mask: torch.Tensor | None = None, kmax: int = 64, logprobs: bool = False, probs: bool = True):
-    """gbs_sample_rows. Returns a dict of device tensors: ids, greedy, status, and probs / logprobs when asked."""
+                mask: torch.Tensor | None = None, kmax: int = 64, logprobs: bool = False, probs: bool = True,
+                vocab: int | None = None):
+    """gbs_sample_rows over logits [rows, stride] (f32 / bf16, row stride may exceed `vocab`: the lm_head's padded
+    layout; columns past `vocab` are never read). counts int32 [rows, vocab], mask uint32 [rows, ceil(vocab / 32)],
+    uniforms float32 [rows]. Returns a dict of device tensors: ids, greedy, status, and probs / logprobs when asked."""
     _require_cuda(logits, "logits")
     rows, stride = logits.shape
-    vocab = stride
+    vocab = stride if vocab is None else vocab
     dev = logits.device
+    if logits.dtype not in (torch.float32, torch.bfloat16) or logits.stride(1) != 1 or not 0 < vocab <= stride:
+        raise ValueError("logits must be f32 or bf16 rows with unit column stride and vocab <= stride")
+    _check(counts, "counts", torch.int32, (rows, vocab), dev)
+    _check(mask, "mask", (torch.uint32, torch.int32), (rows, -(-vocab // 32)), dev)
+    _check(uniforms, "uniforms", torch.float32, (rows,), dev)
     if isinstance(params, np.ndarray):
         params = torch.from_numpy(np.ascontiguousarray(params, dtype=ROW_PARAMS_DTYPE).view(np.uint8)).to(dev)
+    if params.numel() * params.element_size() != rows * ROW_PARAMS_DTYPE.itemsize:
+        raise ValueError("params must hold one 32-byte record per row")
     out = dict(ids=torch.empty(rows, dtype=torch.int32, device=dev), greedy=torch.empty(rows, dtype=torch.int32, device=dev),
                status=torch.empty(rows, dtype=torch.int32, device=dev))
     if probs:
@@ -347,9 +375,9 @@ def sample_rows(logits: torch.Tensor, params: np.ndarray | torch.Tensor, uniform
         out["logprobs"] = torch.empty(rows, dtype=torch.float32, device=dev)
     wsb = _lib.load().gbs_sample_workspace_bytes(rows, vocab, kmax)
     ws = WORKSPACE.get(dev, "sample", wsb)
-    _lib.call("gbs_sample_rows", _ptr(logits), DTYPE_CODE[logits.dtype], rows, stride, vocab, _ptr(counts), _ptr(mask), _ptr(params),
-              _ptr(uniforms), kmax, _ptr(out["ids"]), _ptr(out["greedy"]), _ptr(out.get("probs")), _ptr(out.get("logprobs")),
-              _ptr(out["status"]), _ptr(ws), ws.numel(), _stream(dev))
+    _lib.call("gbs_sample_rows", _ptr(logits), DTYPE_CODE[logits.dtype], rows, logits.stride(0), vocab, _ptr(counts), _ptr(mask),
+              _ptr(params), _ptr(uniforms), kmax, _ptr(out["ids"]), _ptr(out["greedy"]), _ptr(out.get("probs")),
+              _ptr(out.get("logprobs")), _ptr(out["status"]), _ptr(ws), ws.numel(), _stream(dev))
     return out
 
 

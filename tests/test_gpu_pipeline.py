@@ -351,3 +351,71 @@ def test_full_and_fast_paths_alternate_on_one_workspace():
         log(what)
         g, w = run_both(cfg, kmax=kmax)
         compare(g, w, what)
+
+
+@pytest.mark.parametrize("kmax", [64, 0])
+@pytest.mark.parametrize("vocab,pad", [(151_936, 64), (50_001, 7)])
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_padded_rows_stride_above_vocab(dtype, vocab, pad, kmax):
+    """The lm_head's padded layout (crates/cuda/csrc/glue.cu:1084-1098 reads columns [0, valid) of rows `stride` apart):
+    logits [rows, vocab + pad] whose pad columns hold NaN or +inf. A kernel that read one of them would report NanLogit
+    or pick it; the results must equal the oracle's on the unpadded rows."""
+    need_gpu()
+    rows = 16
+    cfg = W.northstar(seed=31 + pad, rows=rows, vocab=vocab)
+    if kmax == 0:
+        cfg["params"]["top_k"][::2] = 0  # the full-distribution path serves any top_k
+    x = cfg["logits"]
+    if dtype == "bf16":
+        x = W.to_bf16_bits(x)
+        full = np.empty((rows, vocab + pad), np.uint16)
+        full[:, vocab:] = np.where(np.arange(rows)[:, None] % 2 == 0, 0x7FC0, 0x7F80)
+    else:
+        full = np.empty((rows, vocab + pad), np.float32)
+        full[:, vocab:] = np.where(np.arange(rows)[:, None] % 2 == 0, np.nan, np.inf)
+    full[:, :vocab] = x
+    log(f"padded rows dtype={dtype} vocab={vocab} pad={pad} kmax={kmax}")
+    t = dev(full, torch.bfloat16) if dtype == "bf16" else dev(full)
+    g = S.sample_rows(t, cfg["params"], dev(cfg["uniforms"]), dev(cfg["counts"]), dev(cfg["mask"]), kmax=kmax, logprobs=True,
+                      vocab=vocab)
+    g = {k: host(v) for k, v in g.items()}
+    w = O.sample_rows(x, O.DTYPE_BF16 if dtype == "bf16" else O.DTYPE_F32, cfg["counts"], cfg["mask"], cfg["params"],
+                      cfg["uniforms"], threads=8)
+    assert (w["status"] == 0).all()
+    compare(g, w, f"padded {dtype} {vocab}+{pad} kmax {kmax}")
+
+
+def test_wrapper_rejects_mis_shaped_operands():
+    """The host mirror checks operand shapes before any launch: a short uniforms vector or a mask of the wrong width
+    would make the kernel read past its allocation."""
+    need_gpu()
+    cfg = W.northstar(seed=2, rows=4, vocab=4096)
+    x, c, m, u = dev(cfg["logits"]), dev(cfg["counts"]), dev(cfg["mask"]), dev(cfg["uniforms"])
+    with pytest.raises(ValueError):
+        S.sample_rows(x, cfg["params"], u[:3], c, m)
+    with pytest.raises(ValueError):
+        S.sample_rows(x, cfg["params"], u, c, m[:, :-1].contiguous())
+    with pytest.raises(ValueError):
+        S.sample_rows(x, cfg["params"], u, c.to(torch.int64), m)
+    with pytest.raises(ValueError):
+        S.sample_rows(x, cfg["params"][:3], u, c, m)
+
+
+def test_workspaces_are_per_stream():
+    """Two streams get two workspaces (their arrival counters must not be shared by overlapping calls), and both give
+    the oracle's results."""
+    need_gpu()
+    cfg = W.northstar(seed=4, rows=8, vocab=8192)
+    x, c, m, u = dev(cfg["logits"]), dev(cfg["counts"]), dev(cfg["mask"]), dev(cfg["uniforms"])
+    w = O.sample_rows(cfg["logits"], O.DTYPE_F32, cfg["counts"], cfg["mask"], cfg["params"], cfg["uniforms"])
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    torch.cuda.synchronize()
+    outs = []
+    for s in (s1, s2):
+        with torch.cuda.stream(s):
+            outs.append(S.sample_rows(x, cfg["params"], u, c, m))
+    torch.cuda.synchronize()
+    keys = [k for k in S.WORKSPACE.keys() if k[2] == "sample"]
+    assert {s1.cuda_stream, s2.cuda_stream} <= {k[1] for k in keys}
+    for o in outs:
+        assert np.array_equal(host(o["ids"]), w["ids"])

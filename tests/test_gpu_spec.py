@@ -35,6 +35,26 @@ def test_config5_full_vocab():
     assert np.array_equal(s, ws) and np.array_equal(a, wa) and np.array_equal(t, wt)
 
 
+def test_config5_at_its_own_shape():
+    """Config 5 as the bench times it: 32 sequences x (7 drafts + 1 bonus) = 256 rows of 151,936 (the one-block-per-row
+    kernel), with greedy rows whose maxima tie, and drafts the target gives no mass (certain rejections)."""
+    need_gpu()
+    cfg = W.config5(seed=5, n_seq=32, width=7)
+    V = cfg["target"].shape[1]
+    log("config5 32 x 8 x 151936")
+    cfg["temperatures"][0:8] = 0.0                  # sequence 0 greedy; its rows' maxima tie at three ids
+    for j in range(8):
+        cfg["target"][j, [V - 1, 11 + j, V // 2]] = 40.0
+    for s in (3, 9, 20):                            # certain rejection of draft 0 (p(x) = 0)
+        r = s * 8
+        cfg["target"][r, cfg["draft_ids"][s, 0]] = -np.inf
+    (a, t, s), (wa, wt, ws) = run(cfg)
+    assert (ws == 0).all()
+    assert wa[3] == 0 and wa[9] == 0 and wa[20] == 0
+    assert np.array_equal(s, ws) and np.array_equal(a, wa) and np.array_equal(t, wt)
+    log(f"accepted lengths {np.bincount(a, minlength=8)}")
+
+
 @pytest.mark.parametrize("n_seq", [6, 60])  # 24 rows: split kernels; 240 rows: one block per row
 def test_spec_greedy_and_errors(n_seq):
     need_gpu()
