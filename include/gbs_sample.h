@@ -32,6 +32,8 @@ extern "C" {
 
 #define GBS_OK 0
 #define GBS_ERR_INVALID 1
+/* gbs_sample_rows_noalloc: the call needs more workspace than its static scratch holds (2, hipErrorOutOfMemory) */
+#define GBS_ERR_NOALLOC_TOO_LARGE 2
 
 /* per-row status (crates/sampling/src/lib.rs:70-76) */
 #define GBS_ROW_OK 0
@@ -257,6 +259,20 @@ size_t gbs_sample_workspace_bytes(int rows, int vocab, int kmax);
 int gbs_sample_rows(const void* logits, int dtype, int rows, int stride, int vocab, const int32_t* counts, const uint32_t* mask,
                     const GbsRowParams* params, const float* uniforms, int kmax, int* out_ids, int* out_greedy, float* out_probs,
                     float* out_logprobs, int* out_status, void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * Allocation-free gbs_sample_rows. No counterpart in the reference: it is for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). Same arguments, meaning
+ * and results as gbs_sample_rows without `ws` / `ws_bytes`: the workspace is a static device array of
+ * GBS_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends and cleared by the first call on each GPU. A call
+ * whose gbs_sample_workspace_bytes(rows, vocab, kmax) exceeds it returns GBS_ERR_NOALLOC_TOO_LARGE with nothing
+ * launched. No hipMalloc, hipFree or allocating library call is made. Every call on one GPU shares its array: calls
+ * that overlap on one GPU (other streams, other host threads) race and must be serialised by the caller.
+ */
+#define GBS_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+int gbs_sample_rows_noalloc(const void* logits, int dtype, int rows, int stride, int vocab, const int32_t* counts,
+                            const uint32_t* mask, const GbsRowParams* params, const float* uniforms, int kmax, int* out_ids,
+                            int* out_greedy, float* out_probs, float* out_logprobs, int* out_status, void* stream);
 
 /*
  * Speculative verification by rejection (Leviathan et al. 2023 / Chen et al. 2023), exact in integer masses.

@@ -9,6 +9,7 @@
 // row wave 0 then finishes the row (masses of the <= 64 candidates, the exact top-p cut and min-p filter, the draw in
 // ascending id order, the log-probability). With several blocks per row the blocks hand their lists, LSE and NaN flag
 // to the row's last block through the workspace.
+#include <mutex>
 #include <type_traits>
 
 #include "gbs_modeu.hpp"
@@ -718,4 +719,59 @@ GBS_EXPORT int gbs_sample_rows(const void* logits, int dtype, int rows, int stri
     if (dtype == GBS_DTYPE_F32) run.template operator()<GBS_DTYPE_F32>();
     else run.template operator()<GBS_DTYPE_BF16>();
     return launch_status();
+}
+
+// ------------------------------------------------------------------------------------------------ allocation-free form
+// gbs_sample_rows for callers that cannot allocate: the workspace is this file-scope device array, one copy per GPU,
+// held until the process ends. Host code never passes the array's name to a kernel (on the host it is only a
+// stand-in): at a device's first call its device address is looked up once, with that device current, and kept per
+// device. The first call also clears the array (a fill kernel on the caller's stream, ahead of that call's launches);
+// every later call starts from the zeroed arrival counters the previous one left. Calls on one GPU share the array:
+// calls that overlap (other streams, other host threads) race.
+
+namespace {
+
+static __device__ __align__(256) unsigned char scratch[GBS_NOALLOC_SCRATCH_BYTES];
+
+constexpr int NOALLOC_MAX_DEVICES = 64;
+void* g_scratch[NOALLOC_MAX_DEVICES] = {};
+std::mutex g_scratch_mu;
+
+// the calling device's copy of `scratch`, cleared on first use; nullptr (and *rc set) on a HIP error
+void* device_scratch(void* stream, int* rc) {
+    int d = -1;
+    if ((*rc = (int)hipGetDevice(&d)) != 0) return nullptr;
+    if (d < 0 || d >= NOALLOC_MAX_DEVICES) {
+        *rc = GBS_ERR_INVALID;
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch[d] == nullptr) {
+        void* ptr = nullptr;
+        if ((*rc = (int)hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch))) != 0 || ptr == nullptr) {
+            if (*rc == 0) *rc = GBS_ERR_INVALID;
+            return nullptr;
+        }
+        if ((*rc = gbs_workspace_clear(ptr, GBS_NOALLOC_SCRATCH_BYTES, stream)) != 0) return nullptr;
+        g_scratch[d] = ptr;
+    }
+    *rc = 0;
+    return g_scratch[d];
+}
+
+}  // namespace
+
+GBS_EXPORT int gbs_sample_rows_noalloc(const void* logits, int dtype, int rows, int stride, int vocab, const int32_t* counts,
+                                       const uint32_t* mask, const GbsRowParams* params, const float* uniforms, int kmax, int* out_ids,
+                                       int* out_greedy, float* out_probs, float* out_logprobs, int* out_status, void* stream) {
+    if (rows < 0 || vocab <= 0 || vocab > GBS_MAX_VOCAB || stride < vocab || kmax < 0 || kmax > GBS_MAX_COUNT) return GBS_ERR_INVALID;
+    if (dtype != GBS_DTYPE_F32 && dtype != GBS_DTYPE_BF16) return GBS_ERR_INVALID;
+    if (rows == 0) return 0;
+    if (rows > 65535) return GBS_ERR_INVALID;
+    if (gbs_sample_workspace_bytes(rows, vocab, kmax) > GBS_NOALLOC_SCRATCH_BYTES) return GBS_ERR_NOALLOC_TOO_LARGE;
+    int rc = 0;
+    void* ws = device_scratch(stream, &rc);
+    if (ws == nullptr) return rc;
+    return gbs_sample_rows(logits, dtype, rows, stride, vocab, counts, mask, params, uniforms, kmax, out_ids, out_greedy, out_probs,
+                           out_logprobs, out_status, ws, GBS_NOALLOC_SCRATCH_BYTES, stream);
 }
