@@ -6,6 +6,10 @@ inverse-CDF draw from one uniform per row -- at B=256, V=151,936 fp32, inputs re
 gbs_sample_rows launch over the batch. Prints one JSON line.
 
     python bench.py [--steps K] [--warmup W] [--workload northstar|c1|c2|c3|c4|c5|keyed|markov] [--no-cpu]
+                    [--no-per-config]
+
+The default run (north star) also measures configs 1-5 and the keyed (reference-parity) sampler, each with its own CPU
+baseline, and reports them under "per_config" in the same line.
 """
 from __future__ import annotations
 
@@ -31,6 +35,9 @@ def parse():
     ap.add_argument("--workload", default="northstar")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--per-config-steps", type=int, default=100)
+    ap.add_argument("--per-config-cpu-seconds", type=float, default=3.0)
+    ap.add_argument("--no-per-config", action="store_true", help="north star only")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only copy 316,026,880 bytes device to device (the plain copy that scales rocprofv3 FETCH_SIZE)")
     return ap.parse_args()
@@ -68,6 +75,16 @@ def time_launches(launch, steps, warmup):
     return start.elapsed_time(end) / steps  # ms per step
 
 
+def host_threads():
+    """(threads used, cores this process may run on): every core the box gives the process, capped at 16, the CPU share
+    of one GPU on this pool."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(n, 16)), n
+
+
 def cpu_baseline_sample(cfg, seconds, threads):
     """The oracle's extended pipeline (the build's CPU restatement, there is no reference code for it) over the same
     batch, repeated until `seconds` of wall time have passed."""
@@ -87,34 +104,18 @@ def cpu_baseline_sample(cfg, seconds, threads):
     return done / el, done, el
 
 
-def main():
-    args = parse()
-    if args.gpus != 1:
-        print(f"bench.py measures one GPU: every box in this run has one, and the sampler shards by rows with no "
-              f"communication. --gpus {args.gpus} is not supported.", file=sys.stderr)
-        sys.exit(2)
+def measure(wl, args, steps, cpu_seconds, dev, lib, stream):
+    """Times `steps` launches of workload `wl` after `args.warmup` untimed ones; returns its record (and the CPU
+    baseline over `cpu_seconds` unless --no-cpu)."""
     import numpy as np
     import torch
 
-    from rexl3_amd import _lib
     from rexl3_amd import sampling as S
     from rexl3_amd import workloads as W
 
-    dev = torch.device("cuda:0")
-    if args.copy_calibration:
-        src = torch.ones(316_026_880 // 4, dtype=torch.float32, device=dev)
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        print(json.dumps({"copy_bytes": src.numel() * 4, "launches": 3}))
-        return
-    lib = _lib.load()
-    stream = C.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
-    wl = args.workload
-    threads = max(1, min(os.cpu_count() or 1, 16))
+    threads, ncores = host_threads()
+    cores_note = f"{threads} threads of the {ncores} cores this process may use (capped at 16, one GPU's CPU share)"
     cpu = None
-
     if wl in ("northstar", "c1", "c2", "c3", "c4"):
         cfg = {"northstar": W.northstar, "c1": W.config1, "c2": W.config2, "c3": W.config3, "c4": W.config4}[wl]()
         kmax = 0 if wl == "c3" else 64
@@ -143,7 +144,7 @@ def main():
             if rc:
                 raise RuntimeError(f"gbs_sample_rows returned {rc}")
 
-        ms = time_launches(launch, args.steps, args.warmup)
+        ms = time_launches(launch, steps, args.warmup)
         nbytes = algorithmic_bytes(rows, vocab, 2 if is_bf16 else 4, ct is not None, mt is not None)
         # the full path (kmax 0) runs split over fs_* launches when there are fewer rows than CUs
         kernel = ("fs_pass0_k + fs_hist_k + fs_collect_k" if rows < 256 else "sample_full_k") if kmax == 0 else "sample_fast_k"
@@ -157,13 +158,15 @@ def main():
         st = out["status"].cpu().numpy()
         assert (st[cfg["params"]["temperature"] >= 0] >= 0).all()
         if not args.no_cpu:
-            v, done, el = cpu_baseline_sample(cfg, args.cpu_seconds, threads)
-            v1, done1, el1 = cpu_baseline_sample({**cfg, "logits": cfg["logits"][:8], "counts": None if cfg["counts"] is None
-                                                  else cfg["counts"][:8], "mask": None if cfg["mask"] is None else cfg["mask"][:8],
-                                                  "params": cfg["params"][:8], "uniforms": cfg["uniforms"][:8]}, 2.0, 1)
-            cpu = {"value": round(v, 1), "unit": "rows/s", "cores": threads, "kind": "port",
+            v, done, el = cpu_baseline_sample(cfg, cpu_seconds, threads)
+            sub = min(rows, 8)
+            v1, done1, el1 = cpu_baseline_sample({**cfg, "logits": cfg["logits"][:sub], "counts": None if cfg["counts"] is None
+                                                  else cfg["counts"][:sub], "mask": None if cfg["mask"] is None else cfg["mask"][:sub],
+                                                  "params": cfg["params"][:sub], "uniforms": cfg["uniforms"][:sub]},
+                                                 min(2.0, cpu_seconds), 1)
+            cpu = {"value": round(v, 1), "unit": "rows/s", "cores": threads, "host_cores": ncores, "kind": "port",
                    "sample": f"the build's C oracle of the same pipeline on the same {rows}-row batch, repeated for "
-                             f"{el:.1f} s ({done} rows) over {threads} threads; 1 thread: {v1:.1f} rows/s ({done1} rows)",
+                             f"{el:.1f} s ({done} rows) on {cores_note}; 1 thread: {v1:.1f} rows/s ({done1} rows)",
                    "gbps": round(algorithmic_bytes(1, vocab, 2 if is_bf16 else 4, ct is not None, mt is not None) * v / 1e9, 3)}
     elif wl == "keyed":
         # the reference-parity keyed sampler: top-(k+8) of full f32 rows + try_choose, B=256, V=151,936
@@ -187,7 +190,7 @@ def main():
             if rc:
                 raise RuntimeError(f"gbs_keyed_sample_rows returned {rc}")
 
-        ms = time_launches(launch, args.steps, args.warmup)
+        ms = time_launches(launch, steps, args.warmup)
         nbytes = algorithmic_bytes(rows, vocab, 4, False, False)
         kernel = "keyed_fast_k"
         dtype = "f32 (choose in f64)"
@@ -196,13 +199,13 @@ def main():
             from oracle import oracle as O
             t0 = time.perf_counter()
             done = 0
-            while time.perf_counter() - t0 < args.cpu_seconds:
+            while time.perf_counter() - t0 < cpu_seconds:
                 O.batch_keyed_sample(x, O.DTYPE_F32, vocab, recs, 0, threads=threads)
                 done += rows
             el = time.perf_counter() - t0
-            cpu = {"value": round(done / el, 1), "unit": "rows/s", "cores": threads, "kind": "port",
+            cpu = {"value": round(done / el, 1), "unit": "rows/s", "cores": threads, "host_cores": ncores, "kind": "port",
                    "sample": f"C restatement of the reference CPU path (try_top_candidates(row, 58) + try_choose) on the same "
-                             f"batch, {done} rows in {el:.1f} s over {threads} threads"}
+                             f"batch, {done} rows in {el:.1f} s on {cores_note}"}
     elif wl == "c5":
         cfg = W.config5()
         n_seq, width = cfg["n_seq"], cfg["width"]
@@ -228,7 +231,7 @@ def main():
             if rc:
                 raise RuntimeError(f"gbs_spec_verify returned {rc}")
 
-        ms = time_launches(launch, args.steps, args.warmup)
+        ms = time_launches(launch, steps, args.warmup)
         rows = R
         nbytes = 2 * R * vocab * 4
         kernel = "spec_rows_k + spec_draw_k" if R >= 192 else "spec_max_k + spec_mass_k + spec_draw_k"
@@ -238,14 +241,14 @@ def main():
             from oracle import oracle as O
             t0 = time.perf_counter()
             done = 0
-            while time.perf_counter() - t0 < args.cpu_seconds:
+            while time.perf_counter() - t0 < cpu_seconds:
                 O.spec_verify(cfg["target"], cfg["draft"], n_seq, width, cfg["draft_ids"], cfg["temperatures"], cfg["u_accept"],
                               cfg["u_resample"], threads=threads)
                 done += R
             el = time.perf_counter() - t0
-            cpu = {"value": round(done / el, 1), "unit": "rows/s", "cores": threads, "kind": "port",
-                   "sample": f"the build's C oracle of the same verification on the same batch (its sequences over "
-                             f"{threads} threads), {done} rows in {el:.1f} s"}
+            cpu = {"value": round(done / el, 1), "unit": "rows/s", "cores": threads, "host_cores": ncores, "kind": "port",
+                   "sample": f"the build's C oracle of the same verification on the same batch (its sequences over the "
+                             f"threads), {done} rows in {el:.1f} s on {cores_note}"}
     elif wl == "markov":
         # the DSV4 draft head's keyed Markov walk: 8 walk rows over V = 129,280 (bf16 embed / head [V, 256])
         walk_rows, vocab = 8, 129_280
@@ -270,7 +273,7 @@ def main():
             if rc:
                 raise RuntimeError(f"gb_dsv4_mtp_markov_walk_keyed_bf16 returned {rc}")
 
-        ms = time_launches(launch, args.steps, args.warmup)
+        ms = time_launches(launch, steps, args.warmup)
         rows = walk_rows
         # the logits once (candidates), then per row 1024 head rows and one embedding row of 512 B
         nbytes = walk_rows * vocab * 4 + walk_rows * (1024 + 1) * 512
@@ -283,38 +286,76 @@ def main():
             hb = (hed.view(torch.int16).cpu().numpy()).view(np.uint16)
             t0 = time.perf_counter()
             done = 0
-            while time.perf_counter() - t0 < min(args.cpu_seconds, 10.0):
+            while time.perf_counter() - t0 < min(cpu_seconds, 10.0):
                 O.markov_walk(x, 17, eb, hb, walk_rows, True, 16, 1234, 0.8, 0.9, 0.0, 100)
                 done += walk_rows
             el = time.perf_counter() - t0
-            cpu = {"value": round(done / el, 1), "unit": "walk rows/s", "cores": 1, "kind": "port",
+            cpu = {"value": round(done / el, 1), "unit": "walk rows/s", "cores": 1, "host_cores": ncores, "kind": "port",
                    "sample": f"the build's C oracle of the same walk (one thread), {done} walk rows in {el:.1f} s"}
     else:
         raise SystemExit(f"unknown workload {wl}")
-
-    rows_per_s = rows / (ms / 1e3)
     achieved = nbytes / (ms / 1e3) / 1e9
+    return dict(name=wl, workload=workload, kernel=kernel, dtype=dtype, rows=rows, vocab=vocab, steps=steps, ms=ms,
+                rows_per_s=rows / (ms / 1e3), bytes=nbytes, achieved=achieved, cpu=cpu)
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: every box in this run has one, and the sampler shards by rows with no "
+              f"communication. --gpus {args.gpus} is not supported.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from rexl3_amd import _lib
+
+    dev = torch.device("cuda:0")
+    if args.copy_calibration:
+        src = torch.ones(316_026_880 // 4, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": src.numel() * 4, "launches": 3}))
+        return
+    lib = _lib.load()
+    stream = C.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    r = measure(args.workload, args, args.steps, args.cpu_seconds, dev, lib, stream)
+    per_config = None
+    if args.workload == "northstar" and not args.no_per_config:
+        per_config = {}
+        for wl in ("c1", "c2", "c3", "c4", "c5", "keyed"):
+            print(f"# per-config {wl}", file=sys.stderr, flush=True)
+            q = measure(wl, args, args.per_config_steps, args.per_config_cpu_seconds, dev, lib, stream)
+            per_config[wl] = {"workload": q["workload"], "kernel": q["kernel"], "rows": q["rows"], "vocab": q["vocab"],
+                              "steps": q["steps"], "ms_per_step": round(q["ms"], 5), "rows_per_s": round(q["rows_per_s"], 1),
+                              "bytes_per_launch": q["bytes"], "achieved_gbps": round(q["achieved"], 1),
+                              "frac": round(q["achieved"] / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(wl),
+                              "cpu_baseline": q["cpu"]}
+            torch.cuda.empty_cache()
     line = {
         "metric": METRIC,
-        "value": round(rows_per_s, 1),
+        "value": round(r["rows_per_s"], 1),
         "unit": "rows/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms, 5),
+        "ms_per_step": round(r["ms"], 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": dtype,
+        "dtype": r["dtype"],
         "data": "synthetic: seeded splitmix64 logits (Box-Muller normals + peaks), Zipf(1.1) 4096-token count histories, "
                 "log-uniform grammar masks; resident in HBM before timing",
-        "config": {"workload": workload, "name": wl, "rows": rows, "vocab": vocab, "kernel": kernel},
-        "hbm_gbps": round(achieved, 1),
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(wl),
-                     "bytes_per_launch": nbytes, "timing": "HIP events around the timed launches on their stream"},
-        "cpu_baseline": cpu,
+        "config": {"workload": r["workload"], "name": r["name"], "rows": r["rows"], "vocab": r["vocab"], "kernel": r["kernel"]},
+        "hbm_gbps": round(r["achieved"], 1),
+        "roofline": {"bound": "hbm", "achieved": round(r["achieved"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(r["achieved"] / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(r["name"]),
+                     "bytes_per_launch": r["bytes"], "timing": "HIP events around the timed launches on their stream"},
+        "cpu_baseline": r["cpu"],
     }
+    if per_config is not None:
+        line["per_config"] = per_config
     print(json.dumps(line), flush=True)
 
 

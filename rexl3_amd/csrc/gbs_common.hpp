@@ -22,9 +22,6 @@ typedef uint16_t u16;
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-#ifndef GBS_EXP_STATS
-#define GBS_EXP_STATS 0
-#endif
 namespace gbs {
 
 constexpr int WAVE = 64;
@@ -306,9 +303,6 @@ struct WaveTop {
 
     float gate_f;  // the float whose order value is `gate`: for a non-NaN v, okey(v) >= gate <=> v >= gate_f
 
-#if GBS_EXP_STATS
-    int merges = 0;
-#endif
     static constexpr int INSERT_MAX = 6;  // survivors of a flush inserted one by one rather than sorted
     __device__ __forceinline__ void set_thr(u64 t) {
         thr = t;
@@ -448,9 +442,6 @@ struct WaveTop {
             n = base;
             u64 km = ballot(g > thr);
             if (km == 0ull) continue;
-#if GBS_EXP_STATS
-            ++merges;
-#endif
             if (__popcll(km) <= INSERT_MAX) {
                 do {
                     const int src = (int)__builtin_ctzll(km);

@@ -36,34 +36,6 @@ constexpr int LOAD_AUX = GBS_FAST_LOAD_AUX;  // cache-policy bits of the logits 
 #endif
 constexpr int MASK_AUX = GBS_FAST_MASK_AUX;  // cache-policy bits of the mask-word loads
 constexpr int NW = NT / WAVE;
-// GBS_EXP_*: measurement variants, all off in the product build. Each drops or instruments one stage, to measure
-// its cost with the loads kept live (NOPEN penalties, NOSEL selection, NOLSE log-sum-exp, NOFINISH / NOFINISH2 the
-// block merge and row finish, BARE everything but the loads, TIMES per-row wall-clock stamps, STATS gate and merge
-// counts, ORACLE_GATE a gate seeded from the row's true threshold).
-#ifndef GBS_EXP_NOPEN
-#define GBS_EXP_NOPEN 0
-#endif
-#ifndef GBS_EXP_NOSEL
-#define GBS_EXP_NOSEL 0
-#endif
-#ifndef GBS_EXP_NOFINISH
-#define GBS_EXP_NOFINISH 0
-#endif
-#ifndef GBS_EXP_NOLSE
-#define GBS_EXP_NOLSE 0
-#endif
-#ifndef GBS_EXP_TIMES
-#define GBS_EXP_TIMES 0
-#endif
-#ifndef GBS_EXP_NOFINISH2
-#define GBS_EXP_NOFINISH2 0
-#endif
-#ifndef GBS_EXP_BARE
-#define GBS_EXP_BARE 0
-#endif
-#ifndef GBS_EXP_ORACLE_GATE
-#define GBS_EXP_ORACLE_GATE 0
-#endif
 #ifndef GBS_FAST_LATE_B
 #define GBS_FAST_LATE_B 1  // the second buffer's first load: 0 at the start, 1 once the first's data has arrived, 2 after the seeding barrier
 #endif
@@ -307,11 +279,6 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
     __shared__ u32 s_top[NW * WaveTop<BUF>::TOPN];
     const int S = gridDim.x, sp = blockIdx.x, r = blockIdx.y;
     const int tid = threadIdx.x, w = tid / WAVE, l = lane_id();
-#if GBS_EXP_TIMES
-    const u64 t_start = wall_clock64();
-    u64 t_stream = 0;
-    __shared__ u64 s_tseed;
-#endif
     const size_t esz = DT == GBS_DTYPE_F32 ? 4 : 2;
     const void* row = (const char*)logits + (size_t)r * (size_t)stride * esz;
     const int* crow = COUNTS ? counts + (size_t)r * vocab : nullptr;
@@ -354,7 +321,7 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
     // c > 0: (x > 0 ? x * rinv : x * rep) - ((float)c * freq + pres); otherwise x.
     auto penalized = [&](float x, int c) {
         float v = x;
-        if (COUNTS && !GBS_EXP_NOPEN) {
+        if (COUNTS) {
             const float a = x * (x > 0.0f ? rinv : rep);
             const float b = (float)c * freq + pres;
             v = c > 0 ? a - b : x;
@@ -362,9 +329,6 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
         return v;
     };
     u32 nanv = 0;  // per lane: a NaN was seen
-#if GBS_EXP_STATS
-    int st_any = 0;
-#endif
     const float lse_c = clp;
     // one 4-element group: penalties, mask, NaN flag, keys offered to the wave list, online log-sum-exp.
     // The mask is applied with a bitfield insert: bfe_i32 of the element's bit is all ones or all zeros.
@@ -377,11 +341,9 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
             lv[q] = __uint_as_float((__float_as_uint(v) & keep) | (0xFF800000u & ~keep));
         }
         nanv |= (__builtin_isunordered(lv[0], lv[1]) | __builtin_isunordered(lv[2], lv[3])) ? 1u : 0u;
-        if (!GBS_EXP_NOSEL) {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) wt.offer_f(lv[q], (u32)(eg + q));
-        }
-        if (LOGPROB && !GBS_EXP_NOLSE) {
+        for (int q = 0; q < 4; ++q) wt.offer_f(lv[q], (u32)(eg + q));
+        if (LOGPROB) {
             const float gm = fmaxf(fmaxf(lv[0], lv[1]), fmaxf(lv[2], lv[3]));
             if (gm > lse.m) {
                 lse.s = lse.m == -INFINITY ? 0.f : lse.s * __builtin_amdgcn_exp2f((lse.m - gm) * lse_c);
@@ -410,18 +372,13 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
                 const int eg = e + j * GS;
                 float x[4];
                 unpack_x<DT>(B, j, x);
-#if GBS_EXP_BARE
-                for (int q = 0; q < 4; ++q)
-                    lv[jj * 4 + q] = __uint_as_float(__float_as_uint(x[q]) ^ (COUNTS ? (u32)B.c[j][q] : 0u) ^ (MASK ? B.m[j] : 0u));
-                continue;
-#endif
                 u32 mb = MASK ? (B.m[j] >> (eg & 31)) : 0xFu;
                 if (guard && eg >= hi) mb = 0u;
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     const u32 keep = (MASK || guard) ? (u32)__builtin_amdgcn_sbfe((int)mb, q, 1) : 0xFFFFFFFFu;
                     float v = x[q];
-                    if (COUNTS && !GBS_EXP_NOPEN) {
+                    if (COUNTS) {
                         const int c = (int)B.c[j][q];
                         if (ballot(c > 0 && keep != 0u)) v = penalized(x[q], c);
                     }
@@ -431,10 +388,6 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
         };
         // NaN flag, gate test and offers, online log-sum-exp of one half (element i of lane group jj: id e + jj*GS + q)
         auto rank_fn = [&](const float (&lv)[NE], int e) __attribute__((always_inline)) {
-#if GBS_EXP_BARE
-            for (int i = 0; i < NE; ++i) nanv ^= __float_as_uint(lv[i]);
-            return;
-#endif
             bool nan_step = false;
 #pragma unroll
             for (int i = 0; i < NE; i += 2) nan_step |= __builtin_isunordered(lv[i], lv[i + 1]);
@@ -449,10 +402,7 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
             for (int jj = 1; jj < HALF; ++jj) gm = fmaxf(gm, gmax[jj]);
             // the gate in two levels: the half's maximum, then each group's; only a group with a candidate tests its
             // elements (a lane whose values are all NaN also tests its elements, which never pass)
-            if (!GBS_EXP_NOSEL && ballot(!(gm < wt.gate_f))) {
-#if GBS_EXP_STATS
-                ++st_any;
-#endif
+            if (ballot(!(gm < wt.gate_f))) {
 #pragma unroll
                 for (int jj = 0; jj < HALF; ++jj) {
                     if (ballot(!(gmax[jj] < wt.gate_f))) {
@@ -462,7 +412,7 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
                     }
                 }
             }
-            if (LOGPROB && !GBS_EXP_NOLSE) {
+            if (LOGPROB) {
                 if (gm > lse.m) {
                     lse.s = lse.m == -INFINITY ? 0.f : lse.s * __builtin_amdgcn_exp2f((lse.m - gm) * lse_c);
                     lse.m = gm;
@@ -500,16 +450,7 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
                 wt.seed(m);
                 __syncthreads();
                 late_b(2);
-#if GBS_EXP_TIMES
-                if (tid == 0) s_tseed = wall_clock64();
-#endif
                 wt.block_bound();
-#if GBS_EXP_ORACLE_GATE
-                if (p.reserved != 0) {
-                    const u64 t = ((u64)(u32)p.reserved << 32) - 1ull;
-                    if (t > wt.thr) wt.set_thr(t);
-                }
-#endif
             }
             reload();
             rank_fn(lv, e);
@@ -571,43 +512,17 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
     wt.apply_shared();
     wt.flush(true);
 
-#if GBS_EXP_TIMES
-    t_stream = wall_clock64();
-    __shared__ u64 s_tw[NW];
-    if (l == 0) s_tw[w] = t_stream;
-#endif
-#if GBS_EXP_STATS
-    if (l == 0) {
-        atomicAdd(out_greedy + r, st_any);
-        atomicAdd(out_status + r, wt.merges);
-    }
-#endif
-    if (GBS_EXP_NOFINISH) {
-        if (l == 0) out_ids[r] = (int)(wt.list >> 40) + (int)nanv;
-        if (l == 0 && out_probs) out_probs[r] = lse.s;
-        return;
-    }
     // block reduction: lists, LSE, NaN
     if (LOGPROB) lse = wave_lse(lse, clp);
     const bool wnan = ballot(nanv != 0u) != 0ull;
     Lse rl{-INFINITY, 0.f};
     unsigned rn = 0;
     u64 list;
-#if GBS_EXP_TIMES
-    u64 t_bar = 0, t_merge = 0;
-#endif
     if (l == 0) {
         s_lse[w] = lse;
         s_nan[w] = wnan ? 1u : 0u;
     }
-#if GBS_EXP_TIMES
-    __syncthreads();
-    t_bar = wall_clock64();
-#endif
     wt.list = block_tree_merge<NW>(wt.list, s_list);  // also orders s_lse / s_nan before the reads below
-#if GBS_EXP_TIMES
-    t_merge = wall_clock64();
-#endif
     if (S == 1) {
         if (w != 0) return;
         if (l < NW) {
@@ -643,10 +558,6 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
     }
     if (LOGPROB) rl = wave_lse(rl, clp);  // lanes without a partial hold (-inf, 0)
     rn = wave_or(rn);
-#if GBS_EXP_NOFINISH2
-    if (l == 0) out_ids[r] = (int)(list >> 40) + (int)rn + (int)rl.s;
-    return;
-#endif
     const RowOut o = finish_row(list, p, u, invalid, rn != 0u, count, rl, clp);
     if (l == 0) {
         out_ids[r] = o.id;
@@ -654,16 +565,6 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
         if (out_probs) out_probs[r] = o.prob;
         if (out_logprobs) out_logprobs[r] = o.status == GBS_ROW_OK ? o.logprob : __uint_as_float(0x7fc00000u);
         if (out_status) out_status[r] = o.status;
-#if GBS_EXP_TIMES
-        const u64 t_end = wall_clock64();
-        u64 mn = ~0ull, mx = 0;
-        for (int o = 0; o < NW; ++o) { mn = s_tw[o] < mn ? s_tw[o] : mn; mx = s_tw[o] > mx ? s_tw[o] : mx; }
-        out_greedy[r] = (int)(t_start & 0x7fffffffu);
-        out_ids[r] = (int)(mn - t_start) | ((int)(s_tseed - t_start) << 16);
-        out_probs[r] = (float)(mx - t_start);
-        out_logprobs[r] = (float)(t_end - t_start);
-        out_status[r] = (int)(t_bar - t_start) | ((int)(t_merge - t_start) << 16);
-#endif
     }
 }
 
