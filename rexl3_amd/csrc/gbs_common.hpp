@@ -377,6 +377,7 @@ struct WaveTop {
         s_top = nullptr;
         top_w = 0;
         top_n = 0;
+        pend_l = 0;
     }
 
     __device__ __forceinline__ void publish() {
