@@ -125,9 +125,14 @@ def measure(wl, args, steps, cpu_seconds, dev, lib, stream):
     threads, ncores = host_threads()
     cores_note = f"{threads} threads of the {ncores} cores this process may use (capped at 16, one GPU's CPU share)"
     cpu = None
-    if wl in ("northstar", "c1", "c2", "c3", "c4"):
-        cfg = {"northstar": W.northstar, "c1": W.config1, "c2": W.config2, "c3": W.config3, "c4": W.config4}[wl]()
+    if wl in ("northstar", "c1", "c2", "c3", "c4", "mixed"):
+        cfg = {"northstar": W.northstar, "c1": W.config1, "c2": W.config2, "c3": W.config3, "c4": W.config4,
+               "mixed": W.northstar}[wl]()
         kmax = 0 if wl == "c3" else 64
+        if wl == "mixed":
+            # an engine's decode round: every tenth row samples top-p over the whole vocabulary (top_k 0)
+            cfg["params"]["top_k"][::10] = 0
+            kmax = -1  # GBS_KMAX_MIXED
         x = cfg["logits"]
         rows, vocab = x.shape
         is_bf16 = cfg["dtype"] == "bf16"
@@ -162,13 +167,17 @@ def measure(wl, args, steps, cpu_seconds, dev, lib, stream):
         ms = time_launches(launch, steps, args.warmup)
         # the full path (kmax 0) runs split over fs_* launches when there are fewer rows than CUs
         kernel = ("fs_pass0_k + fs_hist_k + fs_collect_k" if rows < 256 else "sample_full_k") if kmax == 0 else "sample_fast_k"
+        if kmax < 0:
+            kernel = "sample_fast_k + fs_pass0_k + fs_hist_k + fs_collect_k over the rows it leaves over"
         dtype = "bf16->f32" if is_bf16 else "f32"
         workload = {"northstar": "extended pipeline: penalties (dense i32 counts) + u32 grammar mask + T 0.8 + top-k 50 / top-p 0.9"
                                  " + log-softmax + inverse-CDF draw",
                     "c1": "config 1: single row, T 0.7, top-k 50, top-p 0.9",
                     "c2": "config 2: bf16 batched, per-row T, top-k 40, top-p 0.95, min-p 0.05",
                     "c3": "config 3: penalties over dense counts, T 0.8, top-p 0.9 over the whole vocabulary (no top-k)",
-                    "c4": "config 4: grammar mask, top-k 64, top-p 0.95"}[wl]
+                    "c4": "config 4: grammar mask, top-k 64, top-p 0.95",
+                    "mixed": "north-star batch with every tenth row at top_k 0 (top-p over the whole vocabulary), per-row "
+                             "dispatch (GBS_KMAX_MIXED)"}[wl]
         st = out["status"].cpu().numpy()
         assert (st[cfg["params"]["temperature"] >= 0] >= 0).all()
         if not args.no_cpu:
@@ -346,7 +355,7 @@ def main():
     per_config = None
     if args.workload == "northstar" and not args.no_per_config:
         per_config = {}
-        for wl in ("c1", "c2", "c3", "c4", "c5", "keyed"):
+        for wl in ("c1", "c2", "c3", "c4", "c5", "keyed", "mixed"):
             print(f"# per-config {wl}", file=sys.stderr, flush=True)
             q = measure(wl, args, args.per_config_steps, args.per_config_cpu_seconds, dev, lib, stream)
             per_config[wl] = {"workload": q["workload"], "kernel": q["kernel"], "rows": q["rows"], "vocab": q["vocab"],

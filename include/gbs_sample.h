@@ -50,6 +50,8 @@ extern "C" {
 #define GBS_MAX_VOCAB 524288
 /* Candidates per row of the exact top-count kernels (crates/cuda/csrc/glue.cu:1088). */
 #define GBS_MAX_COUNT 64
+/* gbs_sample_rows's `kmax` for a batch that mixes rows of any top_k (per-row dispatch). */
+#define GBS_KMAX_MIXED (-1)
 
 /*
  * The keyed sampling record of one row, 48 bytes, field for field the `KeyedRow` of crates/cuda/csrc/glm_mtp.cu:258-264:
@@ -243,11 +245,17 @@ int gbs_tree_verify(const void* logits, int dtype, int n_tree, int nodes, int st
                     void* ws, size_t ws_bytes, void* stream);
 
 /*
- * Extended sampling pipeline. logits [rows, stride] (dtype f32 or bf16, bf16 widened exactly), columns [0, vocab);
+ * Extended sampling pipeline. logits [rows, stride] (dtype f32, bf16 or f16; 16-bit values widened exactly), columns
+ * [0, vocab);
  * counts i32 [rows, vocab] (NULL = all zero); mask u32 [rows, ceil(vocab/32)] (bit i%32 of word i/32 set = token
  * allowed; NULL = all allowed); params GbsRowParams[rows]; uniforms f32 [rows], each in [0, 1).
  * `kmax` in [1, 64] promises top_k in [1, kmax] on every row and selects the single-pass kernel (a row that breaks the
  * promise gets GBS_ROW_INVALID_PARAMS); kmax == 0 selects the multi-pass full-distribution path (any top_k, 0 = off).
+ * kmax == GBS_KMAX_MIXED dispatches per row, for a batch that mixes them (as REXL3's engine sends its decode rounds,
+ * crates/engine/src/lib.rs:2089-2117): every row takes the single-pass kernel, which finishes rows with top_k in
+ * [1, 64] and, from its best 64 candidates and the row's log-sum-exp, the rows with top_k 0 or above 64 whose top-p /
+ * min-p cut provably lies among those candidates; the other rows are finished by the full-distribution path in a
+ * second launch. Results are the same as with kmax 0.
  * Outputs (any but out_ids may be NULL): out_ids i32 [rows] (-1 on error), out_greedy i32 [rows] (argmax, ties to the
  * lowest id), out_probs f32 [rows] (probability of the chosen token in the final kept distribution),
  * out_logprobs f32 [rows] (log-softmax of the chosen token over every allowed token at temperature T, or 1 when T == 0),

@@ -1,6 +1,7 @@
 // Exact integer arithmetic of the extended pipeline, device side. The definitions (the per-element penalty, the mass
 // of a token, the exact products with an f32 fraction) are the pipeline's specification; each helper states it.
 #pragma once
+#include <hip/hip_fp16.h>
 #include "gbs_common.hpp"
 
 namespace gbs {
@@ -151,6 +152,25 @@ __device__ __forceinline__ u64 mul_ceil64(float x, u64 z) {
 }
 
 // (max, sum of 2^((l - max) * c)) pairs: the online log-sum-exp, base 2
+// The two 16-bit logits of a 32-bit word (low half first), widened exactly to f32: bf16 by a shift, fp16 by the
+// conversion instruction (every fp16 value, NaN and infinities included, is an f32 value).
+template <int DT>
+__device__ __forceinline__ void widen2(u32 w, float& a, float& b) {
+    if constexpr (DT == GBS_DTYPE_BF16) {
+        a = __uint_as_float(w << 16);
+        b = __uint_as_float(w & 0xFFFF0000u);
+    } else {
+        a = __half2float(__ushort_as_half((unsigned short)(w & 0xFFFFu)));
+        b = __half2float(__ushort_as_half((unsigned short)(w >> 16)));
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ float widen1(u32 h) {
+    if constexpr (DT == GBS_DTYPE_BF16) return __uint_as_float(h << 16);
+    else return __half2float(__ushort_as_half((unsigned short)h));
+}
+
 struct Lse {
     float m, s;
 };

@@ -72,19 +72,19 @@ int fast_splits(int rows, int vocab) {
     return s;
 }
 
-// Workspace. Its first CTL_BYTES hold the per-row arrival counters, which must be zero between launches, at offsets that
-// depend only on the row (room for 65535 rows whatever this launch's row count); every launch leaves them zero. The
-// partial results after them are written before they are read. So a workspace cleared once serves launches of any
-// shape.
-// The full-distribution path (kmax 0) keeps three counters per row in the same region (three quarters of it), so one
-// workspace also serves launches that alternate between the two paths.
-constexpr size_t CTL_BYTES = (size_t)3 * 65536 * 4;
+// Workspace. Its first CTL_BYTES are the control region (pipeline_full.hpp): per-row arrival counters, which must be
+// zero between launches, at offsets that depend only on the row (room for 65535 rows whatever this launch's row count);
+// every launch leaves them zero. The full-distribution path keeps its counters in the same region, and per-row dispatch
+// its flags, so one workspace serves launches of any shape on either path. The partial results after the region are
+// written before they are read.
+constexpr size_t CTL_BYTES = SAMPLE_CTL_BYTES;
 
 struct FastWs {
     unsigned* arrive;  // [rows] the row's blocks that have handed over their partials
     u64* lists;     // [rows][S][64]
     Lse* lse;       // [rows][S]
     unsigned* nan;  // [rows][S]
+    unsigned* defer;  // [rows] per-row dispatch: 1 for a row left to the full path (null without per-row dispatch)
 };
 
 size_t fast_part_bytes(int rows, int S) {
@@ -100,6 +100,7 @@ FastWs fast_ws(void* ws, int rows, int S) {
     w.lse = (Lse*)p;
     p += align256((size_t)rows * S * sizeof(Lse));
     w.nan = (unsigned*)p;
+    w.defer = nullptr;
     return w;
 }
 
@@ -144,15 +145,15 @@ __device__ __forceinline__ void unpack_x(const RawStep<DT>& r, int j, float (&x)
         x[0] = __uint_as_float(v.x); x[1] = __uint_as_float(v.y); x[2] = __uint_as_float(v.z); x[3] = __uint_as_float(v.w);
     } else {
         const u32x2 v = r.x[j];
-        x[0] = __uint_as_float(v.x << 16); x[1] = __uint_as_float(v.x & 0xFFFF0000u);
-        x[2] = __uint_as_float(v.y << 16); x[3] = __uint_as_float(v.y & 0xFFFF0000u);
+        widen2<DT>(v.x, x[0], x[1]);
+        widen2<DT>(v.y, x[2], x[3]);
     }
 }
 
 template <int DT>
 __device__ __forceinline__ float load_x1(const void* row, int e) {
-    if (DT == GBS_DTYPE_F32) return ((const float*)row)[e];
-    return __uint_as_float((u32)((const u16*)row)[e] << 16);
+    if constexpr (DT == GBS_DTYPE_F32) return ((const float*)row)[e];
+    else return widen1<DT>((u32)((const u16*)row)[e]);
 }
 
 // The row's finish, on one wave. `list` holds the row's best 64 keys (lane = rank).
@@ -161,9 +162,36 @@ struct RowOut {
     float prob, logprob;
 };
 
+constexpr int ROW_DEFERRED = -1;  // internal status: the row's cut is not provably inside the list (full path)
+
+// Relative bound on |Z - Zf| / Z, where Z is a row's exact integer mass total and Zf = lse.s * 2^44 its value from the
+// f32 online log-sum-exp over the same values at the same maximum: the exponents agree to |y| * 2^-23 (|y| < 64), the
+// masses are 2^(44 + y) to within 2^-21, and the per-lane sums of at most 2^11 terms and their merges add at most
+// 2^-12; 2^-10 leaves a margin of four.
+constexpr double LSE_MASS_BOUND = 1.0 / 1024.0;
+
 constexpr int SMALL_KEPT = 16;  // kept sets up to this size skip the sort by id
 
-__device__ RowOut finish_row(u64 list, const RowParamsDev& p, float u, bool invalid, bool nan, int count, Lse lse, float clp) {
+// An upper bound of the top-k set's exact mass for a row whose list (zk: its mass, e_last: its last mass) is full: from
+// the log-sum-exp (top_k 0, and any top_k), and from the list for top_k above 64. 0 when no bound is known (the
+// log-sum-exp is not at the maximum, or the maximum or 1/T is not finite).
+__device__ __forceinline__ double kn_total_bound(const RowParamsDev& p, Lse lse, float M, float clp, u64 zk, u64 e_last) {
+    double hi = 0.0;
+    const bool lse_ok = lse.m == M && __builtin_isfinite(M) && __builtin_isfinite(clp) && lse.s > 0.0f && __builtin_isfinite(lse.s);
+    if (lse_ok) hi = ceil(ldexp((double)lse.s, 44) * (1.0 + LSE_MASS_BOUND));
+    if (p.top_k > WAVE) {
+        const double k_hi = (double)zk + (double)(p.top_k - WAVE) * (double)e_last;
+        hi = (hi == 0.0 || k_hi < hi) ? k_hi : hi;
+    }
+    // every mass is at most 2^44 and rows hold at most 2^19 tokens: the bound stays below 2^63
+    const double cap = ldexp(1.0, 63) - 1.0;
+    return hi > cap ? cap : hi;
+}
+
+// `open`: per-row dispatch's row without a top-k the list can hold (top_k 0 or above 64): its list holds the row's best
+// 64 keys, and the row is finished here only when its cut provably lies inside them, else the status is ROW_DEFERRED.
+__device__ RowOut finish_row(u64 list, const RowParamsDev& p, float u, bool invalid, bool nan, int count, Lse lse, float clp,
+                             bool open = false) {
     RowOut o{-1, -1, GBS_ROW_OK, 0.f, __uint_as_float(0x7fc00000u)};
     const int l = lane_id();
     if (invalid) {
@@ -193,14 +221,43 @@ __device__ RowOut finish_row(u64 list, const RowParamsDev& p, float u, bool inva
         const u64 E = valid ? (mass_fast_ok(M, c2) ? mass_fast(lval, M, c2) : mass(lval, M, c2)) : 0ull;
         const u64 C = wave_scan_u64(E);
         const u64 zk = readlane64(C, WAVE - 1);
+        const bool topp = p.top_p > 0.0f && p.top_p < 1.0f;
+        // min-p filters the top-p prefix (the first token, of mass 2^44 >= Q, always stays)
+        const u64 Q = p.min_p > 0.0f ? mul_ceil64(p.min_p, MASS_ONE) : 0ull;
         int keep = kn;
-        if (p.top_p > 0.0f && p.top_p < 1.0f) {
+        if (open && kn == WAVE) {
+            // The list is full, so the row has tokens beyond it. The top-k set's mass Z_K is bounded: at least the
+            // list's; at most, for top_k above 64, the list's plus (top_k - 64) times its last mass; for top_k 0 it is
+            // the row's total, which the log-sum-exp gives to within LSE_MASS_BOUND. The top-p cut is exact when both
+            // ends of the bound put it at the same place inside the list; without top-p, min-p must drop the last entry.
+            const u64 e_last = readlane64(E, WAVE - 1);
+            const u64 zmax = (u64)kn_total_bound(p, lse, M, clp, zk, e_last);
+            u64 zlo = zk, zhi = zmax;
+            if (p.top_k == 0 && zhi != 0ull) {
+                const double zf = ldexp((double)lse.s, 44);
+                const u64 lo = (u64)(zf * (1.0 - LSE_MASS_BOUND));
+                zlo = lo > zlo ? lo : zlo;
+            }
+            bool ok = false;
+            if (topp) {
+                if (zhi != 0ull && zlo <= zhi) {
+                    const int blo = __popcll(ballot(valid && C < mul_ceil64(p.top_p, zlo)));
+                    const int bhi = __popcll(ballot(valid && C < mul_ceil64(p.top_p, zhi)));
+                    ok = blo == bhi && bhi < WAVE;
+                    keep = blo + 1;
+                }
+            } else {
+                ok = Q > 0ull && e_last < Q;
+            }
+            if (!ok) {
+                o.status = ROW_DEFERRED;
+                return o;
+            }
+        } else if (topp) {
             const u64 P = mul_ceil64(p.top_p, zk);
             const int below = __popcll(ballot(valid && C < P));
             keep = below + 1 < kn ? below + 1 : kn;
         }
-        // min-p filters the top-p prefix (the first token, of mass 2^44 >= Q, always stays)
-        const u64 Q = p.min_p > 0.0f ? mul_ceil64(p.min_p, MASS_ONE) : 0ull;
         const bool kept = l < keep && E >= Q;
         const u64 km = ballot(kept);
         const u64 z = wave_sum_u64(kept ? E : 0ull);
@@ -306,8 +363,11 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
     __syncthreads();
     const RowParamsDev p = params[r];
     const float u = uniforms[r];
-    const bool invalid = params_invalid(p, u) || p.top_k < 1 || p.top_k > kmax;
-    const int count = invalid ? 1 : p.top_k;
+    // kmax < 0: per-row dispatch; a row with top_k 0 or above 64 is `open` (its list keeps 64 keys)
+    const bool mixed = kmax < 0;
+    const bool open = mixed && (p.top_k == 0 || p.top_k > WAVE);
+    const bool invalid = params_invalid(p, u) || (!mixed && (p.top_k < 1 || p.top_k > kmax));
+    const int count = invalid ? 1 : (open ? WAVE : p.top_k);
     const float rinv = 1.0f / p.repetition;
     const float rep = p.repetition, freq = p.frequency, pres = p.presence;  // plain scalars for the element loop
     const float clp = p.temperature > 0.0f ? temp_scale(p.temperature) : 1.44269504088896340736f;
@@ -558,13 +618,10 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
     }
     if (LOGPROB) rl = wave_lse(rl, clp);  // lanes without a partial hold (-inf, 0)
     rn = wave_or(rn);
-    const RowOut o = finish_row(list, p, u, invalid, rn != 0u, count, rl, clp);
+    const RowOut o = finish_row(list, p, u, invalid, rn != 0u, count, rl, clp, open);
     if (l == 0) {
-        out_ids[r] = o.id;
-        if (out_greedy) out_greedy[r] = o.greedy;
-        if (out_probs) out_probs[r] = o.prob;
-        if (out_logprobs) out_logprobs[r] = o.status == GBS_ROW_OK ? o.logprob : __uint_as_float(0x7fc00000u);
-        if (out_status) out_status[r] = o.status;
+        if (ws.defer) ws.defer[r] = o.status == ROW_DEFERRED ? 1u : 0u;
+        if (o.status != ROW_DEFERRED) write_row(r, o, out_ids, out_greedy, out_probs, out_logprobs, out_status);
     }
 }
 
@@ -584,16 +641,21 @@ void dispatch_flags(bool c, bool m, bool lp, F&& f) {
 }  // namespace
 
 GBS_EXPORT size_t gbs_sample_workspace_bytes(int rows, int vocab, int kmax) {
-    if (rows <= 0 || vocab <= 0 || vocab > GBS_MAX_VOCAB || kmax < 0 || kmax > GBS_MAX_COUNT) return 0;
+    if (rows <= 0 || vocab <= 0 || vocab > GBS_MAX_VOCAB || kmax < GBS_KMAX_MIXED || kmax > GBS_MAX_COUNT) return 0;
     if (kmax == 0) return sample_full_workspace_bytes(rows, vocab);
-    return CTL_BYTES + fast_part_bytes(rows, fast_splits(rows, vocab));
+    const size_t fast = CTL_BYTES + fast_part_bytes(rows, fast_splits(rows, vocab));
+    if (kmax > 0) return fast;
+    // per-row dispatch: the single-pass kernel's workspace, then the full path's for the rows it leaves over
+    const size_t full = sample_full_deferred_workspace_bytes(rows, vocab);
+    return fast > full ? fast : full;
 }
 
 GBS_EXPORT int gbs_sample_rows(const void* logits, int dtype, int rows, int stride, int vocab, const int32_t* counts, const uint32_t* mask,
                                const GbsRowParams* params, const float* uniforms, int kmax, int* out_ids, int* out_greedy,
                                float* out_probs, float* out_logprobs, int* out_status, void* ws, size_t ws_bytes, void* stream) {
-    if (rows < 0 || vocab <= 0 || vocab > GBS_MAX_VOCAB || stride < vocab || kmax < 0 || kmax > GBS_MAX_COUNT) return GBS_ERR_INVALID;
-    if (dtype != GBS_DTYPE_F32 && dtype != GBS_DTYPE_BF16) return GBS_ERR_INVALID;
+    if (rows < 0 || vocab <= 0 || vocab > GBS_MAX_VOCAB || stride < vocab || kmax < GBS_KMAX_MIXED || kmax > GBS_MAX_COUNT)
+        return GBS_ERR_INVALID;
+    if (dtype != GBS_DTYPE_F32 && dtype != GBS_DTYPE_BF16 && dtype != GBS_DTYPE_F16) return GBS_ERR_INVALID;
     if (rows == 0) return 0;
     if (rows > 65535 || !logits || !params || !uniforms || !out_ids) return GBS_ERR_INVALID;
     if (kmax == 0) {
@@ -610,16 +672,25 @@ GBS_EXPORT int gbs_sample_rows(const void* logits, int dtype, int rows, int stri
     const bool vec = stride % 4 == 0 && vocab % 4 == 0 && aligned(logits, 4 * esz) && (!counts || aligned(counts, 16));
     const hipStream_t st = to_stream(stream);
     const RowParamsDev* p = (const RowParamsDev*)params;
-    const FastWs w = fast_ws(ws, rows, S);
+    const bool mixed = kmax == GBS_KMAX_MIXED;
+    FastWs w = fast_ws(ws, rows, S);
+    if (mixed) w.defer = (unsigned*)((char*)ws + SAMPLE_DEFER_OFFSET);
     auto run = [&]<int DT>() {
-        dispatch_flags(counts != nullptr, mask != nullptr, out_logprobs != nullptr, [&]<bool C, bool M, bool L>() {
+        // per-row dispatch bounds open rows by the log-sum-exp: it is computed whether or not log-probabilities are asked
+        dispatch_flags(counts != nullptr, mask != nullptr, mixed || out_logprobs != nullptr, [&]<bool C, bool M, bool L>() {
             hipLaunchKernelGGL((sample_fast_k<DT, C, M, L>), dim3(S, rows), dim3(NT), 0, st, logits, (long long)stride, vocab, chunk,
                                counts, mask, p, uniforms, kmax, vec, w, out_ids, out_greedy, out_probs, out_logprobs, out_status);
         });
     };
     if (dtype == GBS_DTYPE_F32) run.template operator()<GBS_DTYPE_F32>();
-    else run.template operator()<GBS_DTYPE_BF16>();
-    return launch_status();
+    else if (dtype == GBS_DTYPE_BF16) run.template operator()<GBS_DTYPE_BF16>();
+    else run.template operator()<GBS_DTYPE_F16>();
+    if (!mixed) return launch_status();
+    const int rc = launch_status();
+    if (rc != 0) return rc;
+    // the rows the single pass left over (their flags set): the full-distribution path
+    return launch_sample_full(logits, dtype, rows, stride, vocab, counts, mask, params, uniforms, out_ids, out_greedy, out_probs,
+                              out_logprobs, out_status, ws, ws_bytes, stream, w.defer);
 }
 
 // ------------------------------------------------------------------------------------------------ allocation-free form
@@ -665,8 +736,9 @@ void* device_scratch(void* stream, int* rc) {
 GBS_EXPORT int gbs_sample_rows_noalloc(const void* logits, int dtype, int rows, int stride, int vocab, const int32_t* counts,
                                        const uint32_t* mask, const GbsRowParams* params, const float* uniforms, int kmax, int* out_ids,
                                        int* out_greedy, float* out_probs, float* out_logprobs, int* out_status, void* stream) {
-    if (rows < 0 || vocab <= 0 || vocab > GBS_MAX_VOCAB || stride < vocab || kmax < 0 || kmax > GBS_MAX_COUNT) return GBS_ERR_INVALID;
-    if (dtype != GBS_DTYPE_F32 && dtype != GBS_DTYPE_BF16) return GBS_ERR_INVALID;
+    if (rows < 0 || vocab <= 0 || vocab > GBS_MAX_VOCAB || stride < vocab || kmax < GBS_KMAX_MIXED || kmax > GBS_MAX_COUNT)
+        return GBS_ERR_INVALID;
+    if (dtype != GBS_DTYPE_F32 && dtype != GBS_DTYPE_BF16 && dtype != GBS_DTYPE_F16) return GBS_ERR_INVALID;
     if (rows == 0) return 0;
     if (rows > 65535) return GBS_ERR_INVALID;
     if (gbs_sample_workspace_bytes(rows, vocab, kmax) > GBS_NOALLOC_SCRATCH_BYTES) return GBS_ERR_NOALLOC_TOO_LARGE;

@@ -66,8 +66,8 @@ struct Row {
         if (DT == GBS_DTYPE_F32) {
             xv[0] = __uint_as_float(w.x.x); xv[1] = __uint_as_float(w.x.y); xv[2] = __uint_as_float(w.x.z); xv[3] = __uint_as_float(w.x.w);
         } else {
-            xv[0] = __uint_as_float(w.x.x << 16); xv[1] = __uint_as_float(w.x.x & 0xFFFF0000u);
-            xv[2] = __uint_as_float(w.x.y << 16); xv[3] = __uint_as_float(w.x.y & 0xFFFF0000u);
+            widen2<DT>(w.x.x, xv[0], xv[1]);
+            widen2<DT>(w.x.y, xv[2], xv[3]);
         }
         const u32 mw = MASK ? w.m >> (e & 31) : 0xFu;
 #pragma unroll
@@ -87,8 +87,8 @@ struct Row {
                 xv[0] = v.x; xv[1] = v.y; xv[2] = v.z; xv[3] = v.w;
             } else {
                 const uint2 v = *(const uint2*)((const u16*)x + e);
-                xv[0] = __uint_as_float(v.x << 16); xv[1] = __uint_as_float(v.x & 0xFFFF0000u);
-                xv[2] = __uint_as_float(v.y << 16); xv[3] = __uint_as_float(v.y & 0xFFFF0000u);
+                widen2<DT>(v.x, xv[0], xv[1]);
+                widen2<DT>(v.y, xv[2], xv[3]);
             }
             if (COUNTS) {
                 const int4 cc = *(const int4*)(c + e);
@@ -98,7 +98,8 @@ struct Row {
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const bool in = e + q < vocab;
-                xv[q] = in ? (DT == GBS_DTYPE_F32 ? ((const float*)x)[e + q] : __uint_as_float((u32)((const u16*)x)[e + q] << 16)) : 0.f;
+                if constexpr (DT == GBS_DTYPE_F32) xv[q] = in ? ((const float*)x)[e + q] : 0.f;
+                else xv[q] = in ? widen1<DT>((u32)((const u16*)x)[e + q]) : 0.f;
                 if (COUNTS) cv[q] = in ? c[e + q] : 0;
             }
         }
@@ -649,8 +650,10 @@ __global__ void __launch_bounds__(NTF) sample_full_k(const void* __restrict__ lo
                                                      const int* __restrict__ counts, const u32* __restrict__ mask,
                                                      const RowParamsDev* __restrict__ params, const float* __restrict__ uniforms, bool vec,
                                                      int* __restrict__ out_ids, int* __restrict__ out_greedy, float* __restrict__ out_probs,
-                                                     float* __restrict__ out_logprobs, int* __restrict__ out_status) {
+                                                     float* __restrict__ out_logprobs, int* __restrict__ out_status,
+                                                     const unsigned* __restrict__ flags) {
     __shared__ Shared sh;
+    if (flags && flags[blockIdx.x] == 0u) return;
     full_row<DT, COUNTS, MASK>(logits, stride, vocab, counts, mask, params, uniforms, vec, out_ids, out_greedy, out_probs, out_logprobs,
                                out_status, (int)blockIdx.x, sh);
 }
@@ -688,7 +691,7 @@ struct FsWs {
     u64* tiles;                    // [rows][ntiles]
 };
 
-constexpr size_t FS_CTL = (size_t)3 * 65536 * 4;  // the same control region as the fast path's (pipeline.hip)
+constexpr size_t FS_CTL = SAMPLE_CTL_BYTES;  // the control region shared with the single-pass kernel
 
 size_t fs_align(size_t b) { return (b + 255) & ~(size_t)255; }
 
@@ -764,24 +767,62 @@ __device__ __forceinline__ float fs_clp(const RowParamsDev& p) {
     return p.temperature > 0.0f ? temp_scale(p.temperature) : 1.44269504088896340736f;
 }
 
+// Under per-row dispatch the split path runs over the rows the single-pass kernel flagged: its workspace holds DEFER_ROWS
+// of them (8 blocks each); a flagged row past those is taken whole by one block of fs_collect_k (full_row).
+constexpr int DEFER_ROWS = 32;
+
+// The row a block of the split path works on, and its place in the workspace. Without per-row dispatch (flags null)
+// both are blockIdx.y. Under it the grid is (S, DEFER_ROWS + 1): blockIdx.y = i < DEFER_ROWS is the i-th flagged row
+// (in row order), and the blocks of blockIdx.y = DEFER_ROWS share out the flagged rows past those (rank DEFER_ROWS +
+// blockIdx.x, + S, ...), each taken whole by fs_collect_k. Returns the row (-1: none) and sets *wr to the workspace
+// place. Every thread of the block calls it.
+__device__ int fs_row(const unsigned* __restrict__ flags, int rows, int rank, int* s_row) {
+    if (threadIdx.x == 0) *s_row = -1;
+    __syncthreads();
+    const int w = threadIdx.x / WAVE, l = lane_id();
+    __shared__ int s_wc[NWF];
+    int base = 0;  // flagged rows before this chunk
+    for (int c0 = 0; c0 < rows; c0 += NTF) {
+        const int i = c0 + (int)threadIdx.x;
+        const bool f = i < rows && flags[i] != 0u;
+        const u64 b = ballot(f);
+        if (l == 0) s_wc[w] = __popcll(b);
+        __syncthreads();
+        int before = base;
+        for (int o = 0; o < w; ++o) before += s_wc[o];
+        if (f && before + mbcnt(b) == rank) *s_row = i;
+        int tot = 0;
+        for (int o = 0; o < NWF; ++o) tot += s_wc[o];
+        __syncthreads();
+        base += tot;
+        if (base > rank) break;
+    }
+    __syncthreads();
+    return *s_row;
+}
+
 template <int DT, bool COUNTS, bool MASK>
 __global__ void __launch_bounds__(NTF) fs_pass0_k(const void* __restrict__ logits, long long stride, int vocab,
                                                   const int* __restrict__ counts, const u32* __restrict__ mask,
                                                   const RowParamsDev* __restrict__ params, const float* __restrict__ uniforms, bool vec,
                                                   int tpb, FsWs ws, int* __restrict__ out_ids, int* __restrict__ out_greedy,
                                                   float* __restrict__ out_probs, float* __restrict__ out_logprobs,
-                                                  int* __restrict__ out_status) {
+                                                  int* __restrict__ out_status, const unsigned* __restrict__ flags, int rows) {
     __shared__ u64 s_red[NWF];
     __shared__ float s_lm[NWF], s_ls[NWF];
     __shared__ unsigned s_flag;
-    const int S = gridDim.x, sp = blockIdx.x, r = blockIdx.y;
+    __shared__ int s_sel;
+    const int S = gridDim.x, sp = blockIdx.x, wr = blockIdx.y;  // wr: the row's place in the workspace
+    if (flags && wr >= DEFER_ROWS) return;  // flagged rows past the workspace's: fs_collect_k
+    const int r = flags ? fs_row(flags, rows, wr, &s_sel) : wr;
+    if (r < 0) return;
     const int tid = threadIdx.x, w = tid / WAVE, l = lane_id();
     const RowParamsDev p = params[r];
     const float u = uniforms[r];
     if (params_invalid(p, u)) {  // every block of the row returns; the first writes the row's results
         if (sp == 0 && tid == 0) {
             fs_out(r, -1, -1, GBS_ROW_INVALID_PARAMS, 0.f, 0.f, out_ids, out_greedy, out_probs, out_logprobs, out_status);
-            st_agent(&ws.rows[r].state, (u32)FS_DONE);
+            st_agent(&ws.rows[wr].state, (u32)FS_DONE);
         }
         return;
     }
@@ -804,7 +845,7 @@ __global__ void __launch_bounds__(NTF) fs_pass0_k(const void* __restrict__ logit
     if (tid == 0) {
         Lse b{-INFINITY, 0.f};
         for (int o = 0; o < NWF; ++o) b = lse_merge(b, Lse{s_lm[o], s_ls[o]}, clp);
-        FsPart0* pp = &ws.p0[(size_t)r * S + sp];
+        FsPart0* pp = &ws.p0[(size_t)wr * S + sp];
         st_agent(&pp->key, top);
         st_agent(&pp->nan, nan_any);
         st_agent(&pp->nallowed, (u32)nall);
@@ -816,7 +857,7 @@ __global__ void __launch_bounds__(NTF) fs_pass0_k(const void* __restrict__ logit
     u64 k = 0, na = 0, nn = 0;
     Lse rl{-INFINITY, 0.f};
     if (tid < S) {
-        const FsPart0* pp = &ws.p0[(size_t)r * S + tid];
+        const FsPart0* pp = &ws.p0[(size_t)wr * S + tid];
         k = ld_agent(&pp->key);
         nn = ld_agent(&pp->nan);
         na = ld_agent(&pp->nallowed);
@@ -824,7 +865,7 @@ __global__ void __launch_bounds__(NTF) fs_pass0_k(const void* __restrict__ logit
     }
     if (w == 0) {  // S <= 128: lanes hold two partials at most
         if (tid + WAVE < S) {
-            const FsPart0* pp = &ws.p0[(size_t)r * S + tid + WAVE];
+            const FsPart0* pp = &ws.p0[(size_t)wr * S + tid + WAVE];
             const u64 k2 = ld_agent(&pp->key);
             k = k2 > k ? k2 : k;
             nn += ld_agent(&pp->nan);
@@ -841,7 +882,7 @@ __global__ void __launch_bounds__(NTF) fs_pass0_k(const void* __restrict__ logit
         }
     }
     if (tid != 0) return;
-    FsRow* row = &ws.rows[r];
+    FsRow* row = &ws.rows[wr];
     u32 state = FS_CUT;
     const float M = okey_to_f32(key_ok(k));
     const int greedy = (int)key_id(k);
@@ -872,16 +913,21 @@ __global__ void __launch_bounds__(NTF) fs_pass0_k(const void* __restrict__ logit
 template <int DT, bool COUNTS, bool MASK>
 __global__ void __launch_bounds__(NTF) fs_hist_k(const void* __restrict__ logits, long long stride, int vocab,
                                                  const int* __restrict__ counts, const u32* __restrict__ mask,
-                                                 const RowParamsDev* __restrict__ params, bool vec, int tpb, FsWs ws) {
+                                                 const RowParamsDev* __restrict__ params, bool vec, int tpb, FsWs ws,
+                                                 const unsigned* __restrict__ flags, int rows) {
     __shared__ u64 s_hist[NBINS];
     __shared__ unsigned s_flag;
-    const int S = gridDim.x, sp = blockIdx.x, r = blockIdx.y;
+    __shared__ int s_sel;
+    const int S = gridDim.x, sp = blockIdx.x, wr = blockIdx.y;
+    if (flags && wr >= DEFER_ROWS) return;
+    const int r = flags ? fs_row(flags, rows, wr, &s_sel) : wr;
+    if (r < 0) return;
     const int tid = threadIdx.x, l = lane_id();
     const RowParamsDev p = params[r];
     if (!(p.top_p > 0.0f && p.top_p < 1.0f)) return;  // no top-p: no histogram
-    if (ld_agent(&ws.rows[r].state) != FS_CUT) return;
+    if (ld_agent(&ws.rows[wr].state) != FS_CUT) return;
     const Row<DT, COUNTS, MASK> R = make_row<DT, COUNTS, MASK>(logits, stride, vocab, counts, mask, p, vec, r);
-    const float M = okey_to_f32(key_ok(ld_agent(&ws.rows[r].top)));
+    const float M = okey_to_f32(key_ok(ld_agent(&ws.rows[wr].top)));
     const float c2 = temp_scale(p.temperature);
     const int ntiles = (vocab + TILE - 1) / TILE;
     const int t0 = sp * tpb, t1 = min(ntiles, t0 + tpb);
@@ -895,11 +941,11 @@ __global__ void __launch_bounds__(NTF) fs_hist_k(const void* __restrict__ logits
         }
     });
     __syncthreads();
-    u64* mine = ws.hist + ((size_t)r * S + sp) * NBINS;
+    u64* mine = ws.hist + ((size_t)wr * S + sp) * NBINS;
     for (int i = tid; i < NBINS; i += NTF) st_agent(&mine[i], s_hist[i]);
     if (!arrive_last(&ws.cnt1[r], (unsigned)S, &s_flag)) return;
     // the row's histogram: the blocks' histograms summed bin by bin
-    const u64* all = ws.hist + (size_t)r * S * NBINS;
+    const u64* all = ws.hist + (size_t)wr * S * NBINS;
     for (int i = tid; i < NBINS; i += NTF) {
         u64 v = 0;
         for (int o = 0; o < S; ++o) v += ld_agent(&all[(size_t)o * NBINS + i]);
@@ -924,7 +970,7 @@ __global__ void __launch_bounds__(NTF) fs_hist_k(const void* __restrict__ logits
                 if (acc + s_hist[b] >= Pv) break;
                 acc += s_hist[b];
             }
-            FsRow* row = &ws.rows[r];
+            FsRow* row = &ws.rows[wr];
             st_agent(&row->bstar, (u32)b);
             st_agent(&row->above, acc);
             st_agent(&row->P, Pv);
@@ -938,7 +984,7 @@ __global__ void __launch_bounds__(NTF) fs_collect_k(const void* __restrict__ log
                                                     const RowParamsDev* __restrict__ params, const float* __restrict__ uniforms,
                                                     bool vec, int tpb, FsWs ws, int* __restrict__ out_ids, int* __restrict__ out_greedy,
                                                     float* __restrict__ out_probs, float* __restrict__ out_logprobs,
-                                                    int* __restrict__ out_status) {
+                                                    int* __restrict__ out_status, const unsigned* __restrict__ flags, int rows) {
     // the collection's arrays live in the radix path's LDS record (the two never run at the same time)
     __shared__ Shared sh;
     u64* const s_key = sh.maxk;
@@ -950,10 +996,24 @@ __global__ void __launch_bounds__(NTF) fs_collect_k(const void* __restrict__ log
     u32& s_ncol = sh.ncol;
     __shared__ u32 s_off[FS_MAX_SPLITS + 1];
     __shared__ unsigned s_flag;
-    const int S = gridDim.x, sp = blockIdx.x, r = blockIdx.y;
+    __shared__ int s_sel;
+    const int S = gridDim.x, sp = blockIdx.x, wr = blockIdx.y;
+    if (flags && wr >= DEFER_ROWS) {
+        // the flagged rows past the workspace's, shared out over this row of blocks, each taken whole
+        for (int k = DEFER_ROWS + sp;; k += S) {
+            const int q = fs_row(flags, rows, k, &s_sel);
+            if (q < 0) break;
+            full_row<DT, COUNTS, MASK>(logits, stride, vocab, counts, mask, params, uniforms, vec, out_ids, out_greedy, out_probs,
+                                       out_logprobs, out_status, q, sh);
+            __syncthreads();
+        }
+        return;
+    }
+    const int r = flags ? fs_row(flags, rows, wr, &s_sel) : wr;
+    if (r < 0) return;
     const int tid = threadIdx.x, w = tid / WAVE, l = lane_id();
     const RowParamsDev p = params[r];
-    const FsRow* row = &ws.rows[r];
+    const FsRow* row = &ws.rows[wr];
     const u32 state0 = ld_agent(&row->state);
     if (state0 == FS_RADIX) {
         // marked by pass 0 (top-k with a cut, an infinite maximum or 1/T): the row's first block takes the radix path
@@ -1014,10 +1074,10 @@ __global__ void __launch_bounds__(NTF) fs_collect_k(const void* __restrict__ log
         u64 v = 0;
 #pragma unroll
         for (int k = 0; k < NWF; ++k) v += s_tilew[t - t0][k];
-        st_agent(&ws.tiles[(size_t)r * ntiles + t], v);
+        st_agent(&ws.tiles[(size_t)wr * ntiles + t], v);
     }
     const u32 nb = s_ncol;
-    const size_t slot = (size_t)r * S + sp;
+    const size_t slot = (size_t)wr * S + sp;
     if (tid == 0) st_agent(&ws.ccount[slot], nb);
     for (u32 i = tid; i < nb && i < (u32)CAP; i += NTF) {
         st_agent(&ws.ckey[slot * CAP + i], s_key[i]);
@@ -1026,7 +1086,7 @@ __global__ void __launch_bounds__(NTF) fs_collect_k(const void* __restrict__ log
     if (!arrive_last(&ws.cnt2[r], (unsigned)S, &s_flag)) return;
     // ---- the row's last block: gather the collected tokens (or hand the row to the radix path)
     // the blocks' counts (one load per thread), then their offsets
-    if (tid < S) s_off[tid + 1] = ld_agent(&ws.ccount[(size_t)r * S + tid]);
+    if (tid < S) s_off[tid + 1] = ld_agent(&ws.ccount[(size_t)wr * S + tid]);
     __syncthreads();
     if (tid == 0) {
         u32 off = 0;
@@ -1047,11 +1107,11 @@ __global__ void __launch_bounds__(NTF) fs_collect_k(const void* __restrict__ log
     for (int o = 0; o < S; ++o) {
         const u32 cnt = s_off[o + 1] - s_off[o];
         for (u32 i = tid; i < cnt; i += NTF) {
-            s_key[s_off[o] + i] = ld_agent(&ws.ckey[((size_t)r * S + o) * CAP + i]);
-            s_mass[s_off[o] + i] = ld_agent(&ws.cmass[((size_t)r * S + o) * CAP + i]);
+            s_key[s_off[o] + i] = ld_agent(&ws.ckey[((size_t)wr * S + o) * CAP + i]);
+            s_mass[s_off[o] + i] = ld_agent(&ws.cmass[((size_t)wr * S + o) * CAP + i]);
         }
     }
-    for (int t = tid; t < ntiles; t += NTF) s_tile[t] = ld_agent(&ws.tiles[(size_t)r * ntiles + t]);
+    for (int t = tid; t < ntiles; t += NTF) s_tile[t] = ld_agent(&ws.tiles[(size_t)wr * ntiles + t]);
     __syncthreads();
     u64 kp = (u64)VALID_MIN_OK << 32;  // every valid key
     if (topp) {
@@ -1154,30 +1214,36 @@ size_t sample_full_workspace_bytes(int rows, int vocab) {
     return pl.S >= 2 ? pl.bytes : 256;
 }
 
+size_t sample_full_deferred_workspace_bytes(int rows, int vocab) {
+    return fs_plan(rows < DEFER_ROWS ? rows : DEFER_ROWS, vocab).bytes;
+}
+
 int launch_sample_full(const void* logits, int dtype, int rows, int stride, int vocab, const int32_t* counts, const uint32_t* mask,
                        const void* params, const float* uniforms, int* out_ids, int* out_greedy, float* out_probs, float* out_logprobs,
-                       int* out_status, void* ws, size_t ws_bytes, void* stream) {
+                       int* out_status, void* ws, size_t ws_bytes, void* stream, const unsigned* row_flags) {
     const size_t esz = dtype == GBS_DTYPE_F32 ? 4 : 2;
     const bool vec = stride % 4 == 0 && aligned(logits, 4 * esz) && (!counts || (vocab % 4 == 0 && aligned(counts, 16)));
     const hipStream_t st = to_stream(stream);
     const RowParamsDev* p = (const RowParamsDev*)params;
-    const FsPlan pl = fs_plan(rows, vocab);
-    const bool split = pl.S >= 2;
+    // under per-row dispatch the split path serves the flagged rows, its workspace sized for DEFER_ROWS of them
+    const int wrows = row_flags ? (rows < DEFER_ROWS ? rows : DEFER_ROWS) : rows;
+    const FsPlan pl = fs_plan(wrows, vocab);
+    const bool split = pl.S >= 2 || row_flags;
     if (split && (!ws || !aligned(ws, 256) || ws_bytes < pl.bytes)) return GBS_ERR_INVALID;
-    const FsWs w = split ? fs_carve(ws, rows, pl) : FsWs{};
+    const FsWs w = split ? fs_carve(ws, wrows, pl) : FsWs{};
     auto run = [&]<int D, bool C, bool Mk>() {
         if (split) {
-            const dim3 grid(pl.S, rows);
+            const dim3 grid(pl.S, row_flags ? DEFER_ROWS + 1 : rows);
             hipLaunchKernelGGL((fs_pass0_k<D, C, Mk>), grid, dim3(NTF), 0, st, logits, (long long)stride, vocab, counts, mask, p, uniforms, vec,
-                               pl.tpb, w, out_ids, out_greedy, out_probs, out_logprobs, out_status);
+                               pl.tpb, w, out_ids, out_greedy, out_probs, out_logprobs, out_status, row_flags, rows);
             hipLaunchKernelGGL((fs_hist_k<D, C, Mk>), grid, dim3(NTF), 0, st, logits, (long long)stride, vocab, counts, mask, p, vec, pl.tpb,
-                               w);
+                               w, row_flags, rows);
             hipLaunchKernelGGL((fs_collect_k<D, C, Mk>), grid, dim3(NTF), 0, st, logits, (long long)stride, vocab, counts, mask, p,
-                               uniforms, vec, pl.tpb, w, out_ids, out_greedy, out_probs, out_logprobs, out_status);
+                               uniforms, vec, pl.tpb, w, out_ids, out_greedy, out_probs, out_logprobs, out_status, row_flags, rows);
         }
         else
             hipLaunchKernelGGL((sample_full_k<D, C, Mk>), dim3(rows), dim3(NTF), 0, st, logits, (long long)stride, vocab, counts, mask,
-                               p, uniforms, vec, out_ids, out_greedy, out_probs, out_logprobs, out_status);
+                               p, uniforms, vec, out_ids, out_greedy, out_probs, out_logprobs, out_status, row_flags);
     };
     const bool c = counts != nullptr, m = mask != nullptr;
     if (dtype == GBS_DTYPE_F32) {
@@ -1185,11 +1251,16 @@ int launch_sample_full(const void* logits, int dtype, int rows, int stride, int 
         else if (c) run.template operator()<GBS_DTYPE_F32, true, false>();
         else if (m) run.template operator()<GBS_DTYPE_F32, false, true>();
         else run.template operator()<GBS_DTYPE_F32, false, false>();
-    } else {
+    } else if (dtype == GBS_DTYPE_BF16) {
         if (c && m) run.template operator()<GBS_DTYPE_BF16, true, true>();
         else if (c) run.template operator()<GBS_DTYPE_BF16, true, false>();
         else if (m) run.template operator()<GBS_DTYPE_BF16, false, true>();
         else run.template operator()<GBS_DTYPE_BF16, false, false>();
+    } else {
+        if (c && m) run.template operator()<GBS_DTYPE_F16, true, true>();
+        else if (c) run.template operator()<GBS_DTYPE_F16, true, false>();
+        else if (m) run.template operator()<GBS_DTYPE_F16, false, true>();
+        else run.template operator()<GBS_DTYPE_F16, false, false>();
     }
     return launch_status();
 }

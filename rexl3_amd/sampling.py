@@ -18,6 +18,7 @@ from . import _lib
 MARGIN = 8  # crates/sampling/src/lib.rs:26
 TOP_K_CAP = 56  # crates/server/src/api.rs:43-44
 ROW_OK, ROW_NO_CANDIDATES, ROW_NAN_LOGIT, ROW_INVALID_PARAMS = 0, 1, 2, 3
+KMAX_MIXED = -1  # sample_rows: per-row dispatch for a batch that mixes rows of any top_k (GBS_KMAX_MIXED)
 STATUS_NAMES = {0: "ok", 1: "NoCandidates", 2: "NanLogit", 3: "InvalidParams"}
 DTYPE_CODE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 
@@ -351,15 +352,15 @@ def _check(t, name: str, dtype, shape: tuple, device):
 def sample_rows(logits: torch.Tensor, params: np.ndarray | torch.Tensor, uniforms: torch.Tensor, counts: torch.Tensor | None = None,
                 mask: torch.Tensor | None = None, kmax: int = 64, logprobs: bool = False, probs: bool = True,
                 vocab: int | None = None):
-    """gbs_sample_rows over logits [rows, stride] (f32 / bf16, row stride may exceed `vocab`: the lm_head's padded
+    """gbs_sample_rows over logits [rows, stride] (f32 / bf16 / f16, row stride may exceed `vocab`: the lm_head's padded
     layout; columns past `vocab` are never read). counts int32 [rows, vocab], mask uint32 [rows, ceil(vocab / 32)],
     uniforms float32 [rows]. Returns a dict of device tensors: ids, greedy, status, and probs / logprobs when asked."""
     _require_cuda(logits, "logits")
     rows, stride = logits.shape
     vocab = stride if vocab is None else vocab
     dev = logits.device
-    if logits.dtype not in (torch.float32, torch.bfloat16) or logits.stride(1) != 1 or not 0 < vocab <= stride:
-        raise ValueError("logits must be f32 or bf16 rows with unit column stride and vocab <= stride")
+    if logits.dtype not in DTYPE_CODE or logits.stride(1) != 1 or not 0 < vocab <= stride:
+        raise ValueError("logits must be f32, bf16 or f16 rows with unit column stride and vocab <= stride")
     _check(counts, "counts", torch.int32, (rows, vocab), dev)
     _check(mask, "mask", (torch.uint32, torch.int32), (rows, -(-vocab // 32)), dev)
     _check(uniforms, "uniforms", torch.float32, (rows,), dev)

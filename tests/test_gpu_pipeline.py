@@ -355,7 +355,7 @@ def test_full_and_fast_paths_alternate_on_one_workspace():
 
 @pytest.mark.parametrize("kmax", [64, 0])
 @pytest.mark.parametrize("vocab,pad", [(151_936, 64), (50_001, 7)])
-@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
 def test_padded_rows_stride_above_vocab(dtype, vocab, pad, kmax):
     """The lm_head's padded layout (crates/cuda/csrc/glue.cu:1084-1098 reads columns [0, valid) of rows `stride` apart):
     logits [rows, vocab + pad] whose pad columns hold NaN or +inf. A kernel that read one of them would report NanLogit
@@ -370,17 +370,22 @@ def test_padded_rows_stride_above_vocab(dtype, vocab, pad, kmax):
         x = W.to_bf16_bits(x)
         full = np.empty((rows, vocab + pad), np.uint16)
         full[:, vocab:] = np.where(np.arange(rows)[:, None] % 2 == 0, 0x7FC0, 0x7F80)
+    elif dtype == "f16":
+        x = x.astype(np.float16).view(np.uint16)
+        full = np.empty((rows, vocab + pad), np.uint16)
+        full[:, vocab:] = np.where(np.arange(rows)[:, None] % 2 == 0, 0x7E00, 0x7C00)
     else:
         full = np.empty((rows, vocab + pad), np.float32)
         full[:, vocab:] = np.where(np.arange(rows)[:, None] % 2 == 0, np.nan, np.inf)
     full[:, :vocab] = x
     log(f"padded rows dtype={dtype} vocab={vocab} pad={pad} kmax={kmax}")
-    t = dev(full, torch.bfloat16) if dtype == "bf16" else dev(full)
+    tdt = {"bf16": torch.bfloat16, "f16": torch.float16}.get(dtype)
+    t = dev(full, tdt) if tdt is not None else dev(full)
     g = S.sample_rows(t, cfg["params"], dev(cfg["uniforms"]), dev(cfg["counts"]), dev(cfg["mask"]), kmax=kmax, logprobs=True,
                       vocab=vocab)
     g = {k: host(v) for k, v in g.items()}
-    w = O.sample_rows(x, O.DTYPE_BF16 if dtype == "bf16" else O.DTYPE_F32, cfg["counts"], cfg["mask"], cfg["params"],
-                      cfg["uniforms"], threads=8)
+    w = O.sample_rows(x, {"bf16": O.DTYPE_BF16, "f16": O.DTYPE_F16}.get(dtype, O.DTYPE_F32), cfg["counts"], cfg["mask"],
+                      cfg["params"], cfg["uniforms"], threads=8)
     assert (w["status"] == 0).all()
     compare(g, w, f"padded {dtype} {vocab}+{pad} kmax {kmax}")
 
@@ -419,3 +424,123 @@ def test_workspaces_are_per_stream():
     assert {s1.cuda_stream, s2.cuda_stream} <= {k[1] for k in keys}
     for o in outs:
         assert np.array_equal(host(o["ids"]), w["ids"])
+
+
+@pytest.mark.parametrize("kmax", [64, 0])
+def test_f16_logits_edge_values(kmax):
+    """fp16 logits (the lm_head's half-precision output) widened exactly: subnormals, +-0 ties, the largest finite
+    values, -inf (a banned token), and a row with a NaN (status NanLogit), against the oracle."""
+    need_gpu()
+    rows, vocab = 12, 20_000
+    cfg = W.northstar(seed=17, rows=rows, vocab=vocab)
+    x = cfg["logits"].astype(np.float16)
+    x[0, :50] = np.float16(6.0e-8)                    # subnormals
+    x[1, :] = np.float16(0.0)
+    x[1, ::3] = np.float16(-0.0)                      # ties of +0 and -0 everywhere
+    x[2, 123] = np.float16(65504.0)                   # the largest finite value
+    x[3, 77] = np.float16(-np.inf)
+    x[4, 5] = np.float16(np.nan)
+    cfg["mask"][4, 0] |= np.uint32(1 << 5)             # allowed: a NaN at a banned position is ignored
+    if kmax == 0:
+        cfg["params"]["top_k"][::3] = 0
+    bits = x.view(np.uint16)
+    g = S.sample_rows(dev(bits, torch.float16), cfg["params"], dev(cfg["uniforms"]), dev(cfg["counts"]), dev(cfg["mask"]), kmax=kmax,
+                      logprobs=True)
+    g = {k: host(v) for k, v in g.items()}
+    w = O.sample_rows(bits, O.DTYPE_F16, cfg["counts"], cfg["mask"], cfg["params"], cfg["uniforms"], threads=8)
+    assert w["status"][4] == O.ROW_NAN_LOGIT
+    compare(g, w, f"f16 kmax {kmax}")
+
+
+DEFER_OFFSET = 3 * 65536 * 4  # the per-row dispatch flags in the workspace's control region
+
+
+def mixed_batch(rows, vocab, seed=23):
+    """A north-star batch whose rows mix top-k settings as an engine's decode round does: most rows top_k 50, some
+    top_k 0 (top-p over the whole vocabulary) on peaked rows, some top_k 100, and some top_k 0 rows whose logits are
+    flat (config 3's N(0, 1.5^2)), where the top-p cut lies far beyond any 64 candidates."""
+    cfg = W.northstar(seed=seed, rows=rows, vocab=vocab)
+    p = cfg["params"]
+    peaked0 = np.arange(1, rows, 10)
+    k100 = np.setdiff1d(np.arange(4, rows, 16), peaked0)
+    flat = np.setdiff1d(np.setdiff1d(np.arange(7, rows, 21), peaked0), k100)
+    p["top_k"][peaked0] = 0
+    p["top_k"][k100] = 100
+    p["top_k"][flat] = 0
+    p["min_p"][k100[::2]] = 0.02
+    x = cfg["logits"]
+    x[flat] = (W.normals(seed + 1, len(flat) * vocab) * 1.5).astype(np.float32).reshape(len(flat), vocab)
+    # the peaked rows: five dominant tokens (allowed, no history) that hold nearly all the mass, the top-p cut among them
+    rng = np.random.default_rng(seed)
+    for r in peaked0:
+        ids = rng.choice(vocab, 5, replace=False)
+        x[r, ids] = [24.0, 23.6, 23.3, 23.0, 22.8]
+        cfg["counts"][r, ids] = 0
+        cfg["mask"][r, ids // 32] |= (np.uint32(1) << (ids % 32).astype(np.uint32))
+    return cfg, peaked0, k100, flat
+
+
+@pytest.mark.parametrize("rows", [256, 40])  # one block per row; split rows
+def test_per_row_dispatch_mixed_batch(rows):
+    need_gpu()
+    vocab = 151_936 if rows == 256 else 60_000
+    cfg, peaked0, k100, flat = mixed_batch(rows, vocab)
+    log(f"mixed batch rows={rows}")
+    g, w = run_both(cfg, kmax=S.KMAX_MIXED)
+    compare(g, w, f"mixed {rows}")
+    # the same ids as the full-distribution path
+    g0, _ = run_both(cfg, kmax=0)
+    assert np.array_equal(g["ids"], g0["ids"]) and np.array_equal(g["status"], g0["status"])
+    # which rows the single pass left over: the flat ones, not the peaked top_k 0 rows nor the top-k rows
+    ws = S.WORKSPACE.get(torch.device("cuda", torch.cuda.current_device()), "sample", 0)
+    flags = host(ws[DEFER_OFFSET:DEFER_OFFSET + 4 * rows].view(torch.int32))
+    allowed = np.unpackbits(cfg["mask"].view(np.uint8), axis=1, bitorder="little")[:, :vocab].sum(axis=1)
+    wide = flat[allowed[flat] >= 1000]  # a flat row with a handful of allowed tokens is exact in the single pass
+    assert len(wide) > 0 and flags[wide].all(), (wide, flags[wide])
+    assert not flags[peaked0].any(), (peaked0, flags[peaked0])
+    in_range = np.setdiff1d(np.arange(rows), np.concatenate([peaked0, k100, flat]))
+    assert not flags[in_range].any()
+    log(f"deferred rows {np.nonzero(flags)[0].tolist()}; top_k 100 rows deferred {int(flags[k100].sum())} of {len(k100)}")
+
+
+def test_per_row_dispatch_edge_rows():
+    """Open rows at the edges: fewer allowed tokens than the list holds (the list is the whole row, exact), min-p alone
+    (no top-p) cutting inside the list or not, T = 0, and an open row with NaN."""
+    need_gpu()
+    rows, vocab = 16, 30_000
+    cfg = W.northstar(seed=29, rows=rows, vocab=vocab)
+    p = cfg["params"]
+    p["top_k"][:] = 0
+    m = cfg["mask"]
+    m[0] = 0
+    m[0, 0] = 0xFFFFFFFF
+    m[0, 1] = 0x7FFFFFFF            # 63 allowed tokens: the list holds them all
+    m[1] = 0
+    m[1, 0] = 0x0000FFFF            # 16 allowed
+    p["top_p"][2:6] = 1.0           # min-p alone
+    p["min_p"][2:4] = 0.2           # cuts inside the list on a peaked row
+    p["min_p"][4:6] = 1e-9          # keeps far more than 64: the full path
+    p["temperature"][6] = 0.0
+    cfg["logits"][7, 11] = np.nan
+    m[7, 0] |= np.uint32(1 << 11)   # allowed: status NanLogit
+    g, w = run_both(cfg, kmax=S.KMAX_MIXED)
+    assert w["status"][7] == O.ROW_NAN_LOGIT
+    compare(g, w, "open edge rows")
+    ws = S.WORKSPACE.get(torch.device("cuda", torch.cuda.current_device()), "sample", 0)
+    flags = host(ws[DEFER_OFFSET:DEFER_OFFSET + 4 * rows].view(torch.int32))
+    assert not flags[[0, 1, 2, 3, 6, 7]].any() and flags[[4, 5]].all(), flags
+
+
+def test_per_row_dispatch_more_deferred_rows_than_the_workspace_holds():
+    """Every row flat with top_k 0: all of them are left over, more than the follow-up's 32 workspace rows, so the rest
+    are taken whole by single blocks; the results are the oracle's."""
+    need_gpu()
+    rows, vocab = 100, 30_000
+    cfg = W.config3(seed=41, rows=rows)
+    cfg["logits"] = np.ascontiguousarray(cfg["logits"][:, :vocab])
+    cfg["counts"] = np.ascontiguousarray(cfg["counts"][:, :vocab])
+    g, w = run_both(cfg, kmax=S.KMAX_MIXED)
+    compare(g, w, "all rows left over")
+    ws = S.WORKSPACE.get(torch.device("cuda", torch.cuda.current_device()), "sample", 0)
+    flags = host(ws[DEFER_OFFSET:DEFER_OFFSET + 4 * rows].view(torch.int32))
+    assert flags.all()
