@@ -229,7 +229,8 @@ __device__ __forceinline__ u64 block_max_u64(u64 v, u64* s_red) {
 // The binned cut: 128 bins per unit of y = log2 of the mass relative to the maximum, down to y = -52 (below -51.5 every
 // mass is 0; the last bin takes them).
 constexpr int BINS_PER_UNIT = 128;
-constexpr int NBINS = 52 * BINS_PER_UNIT;
+constexpr int NUNITS = 52;
+constexpr int NBINS = NUNITS * BINS_PER_UNIT;
 constexpr int CAP = NB;  // collected tokens of the crossing bin (keys in sh.maxk, masses in sh.mass)
 
 struct Shared {
@@ -686,6 +687,7 @@ struct FsWs {
     FsRow* rows;                   // [rows]
     FsPart0* p0;                   // [rows][S]
     u64* hist;                     // [rows][S][NBINS]
+    u64* units;                    // [rows][S][NUNITS]: each block's histogram summed per unit of y
     u64 *ckey, *cmass;             // [rows][S][CAP]
     u32* ccount;                   // [rows][S]
     u64* tiles;                    // [rows][ntiles]
@@ -711,7 +713,7 @@ FsPlan fs_plan(int rows, int vocab) {
     p.S = (p.ntiles + p.tpb - 1) / p.tpb;
     const size_t rs = (size_t)rows * p.S;
     p.bytes = FS_CTL + fs_align((size_t)rows * sizeof(FsRow)) + fs_align(rs * sizeof(FsPart0)) + fs_align(rs * NBINS * 8) +
-              2 * fs_align(rs * CAP * 8) + fs_align(rs * 4) + fs_align((size_t)rows * p.ntiles * 8);
+              fs_align(rs * NUNITS * 8) + 2 * fs_align(rs * CAP * 8) + fs_align(rs * 4) + fs_align((size_t)rows * p.ntiles * 8);
     return p;
 }
 
@@ -726,6 +728,7 @@ FsWs fs_carve(void* ws, int rows, const FsPlan& p) {
     w.rows = (FsRow*)c; c += fs_align((size_t)rows * sizeof(FsRow));
     w.p0 = (FsPart0*)c; c += fs_align(rs * sizeof(FsPart0));
     w.hist = (u64*)c; c += fs_align(rs * NBINS * 8);
+    w.units = (u64*)c; c += fs_align(rs * NUNITS * 8);
     w.ckey = (u64*)c; c += fs_align(rs * CAP * 8);
     w.cmass = (u64*)c; c += fs_align(rs * CAP * 8);
     w.ccount = (u32*)c; c += fs_align(rs * 4);
@@ -941,38 +944,61 @@ __global__ void __launch_bounds__(NTF) fs_hist_k(const void* __restrict__ logits
         }
     });
     __syncthreads();
+    // the block's histogram, and its sums per unit of y (wave w sums units w, w + NWF, ...; two bins per lane)
+    const int w = tid / WAVE;
     u64* mine = ws.hist + ((size_t)wr * S + sp) * NBINS;
     for (int i = tid; i < NBINS; i += NTF) st_agent(&mine[i], s_hist[i]);
+    u64* my_units = ws.units + ((size_t)wr * S + sp) * NUNITS;
+    for (int u = w; u < NUNITS; u += NWF) {
+        const u64 v = wave_sum_u64(s_hist[u * BINS_PER_UNIT + l] + s_hist[u * BINS_PER_UNIT + WAVE + l]);
+        if (l == 0) st_agent(&my_units[u], v);
+    }
     if (!arrive_last(&ws.cnt1[r], (unsigned)S, &s_flag)) return;
-    // the row's histogram: the blocks' histograms summed bin by bin
-    const u64* all = ws.hist + (size_t)wr * S * NBINS;
-    for (int i = tid; i < NBINS; i += NTF) {
+    // The row's crossing bin, from a few KB: the blocks' unit sums give the total, P and the unit where the cumulative
+    // mass from the top reaches P; then only that unit's 128 bins are summed over the blocks.
+    __shared__ u64 s_units[NUNITS];
+    __shared__ u64 s_fine[BINS_PER_UNIT];
+    __shared__ u64 s_bc[3];
+    if (tid < NUNITS) {
+        const u64* all = ws.units + (size_t)wr * S * NUNITS + tid;
         u64 v = 0;
-        for (int o = 0; o < S; ++o) v += ld_agent(&all[(size_t)o * NBINS + i]);
-        s_hist[i] = v;
+        for (int o = 0; o < S; ++o) v += ld_agent(&all[(size_t)o * NUNITS]);
+        s_units[tid] = v;
     }
     __syncthreads();
     if (tid < WAVE) {
-        // lane i owns bins [PB i, PB i + PB): the total, P, then the bin where the cumulative mass reaches P
-        constexpr int PB = NBINS / WAVE;
-        u64 s = 0;
-        for (int k = 0; k < PB; ++k) s += s_hist[l * PB + k];
-        const u64 Z = wave_sum_u64(s);
+        const u64 v = l < NUNITS ? s_units[l] : 0ull;
+        const u64 Z = wave_sum_u64(v);
         const u64 Pv = mul_ceil64(p.top_p, Z);
-        const u64 incl = wave_scan_u64(s);
-        const u64 hit = ballot(incl >= Pv);
-        const int f = (int)__builtin_ctzll(hit);
+        const u64 incl = wave_scan_u64(v);
+        const int f = (int)__builtin_ctzll(ballot(incl >= Pv));  // Pv <= Z: some unit reaches it
         if (l == f) {
-            u64 acc = incl - s;
-            int b = l * PB;
-            for (int k = 0; k < PB; ++k) {
-                b = l * PB + k;
-                if (acc + s_hist[b] >= Pv) break;
-                acc += s_hist[b];
-            }
+            s_bc[0] = (u64)f;
+            s_bc[1] = incl - v;  // the mass of the units above
+            s_bc[2] = Pv;
+        }
+    }
+    __syncthreads();
+    const int ustar = (int)s_bc[0];
+    if (tid < BINS_PER_UNIT) {
+        const u64* all = ws.hist + (size_t)wr * S * NBINS + ustar * BINS_PER_UNIT + tid;
+        u64 v = 0;
+        for (int o = 0; o < S; ++o) v += ld_agent(&all[(size_t)o * NBINS]);
+        s_fine[tid] = v;
+    }
+    __syncthreads();
+    if (tid < WAVE) {
+        // lane i holds bins 2i, 2i + 1 of the unit: the first bin where the cumulative mass reaches P
+        const u64 a0 = s_fine[2 * l], a1 = s_fine[2 * l + 1];
+        const u64 above_u = s_bc[1], Pv = s_bc[2];
+        const u64 incl = above_u + wave_scan_u64(a0 + a1);
+        const u64 excl = incl - a0 - a1;
+        const int f = (int)__builtin_ctzll(ballot(incl >= Pv));
+        if (l == f) {
+            const bool first = excl + a0 >= Pv;
             FsRow* row = &ws.rows[wr];
-            st_agent(&row->bstar, (u32)b);
-            st_agent(&row->above, acc);
+            st_agent(&row->bstar, (u32)(ustar * BINS_PER_UNIT + 2 * l + (first ? 0 : 1)));
+            st_agent(&row->above, first ? excl : excl + a0);
             st_agent(&row->P, Pv);
         }
     }
