@@ -85,6 +85,7 @@ struct FastWs {
     Lse* lse;       // [rows][S]
     unsigned* nan;  // [rows][S]
     unsigned* defer;  // [rows] per-row dispatch: 1 for a row left to the full path (null without per-row dispatch)
+    FsRow* fsrows;    // [rows] per-row dispatch: the full path's record of each row left to it
 };
 
 size_t fast_part_bytes(int rows, int S) {
@@ -101,6 +102,7 @@ FastWs fast_ws(void* ws, int rows, int S) {
     p += align256((size_t)rows * S * sizeof(Lse));
     w.nan = (unsigned*)p;
     w.defer = nullptr;
+    w.fsrows = nullptr;
     return w;
 }
 
@@ -619,9 +621,26 @@ __global__ void __launch_bounds__(NT, GBS_FAST_MINBLOCKS) sample_fast_k(const vo
     if (LOGPROB) rl = wave_lse(rl, clp);  // lanes without a partial hold (-inf, 0)
     rn = wave_or(rn);
     const RowOut o = finish_row(list, p, u, invalid, rn != 0u, count, rl, clp, open);
+    const u64 top = readlane64(list, 0);
     if (l == 0) {
         if (ws.defer) ws.defer[r] = o.status == ROW_DEFERRED ? 1u : 0u;
-        if (o.status != ROW_DEFERRED) write_row(r, o, out_ids, out_greedy, out_probs, out_logprobs, out_status);
+        if (o.status != ROW_DEFERRED) {
+            write_row(r, o, out_ids, out_greedy, out_probs, out_logprobs, out_status);
+        } else {
+            // the full path's record of the row, as its pass 0 would write it (which it then skips): a flagged row is
+            // valid, NaN-free, has 64 allowed tokens or more and T > 0; a top_k above 64 takes the radix path
+            FsRow* fr = ws.fsrows + r;
+            const float M = okey_to_f32(key_ok(top));
+            const bool radix = p.top_k > WAVE || !mass_fast_ok(M, temp_scale(p.temperature));
+            st_agent(&fr->top, top);
+            st_agent((u32*)&fr->lse_m, __float_as_uint(rl.m));
+            st_agent((u32*)&fr->lse_s, __float_as_uint(rl.s));
+            st_agent(&fr->nallowed, (u32)WAVE);
+            st_agent(&fr->bstar, FS_NBINS);
+            st_agent(&fr->above, (u64)0);
+            st_agent(&fr->P, (u64)0);
+            st_agent(&fr->state, radix ? (u32)FS_RADIX : (u32)FS_CUT);
+        }
     }
 }
 
@@ -674,7 +693,10 @@ GBS_EXPORT int gbs_sample_rows(const void* logits, int dtype, int rows, int stri
     const RowParamsDev* p = (const RowParamsDev*)params;
     const bool mixed = kmax == GBS_KMAX_MIXED;
     FastWs w = fast_ws(ws, rows, S);
-    if (mixed) w.defer = (unsigned*)((char*)ws + SAMPLE_DEFER_OFFSET);
+    if (mixed) {
+        w.defer = (unsigned*)((char*)ws + SAMPLE_DEFER_OFFSET);
+        w.fsrows = (FsRow*)((char*)ws + SAMPLE_FSROW_OFFSET);
+    }
     auto run = [&]<int DT>() {
         // per-row dispatch bounds open rows by the log-sum-exp: it is computed whether or not log-probabilities are asked
         dispatch_flags(counts != nullptr, mask != nullptr, mixed || out_logprobs != nullptr, [&]<bool C, bool M, bool L>() {

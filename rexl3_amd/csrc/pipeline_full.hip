@@ -245,16 +245,7 @@ struct Shared {
     u32 ncol;   // tokens collected by the binned cut
 };
 
-// The split path's per-row record (see fs_pass0_k): state FS_CUT (the binned cut continues), FS_DONE (the row's results
-// are written), FS_RADIX (the single-block kernel takes the row).
-enum : u32 { FS_CUT = 0, FS_DONE = 1, FS_RADIX = 2 };
-
-struct FsRow {
-    u64 top;  // the maximum's key
-    float lse_m, lse_s;
-    u32 nallowed, state, bstar, pad;
-    u64 above, P;
-};
+static_assert(NBINS == (int)FS_NBINS, "the per-row record's bin count");
 
 // One radix selection over the keys >= lb of the row: the key K at which the descending cumulative weight (count when
 // by_mass is false, mass otherwise) first reaches `target` -- weight(keys > K) < target <= weight(keys >= K).
@@ -664,7 +655,8 @@ __global__ void __launch_bounds__(NTF) sample_full_k(const void* __restrict__ lo
 // launches, each with a last-block hand-off per row (agent-scope stores and loads, an arrival counter):
 //   fs_pass0_k    maximum, NaN flag, allowed count, LSE; the row's last block finishes every row that needs no cut (an
 //                 invalid, NaN or empty row, T = 0) and marks the rows that need the radix path (top-k with a cut,
-//                 an infinite maximum or 1/T)
+//                 an infinite maximum or 1/T). Not launched under per-row dispatch: the single-pass kernel has written
+//                 the record of every row it flags.
 //   fs_hist_k     the binned cut's mass histogram (rows with top-p); the last block sums the blocks' histograms and
 //                 finds the crossing bin
 //   fs_collect_k  kept masses per tile and the crossing bin's tokens; the last block finds the exact top-p key, the
@@ -672,6 +664,10 @@ __global__ void __launch_bounds__(NTF) sample_full_k(const void* __restrict__ lo
 //                 (the single-block path, full_row), and so is a row whose crossing bin held more than CAP tokens, by its
 //                 last block.
 constexpr int FS_TARGET_BLOCKS = 256;
+#ifndef GBS_FS_DEFER_BLOCKS
+#define GBS_FS_DEFER_BLOCKS 512
+#endif
+constexpr int FS_DEFER_BLOCKS = GBS_FS_DEFER_BLOCKS;  // the split path's blocks when it serves flagged rows (DEFER_ROWS)
 constexpr int FS_MAX_SPLITS = 128;
 
 
@@ -684,7 +680,7 @@ struct FsPart0 {
 
 struct FsWs {
     unsigned *cnt0, *cnt1, *cnt2;  // per-row arrival counters, at fixed offsets (zero between launches)
-    FsRow* rows;                   // [rows]
+    FsRow* rows;                   // [65536] in the control region, indexed by row
     FsPart0* p0;                   // [rows][S]
     u64* hist;                     // [rows][S][NBINS]
     u64* units;                    // [rows][S][NUNITS]: each block's histogram summed per unit of y
@@ -702,17 +698,17 @@ struct FsPlan {
     size_t bytes;
 };
 
-FsPlan fs_plan(int rows, int vocab) {
+FsPlan fs_plan(int rows, int vocab, int target_blocks = FS_TARGET_BLOCKS) {
     FsPlan p;
     p.ntiles = (vocab + TILE - 1) / TILE;
-    int want = (FS_TARGET_BLOCKS + rows - 1) / rows;
+    int want = (target_blocks + rows - 1) / rows;
     if (want > p.ntiles) want = p.ntiles;
     if (want > FS_MAX_SPLITS) want = FS_MAX_SPLITS;
     if (want < 1) want = 1;
     p.tpb = (p.ntiles + want - 1) / want;
     p.S = (p.ntiles + p.tpb - 1) / p.tpb;
     const size_t rs = (size_t)rows * p.S;
-    p.bytes = FS_CTL + fs_align((size_t)rows * sizeof(FsRow)) + fs_align(rs * sizeof(FsPart0)) + fs_align(rs * NBINS * 8) +
+    p.bytes = FS_CTL + fs_align(rs * sizeof(FsPart0)) + fs_align(rs * NBINS * 8) +
               fs_align(rs * NUNITS * 8) + 2 * fs_align(rs * CAP * 8) + fs_align(rs * 4) + fs_align((size_t)rows * p.ntiles * 8);
     return p;
 }
@@ -725,7 +721,7 @@ FsWs fs_carve(void* ws, int rows, const FsPlan& p) {
     w.cnt2 = w.cnt1 + 65536;
     c += FS_CTL;
     const size_t rs = (size_t)rows * p.S;
-    w.rows = (FsRow*)c; c += fs_align((size_t)rows * sizeof(FsRow));
+    w.rows = (FsRow*)((char*)ws + SAMPLE_FSROW_OFFSET);
     w.p0 = (FsPart0*)c; c += fs_align(rs * sizeof(FsPart0));
     w.hist = (u64*)c; c += fs_align(rs * NBINS * 8);
     w.units = (u64*)c; c += fs_align(rs * NUNITS * 8);
@@ -825,7 +821,7 @@ __global__ void __launch_bounds__(NTF) fs_pass0_k(const void* __restrict__ logit
     if (params_invalid(p, u)) {  // every block of the row returns; the first writes the row's results
         if (sp == 0 && tid == 0) {
             fs_out(r, -1, -1, GBS_ROW_INVALID_PARAMS, 0.f, 0.f, out_ids, out_greedy, out_probs, out_logprobs, out_status);
-            st_agent(&ws.rows[wr].state, (u32)FS_DONE);
+            st_agent(&ws.rows[r].state, (u32)FS_DONE);
         }
         return;
     }
@@ -885,7 +881,7 @@ __global__ void __launch_bounds__(NTF) fs_pass0_k(const void* __restrict__ logit
         }
     }
     if (tid != 0) return;
-    FsRow* row = &ws.rows[wr];
+    FsRow* row = &ws.rows[r];
     u32 state = FS_CUT;
     const float M = okey_to_f32(key_ok(k));
     const int greedy = (int)key_id(k);
@@ -928,9 +924,9 @@ __global__ void __launch_bounds__(NTF) fs_hist_k(const void* __restrict__ logits
     const int tid = threadIdx.x, l = lane_id();
     const RowParamsDev p = params[r];
     if (!(p.top_p > 0.0f && p.top_p < 1.0f)) return;  // no top-p: no histogram
-    if (ld_agent(&ws.rows[wr].state) != FS_CUT) return;
+    if (ld_agent(&ws.rows[r].state) != FS_CUT) return;
     const Row<DT, COUNTS, MASK> R = make_row<DT, COUNTS, MASK>(logits, stride, vocab, counts, mask, p, vec, r);
-    const float M = okey_to_f32(key_ok(ld_agent(&ws.rows[wr].top)));
+    const float M = okey_to_f32(key_ok(ld_agent(&ws.rows[r].top)));
     const float c2 = temp_scale(p.temperature);
     const int ntiles = (vocab + TILE - 1) / TILE;
     const int t0 = sp * tpb, t1 = min(ntiles, t0 + tpb);
@@ -996,7 +992,7 @@ __global__ void __launch_bounds__(NTF) fs_hist_k(const void* __restrict__ logits
         const int f = (int)__builtin_ctzll(ballot(incl >= Pv));
         if (l == f) {
             const bool first = excl + a0 >= Pv;
-            FsRow* row = &ws.rows[wr];
+            FsRow* row = &ws.rows[r];
             st_agent(&row->bstar, (u32)(ustar * BINS_PER_UNIT + 2 * l + (first ? 0 : 1)));
             st_agent(&row->above, first ? excl : excl + a0);
             st_agent(&row->P, Pv);
@@ -1039,7 +1035,7 @@ __global__ void __launch_bounds__(NTF) fs_collect_k(const void* __restrict__ log
     if (r < 0) return;
     const int tid = threadIdx.x, w = tid / WAVE, l = lane_id();
     const RowParamsDev p = params[r];
-    const FsRow* row = &ws.rows[wr];
+    const FsRow* row = &ws.rows[r];
     const u32 state0 = ld_agent(&row->state);
     if (state0 == FS_RADIX) {
         // marked by pass 0 (top-k with a cut, an infinite maximum or 1/T): the row's first block takes the radix path
@@ -1111,6 +1107,11 @@ __global__ void __launch_bounds__(NTF) fs_collect_k(const void* __restrict__ log
     }
     if (!arrive_last(&ws.cnt2[r], (unsigned)S, &s_flag)) return;
     // ---- the row's last block: gather the collected tokens (or hand the row to the radix path)
+    float lse_m = 0.f, lse_s = 0.f;  // for the log-probability at the end, loaded now
+    if (tid == 0) {
+        lse_m = __uint_as_float(ld_agent((const u32*)&row->lse_m));
+        lse_s = __uint_as_float(ld_agent((const u32*)&row->lse_s));
+    }
     // the blocks' counts (one load per thread), then their offsets
     if (tid < S) s_off[tid + 1] = ld_agent(&ws.ccount[(size_t)wr * S + tid]);
     __syncthreads();
@@ -1130,12 +1131,18 @@ __global__ void __launch_bounds__(NTF) fs_collect_k(const void* __restrict__ log
                                    out_logprobs, out_status, r, sh);
         return;
     }
-    for (int o = 0; o < S; ++o) {
-        const u32 cnt = s_off[o + 1] - s_off[o];
-        for (u32 i = tid; i < cnt; i += NTF) {
-            s_key[s_off[o] + i] = ld_agent(&ws.ckey[((size_t)wr * S + o) * CAP + i]);
-            s_mass[s_off[o] + i] = ld_agent(&ws.cmass[((size_t)wr * S + o) * CAP + i]);
+    // collected token i is block o's token i - s_off[o], with s_off[o] <= i < s_off[o + 1] (a binary search): all of
+    // them in one round of loads
+    for (u32 i = tid; i < n; i += NTF) {
+        int lo = 0, hi = S;
+        while (hi - lo > 1) {
+            const int mid = (lo + hi) >> 1;
+            if (s_off[mid] <= i) lo = mid;
+            else hi = mid;
         }
+        const size_t src = ((size_t)wr * S + lo) * CAP + (i - s_off[lo]);
+        s_key[i] = ld_agent(&ws.ckey[src]);
+        s_mass[i] = ld_agent(&ws.cmass[src]);
     }
     for (int t = tid; t < ntiles; t += NTF) s_tile[t] = ld_agent(&ws.tiles[(size_t)wr * ntiles + t]);
     __syncthreads();
@@ -1224,9 +1231,8 @@ __global__ void __launch_bounds__(NTF) fs_collect_k(const void* __restrict__ log
     __syncthreads();
     if (tid == 0) {
         const float clp = fs_clp(p);
-        const float lm = __uint_as_float(ld_agent((const u32*)&row->lse_m)), ls = __uint_as_float(ld_agent((const u32*)&row->lse_s));
         fs_out(r, (int)s_bc[1], (int)key_id(top), GBS_ROW_OK, (float)((double)s_bc[2] / (double)z),
-               fs_logprob(__uint_as_float((u32)s_bc[3]), M, clp, lm, ls), out_ids, out_greedy, out_probs, out_logprobs, out_status);
+               fs_logprob(__uint_as_float((u32)s_bc[3]), M, clp, lse_m, lse_s), out_ids, out_greedy, out_probs, out_logprobs, out_status);
     }
 }
 
@@ -1241,7 +1247,7 @@ size_t sample_full_workspace_bytes(int rows, int vocab) {
 }
 
 size_t sample_full_deferred_workspace_bytes(int rows, int vocab) {
-    return fs_plan(rows < DEFER_ROWS ? rows : DEFER_ROWS, vocab).bytes;
+    return fs_plan(rows < DEFER_ROWS ? rows : DEFER_ROWS, vocab, FS_DEFER_BLOCKS).bytes;
 }
 
 int launch_sample_full(const void* logits, int dtype, int rows, int stride, int vocab, const int32_t* counts, const uint32_t* mask,
@@ -1253,15 +1259,17 @@ int launch_sample_full(const void* logits, int dtype, int rows, int stride, int 
     const RowParamsDev* p = (const RowParamsDev*)params;
     // under per-row dispatch the split path serves the flagged rows, its workspace sized for DEFER_ROWS of them
     const int wrows = row_flags ? (rows < DEFER_ROWS ? rows : DEFER_ROWS) : rows;
-    const FsPlan pl = fs_plan(wrows, vocab);
+    const FsPlan pl = row_flags ? fs_plan(wrows, vocab, FS_DEFER_BLOCKS) : fs_plan(wrows, vocab);
     const bool split = pl.S >= 2 || row_flags;
     if (split && (!ws || !aligned(ws, 256) || ws_bytes < pl.bytes)) return GBS_ERR_INVALID;
     const FsWs w = split ? fs_carve(ws, wrows, pl) : FsWs{};
     auto run = [&]<int D, bool C, bool Mk>() {
         if (split) {
             const dim3 grid(pl.S, row_flags ? DEFER_ROWS + 1 : rows);
-            hipLaunchKernelGGL((fs_pass0_k<D, C, Mk>), grid, dim3(NTF), 0, st, logits, (long long)stride, vocab, counts, mask, p, uniforms, vec,
-                               pl.tpb, w, out_ids, out_greedy, out_probs, out_logprobs, out_status, row_flags, rows);
+            // flagged rows: the single-pass kernel has written their records (maximum, log-sum-exp, state), so no pass 0
+            if (!row_flags)
+                hipLaunchKernelGGL((fs_pass0_k<D, C, Mk>), grid, dim3(NTF), 0, st, logits, (long long)stride, vocab, counts, mask, p, uniforms,
+                                   vec, pl.tpb, w, out_ids, out_greedy, out_probs, out_logprobs, out_status, row_flags, rows);
             hipLaunchKernelGGL((fs_hist_k<D, C, Mk>), grid, dim3(NTF), 0, st, logits, (long long)stride, vocab, counts, mask, p, vec, pl.tpb,
                                w, row_flags, rows);
             hipLaunchKernelGGL((fs_collect_k<D, C, Mk>), grid, dim3(NTF), 0, st, logits, (long long)stride, vocab, counts, mask, p,
