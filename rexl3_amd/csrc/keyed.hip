@@ -290,13 +290,16 @@ __global__ void __launch_bounds__(KNT, 1) keyed_fast_k(const void* logits, long 
     const void* row = (const char*)logits + (size_t)r * (size_t)stride * esz;
     const int lo = sp * chunk;
     const int hi = min(valid, lo + chunk);
-    // loads past the row's valid columns (rounded up to a whole group, inside the row) return zeros; the last
-    // wave-step's elements at or past `hi` are not offered
-    const u32 nbytes = (u32)((valid + 3) / 4 * 4) * (u32)esz;
-    const __amdgpu_buffer_rsrc_t R = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(row), (short)0, (int)nbytes, 0x00020000);
+    // The buffer resource covers this block's chunk, [lo, hi) rounded up to a whole group (inside the row): loads past it
+    // return zeros and touch no memory, so a refill is issued whether or not its wave-step exists (a fixed count of loads
+    // per refill keeps the compiler's wait counts exact: a buffer waits for its own loads only). The last wave-step's
+    // elements at or past `hi` are not offered.
+    const u32 nbytes = (u32)max(0, (hi + 3) / 4 * 4 - lo) * (u32)esz;
+    const __amdgpu_buffer_rsrc_t R =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>((const char*)row + (size_t)lo * esz), (short)0, (int)nbytes, 0x00020000);
     const int nws = vec ? (hi - lo + KWSTEP - 1) / KWSTEP : 0;
     auto load = [&](int idx, KRaw<DT>& b) {
-        const u32 e = (u32)(lo + idx * KWSTEP + l * 4);
+        const u32 e = (u32)(idx * KWSTEP + l * 4);  // from the chunk's start
 #pragma unroll
         for (int j = 0; j < KGROUPS; ++j) {
             if constexpr (DT == DT_F32) b.x[j] = __builtin_amdgcn_raw_buffer_load_b128(R, (e + j * KGS) * 4u, 0, 2);
@@ -329,15 +332,21 @@ __global__ void __launch_bounds__(KNT, 1) keyed_fast_k(const void* logits, long 
             if (l == 0) t = __hip_atomic_fetch_add(&s_next, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             return __builtin_amdgcn_readfirstlane(t);
         };
-        // the keys of one loaded wave-step (out of the chunk: key 0, not offered); `first` seeds the gate
-        auto step = [&](KRaw<DT>& B, int idx, bool first, auto&& reload) __attribute__((always_inline)) {
+        // the keys of one loaded wave-step (out of the chunk: key 0, not offered); `first` seeds the gate. The step's
+        // words are copied out of the buffer first and the buffer is refilled at once, at one place for every path, so
+        // that the compiler's wait counts keep the other buffer's loads in flight.
+        auto step = [&](KRaw<DT>& B, int idx, auto first_c, auto&& reload) __attribute__((always_inline)) {
+            constexpr bool first = decltype(first_c)::value;
             const int e = lo + idx * KWSTEP + l * 4;
             wt.apply_shared();
             wt.prefetch_shared();
+            const KRaw<DT> C = B;
+            if (first && GBS_KEYED_LATE_B && KNW + w < nws) load(KNW + w, B0);  // once this wave-step has arrived
+            reload();
             // f32 rows whose gate is a float at or above -inf test the gate with one float compare per element (NaN
             // never passes, as its key 0 is below any such gate); the order keys are built for the elements that pass
-            if constexpr (DT == DT_F32) {
-                if (!first && wt.gate >= NEG_INF_OK) {
+            if constexpr (DT == DT_F32 && !first) {
+                if (wt.gate >= NEG_INF_OK) {
                     float v[KGROUPS * 4];
                     bool in[KGROUPS * 4];
 #pragma unroll
@@ -345,10 +354,9 @@ __global__ void __launch_bounds__(KNT, 1) keyed_fast_k(const void* logits, long 
 #pragma unroll
                         for (int q = 0; q < 4; ++q) {
                             in[j * 4 + q] = e + j * KGS + q < hi;
-                            v[j * 4 + q] = __uint_as_float(B.x[j][q]);
+                            v[j * 4 + q] = __uint_as_float(C.x[j][q]);
                         }
                     }
-                    reload();
                     const float gf = okey_to_f32(wt.gate);
                     bool any = false;
 #pragma unroll
@@ -373,15 +381,13 @@ __global__ void __launch_bounds__(KNT, 1) keyed_fast_k(const void* logits, long 
 #pragma unroll
             for (int j = 0; j < KGROUPS; ++j) {
                 u32 kj[4];
-                kraw_keys<DT>(B, j, kj);
+                kraw_keys<DT>(C, j, kj);
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     in[j * 4 + q] = e + j * KGS + q < hi;
                     k[j * 4 + q] = in[j * 4 + q] ? kj[q] : 0u;
                 }
             }
-            if (first && GBS_KEYED_LATE_B && KNW + w < nws) load(KNW + w, B0);  // once this wave-step has arrived
-            reload();
             if (first) {
                 u32 m = 0;
 #pragma unroll
@@ -411,20 +417,27 @@ __global__ void __launch_bounds__(KNT, 1) keyed_fast_k(const void* logits, long 
             __syncthreads();
             wt.block_bound();
         } else {
-            for (bool first = true;; first = false) {
-                int na = 0, nb = 0;
-                step(A, ia, first, [&]() {
-                    na = grab();
-                    if (na < nws) load(na, A);
-                });
-                ia = na;
-                if (ib >= nws) break;
-                step(B, ib, false, [&]() {
-                    nb = grab();
-                    if (nb < nws) load(nb, B);
-                });
-                ib = nb;
-                if (ia >= nws) break;
+            int na = 0, nb = 0;
+            auto refill_a = [&]() {
+                na = grab();
+                load(na, A);  // past the chunk when na >= nws: zeros, no memory read
+            };
+            auto refill_b = [&]() {
+                nb = grab();
+                load(nb, B);
+            };
+            // the first wave-step (it seeds the gate), then the buffers in turn
+            step(A, ia, std::true_type{}, refill_a);
+            ia = na;
+            if (ib < nws) {
+                for (;;) {
+                    step(B, ib, std::false_type{}, refill_b);
+                    ib = nb;
+                    if (ia >= nws) break;
+                    step(A, ia, std::false_type{}, refill_a);
+                    ia = na;
+                    if (ib >= nws) break;
+                }
             }
         }
         e0 = hi;
