@@ -168,7 +168,7 @@ def measure(wl, args, steps, cpu_seconds, dev, lib, stream):
         # the full path (kmax 0) runs split over fs_* launches when there are fewer rows than CUs
         kernel = ("fs_pass0_k + fs_hist_k + fs_collect_k" if rows < 256 else "sample_full_k") if kmax == 0 else "sample_fast_k"
         if kmax < 0:
-            kernel = "sample_fast_k + fs_pass0_k + fs_hist_k + fs_collect_k over the rows it leaves over"
+            kernel = "sample_fast_k + fs_hist_k + fs_collect_k over the rows it leaves over"
         dtype = "bf16->f32" if is_bf16 else "f32"
         workload = {"northstar": "extended pipeline: penalties (dense i32 counts) + u32 grammar mask + T 0.8 + top-k 50 / top-p 0.9"
                                  " + log-softmax + inverse-CDF draw",
