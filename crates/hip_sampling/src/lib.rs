@@ -145,6 +145,8 @@ pub mod ffi {
                                  out_ids: *mut i32, out_vals: *mut f32, stream: *mut c_void) -> i32;
         pub fn gb_qfn_greedy_gather(ids: *const c_void, vals: *const c_void, count: i32, rows: i32, out_ids: *mut c_void,
                                     out_vals: *mut c_void, stream: *mut c_void) -> i32;
+        pub fn gb_dsv4_mtp_argmax(logits: *const f32, out: *mut i32, rows: i32, vocab: i32, stream: *mut c_void) -> i32;
+        pub fn gb_mtp_pick(logits: *const c_void, n: i32, out_id: *mut c_void, out_p: *mut c_void, j: i32, stream: *mut c_void) -> i32;
         // ---- 2. fused and extended entry points
         pub fn gbs_workspace_clear(ws: *mut c_void, bytes: usize, stream: *mut c_void) -> i32;
         pub fn gbs_keyed_sample_workspace_bytes(rows: i32, valid: i32) -> usize;

@@ -187,6 +187,16 @@ int gb_glm_keyed_pick(const int* ids, const float* vals, int count, int rows, co
  * NaN when any of the row's `count` candidates is NaN. */
 int gb_qfn_greedy_gather(const void* ids, const void* vals, int count, int rows, void* out_ids, void* out_vals, void* stream);
 
+/* Replaces crates/cuda/csrc/dsv4_mtp_gpu.cu:981-985 (gb_dsv4_mtp_argmax; Rust binding crates/cuda/src/dsv4_mtp_gpu.rs:119):
+ * out i32 [rows] = per row of logits f32 [rows, vocab] the lowest id of the largest value above -inf (NaN never
+ * counts, +0 and -0 are equal), 0 when the row has none. */
+int gb_dsv4_mtp_argmax(const float* logits, int* out, int rows, int vocab, void* stream);
+
+/* Replaces crates/cuda/csrc/mtp.cu:162-166 (gb_mtp_pick; Rust binding crates/cuda/src/mtpk.rs:24, 119-127): one row of
+ * bf16 logits [n]; out_id i32 [j] = its argmax as above, out_p f32 [j] = 1 / sum_i exp(x_i - max), the maximum's
+ * softmax probability (NaN when the row holds a NaN or has no finite maximum). Returns 1 for n < 1. */
+int gb_mtp_pick(const void* logits, int n, void* out_id, void* out_p, int j, void* stream);
+
 /* ------------------------------------------------------------------------------------------------------------------
  * 2. Fused and extended entry points
  * ------------------------------------------------------------------------------------------------------------------ */

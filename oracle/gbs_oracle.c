@@ -1312,3 +1312,41 @@ void gbo_markov_walk(float* logits, int32_t* ids, float* conf, const uint16_t* e
     }
     free(cand);
 }
+
+/* ---------------------------------------------------------------------------------------------- draft-head argmax picks */
+
+/* crates/cuda/csrc/dsv4_mtp_gpu.cu:503-539 (argmax_k): per row the first index of the largest value that is above
+ * -inf (a NaN never compares greater; +0 and -0 compare equal, so the earlier one stays); 0 when there is none. */
+void gbo_row_argmax(const float* logits, int rows, int vocab, int32_t* out) {
+    for (int r = 0; r < rows; ++r) {
+        const float* x = logits + (size_t)r * vocab;
+        float bv = -INFINITY;
+        int bi = 0;
+        for (int i = 0; i < vocab; ++i) {
+            if (x[i] > bv) {
+                bv = x[i];
+                bi = i;
+            }
+        }
+        out[r] = bi;
+    }
+}
+
+/* crates/cuda/csrc/mtp.cu:78-117 (pick_kernel): the argmax of a bf16 row as above (0 when no value is above -inf),
+ * and p = 1 / sum_i exp(x_i - max), summed here in double (the reference sums __expf terms in float). p is NaN when
+ * the row holds a NaN or its maximum is not finite (max = -inf when no value is above -inf). */
+void gbo_mtp_pick(const uint16_t* logits, int n, int32_t* out_id, float* out_p) {
+    float bv = -INFINITY;
+    int bi = 0;
+    for (int i = 0; i < n; ++i) {
+        const float v = bf16_to_f32(logits[i]);
+        if (v > bv) {
+            bv = v;
+            bi = i;
+        }
+    }
+    double t = 0.0;
+    for (int i = 0; i < n; ++i) t += exp((double)bf16_to_f32(logits[i]) - (double)bv);
+    *out_id = bi;
+    *out_p = (float)(1.0 / t);
+}

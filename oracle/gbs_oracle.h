@@ -118,6 +118,9 @@ void gbo_selector_walk(const int32_t* anchor, const int32_t* ids, const float* v
  * sigmoid of its margin, nullable). */
 void gbo_markov_walk(float* logits, int32_t* ids, float* conf, const uint16_t* embed, const uint16_t* head, int walk_rows, int vocab,
                      int keyed, int cand_k, uint64_t seed, double temperature, double top_p, double min_p, uint64_t base_pos);
+/* draft-head argmax picks: crates/cuda/csrc/dsv4_mtp_gpu.cu:503-539 and crates/cuda/csrc/mtp.cu:78-117 */
+void gbo_row_argmax(const float* logits, int rows, int vocab, int32_t* out);
+void gbo_mtp_pick(const uint16_t* logits, int n, int32_t* out_id, float* out_p);
 
 #ifdef __cplusplus
 }

@@ -112,6 +112,10 @@ def lib():
         L.gbo_markov_walk.restype = None
         L.gbo_markov_walk.argtypes = [P, P, P, P, P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_uint64, C.c_double, C.c_double,
                                       C.c_double, C.c_uint64]
+        L.gbo_row_argmax.restype = None
+        L.gbo_row_argmax.argtypes = [P, C.c_int, C.c_int, P]
+        L.gbo_mtp_pick.restype = None
+        L.gbo_mtp_pick.argtypes = [P, C.c_int, P, P]
         L.gbo_batch_spec_verify.restype = C.c_int
         L.gbo_batch_spec_verify.argtypes = [P, P, C.c_int, C.c_int, C.c_int, P, P, P, P, P, P, P, C.c_int]
         _lib = L
@@ -349,3 +353,21 @@ def selector_walk(anchor, ids, vals, gate, gate_f32: bool, pred_cb, succ_cb, n_s
                             rank, _p(ws), _p(ro), _p(out), _p(conf), _p(margin))
     return out, conf, margin
 
+
+
+def row_argmax(logits):
+    """crates/cuda/csrc/dsv4_mtp_gpu.cu:503-539: per row, the first index of the largest value above -inf (0 if none)."""
+    x = np.ascontiguousarray(logits, dtype=np.float32)
+    rows, vocab = x.shape
+    out = np.zeros(rows, dtype=np.int32)
+    lib().gbo_row_argmax(_p(x), rows, vocab, _p(out))
+    return out
+
+
+def mtp_pick(bf16_bits):
+    """crates/cuda/csrc/mtp.cu:78-117: (argmax, 1 / sum exp(x - max)) of one bf16 row given as uint16 bits."""
+    x = np.ascontiguousarray(bf16_bits, dtype=np.uint16)
+    i = np.zeros(1, dtype=np.int32)
+    p = np.zeros(1, dtype=np.float32)
+    lib().gbo_mtp_pick(_p(x), x.shape[0], _p(i), _p(p))
+    return int(i[0]), float(p[0])

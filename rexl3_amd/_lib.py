@@ -34,6 +34,8 @@ SIGNATURES = {
     "gb_dsv4_mtp_markov_walk_keyed_bf16_params": (I, [P, P, P, P, P, P, P, I, I, I, P, P]),
     "gb_glm_keyed_pick": (I, [P, P, I, I, P, I, P, P, P]),
     "gb_qfn_greedy_gather": (I, [P, P, I, I, P, P, P]),
+    "gb_dsv4_mtp_argmax": (I, [P, P, I, I, P]),
+    "gb_mtp_pick": (I, [P, I, P, P, I, P]),
     "gbs_workspace_clear": (I, [P, Z, P]),
     "gbs_keyed_sample_workspace_bytes": (Z, [I, I]),
     "gbs_keyed_sample_rows": (I, [P, I, I, I, I, P, I, P, P, P, P, Z, P]),

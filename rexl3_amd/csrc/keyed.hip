@@ -5,6 +5,8 @@
 //    cumsum run on lane 0, at most 64 terms), the Gumbel noise of each kept candidate on its own lane, and an argmax that
 //    keeps the first candidate on ties, as the reference's strict `>` does.
 //  - gb_glm_keyed_pick (crates/cuda/csrc/glm_mtp.cu:266-297), gb_qfn_greedy_gather (crates/cuda/csrc/qfn_verify.cu:11-40).
+//  - gb_dsv4_mtp_argmax (crates/cuda/csrc/dsv4_mtp_gpu.cu:981-985), gb_mtp_pick (crates/cuda/csrc/mtp.cu:162-166): the
+//    draft heads' argmax picks.
 //  - gbs_keyed_sample_rows: exact top-(top_k + 8) over the full row and the keyed draw in ONE launch (keyed_fast_k: one
 //    block per row, or a few per row with a last-block hand-off when there are fewer rows than CUs). Only the chosen id
 //    leaves the device.
@@ -192,6 +194,96 @@ __global__ void greedy_gather_k(const int* __restrict__ ids, const float* __rest
     for (int c = 0; c < count; ++c) nan |= vals[base + c] != vals[base + c];
     out_ids[r] = ids[base];
     out_vals[r] = nan ? __uint_as_float(0x7fc00000u) : vals[base];
+}
+
+// ------------------------------------------------------------------------------------------------ draft-head argmax picks
+// One 1024-thread block per row. The largest value above -inf, lowest id on ties, is the largest order key
+// okey << 32 | ~id over those elements (NaN and -inf never count; +-0 compare equal); key 0 means none.
+
+constexpr int PICK_NT = 1024;
+
+__device__ __forceinline__ u64 pick_key(float v, u32 id) { return v > -INFINITY ? make_key(okey_f32(v), id) : 0ull; }
+
+// the block's largest key (every thread gets it)
+__device__ __forceinline__ u64 block_max_key(u64 k, u64* s_red) {
+    const int w = (int)threadIdx.x / WAVE, l = lane_id();
+    k = wave_max_u64(k);
+    if (l == 0) s_red[w] = k;
+    __syncthreads();
+    u64 b = l < PICK_NT / WAVE ? s_red[l] : 0ull;
+    b = wave_max_u64(b);
+    __syncthreads();
+    return b;
+}
+
+// f32 [rows, vocab] -> out[r]: the argmax of row r (0 when no element is above -inf)
+__global__ void __launch_bounds__(PICK_NT) row_argmax_k(const float* __restrict__ logits, int vocab, bool vec, int* __restrict__ out) {
+    __shared__ u64 s_red[PICK_NT / WAVE];
+    const int r = blockIdx.x, tid = (int)threadIdx.x;
+    const float* row = logits + (size_t)r * vocab;
+    u64 best = 0;
+    if (vec) {
+        const float4* row4 = (const float4*)row;
+        for (int i = tid; i < vocab / 4; i += PICK_NT) {
+            const float4 v = row4[i];
+            const u32 e = (u32)i * 4u;
+            const u64 a = max(pick_key(v.x, e), pick_key(v.y, e + 1)), b = max(pick_key(v.z, e + 2), pick_key(v.w, e + 3));
+            best = max(best, max(a, b));
+        }
+    } else {
+        for (int i = tid; i < vocab; i += PICK_NT) best = max(best, pick_key(row[i], (u32)i));
+    }
+    best = block_max_key(best, s_red);
+    if (tid == 0) out[r] = best ? (int)key_id(best) : 0;
+}
+
+// one bf16 row [n] -> out_id[j]: its argmax (0 when no element is above -inf); out_p[j]: 1 / sum_i exp(x_i - max),
+// the softmax probability of the maximum (NaN when the row holds a NaN or no finite maximum)
+__global__ void __launch_bounds__(PICK_NT) mtp_pick_k(const u16* __restrict__ logits, int n, bool vec, int* __restrict__ out_id,
+                                                      float* __restrict__ out_p, int j) {
+    __shared__ u64 s_red[PICK_NT / WAVE];
+    __shared__ float s_sum[PICK_NT / WAVE];
+    const int tid = (int)threadIdx.x, w = tid / WAVE, l = lane_id();
+    auto bf = [](u32 h) { return __uint_as_float(h << 16); };
+    u64 best = 0;
+    if (vec) {
+        const uint4* row8 = (const uint4*)logits;
+        for (int i = tid; i < n / 8; i += PICK_NT) {
+            const uint4 v = row8[i];
+            const u32 e = (u32)i * 8u;
+            const u32 wd[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                best = max(best, max(pick_key(bf(wd[q] & 0xFFFFu), e + 2 * q), pick_key(bf(wd[q] >> 16), e + 2 * q + 1)));
+        }
+    } else {
+        for (int i = tid; i < n; i += PICK_NT) best = max(best, pick_key(bf(logits[i]), (u32)i));
+    }
+    best = block_max_key(best, s_red);
+    const float mx = best ? okey_to_f32(key_ok(best)) : -INFINITY;
+    // second read of the row (from L2): the sum of exp(x - max)
+    float a = 0.f;
+    if (vec) {
+        const uint4* row8 = (const uint4*)logits;
+        for (int i = tid; i < n / 8; i += PICK_NT) {
+            const uint4 v = row8[i];
+            const u32 wd[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) a += __expf(bf(wd[q] & 0xFFFFu) - mx) + __expf(bf(wd[q] >> 16) - mx);
+        }
+    } else {
+        for (int i = tid; i < n; i += PICK_NT) a += __expf(bf(logits[i]) - mx);
+    }
+#pragma unroll
+    for (int m = 1; m < WAVE; m <<= 1) a += __shfl_xor(a, m, WAVE);
+    if (l == 0) s_sum[w] = a;
+    __syncthreads();
+    if (tid == 0) {
+        float t = 0.f;
+        for (int o = 0; o < PICK_NT / WAVE; ++o) t += s_sum[o];
+        out_id[j] = best ? (int)key_id(best) : 0;
+        out_p[j] = 1.f / t;
+    }
 }
 
 // ------------------------------------------------------------------------------------------------ fused keyed sampler
@@ -1032,6 +1124,20 @@ GBS_EXPORT int gb_qfn_greedy_gather(const void* ids, const void* vals, int count
     if (rows == 0) return 0;
     hipLaunchKernelGGL(greedy_gather_k, dim3((rows + 127) / 128), dim3(128), 0, to_stream(stream), (const int*)ids, (const float*)vals,
                        count, rows, (int*)out_ids, (float*)out_vals);
+    return launch_status();
+}
+
+GBS_EXPORT int gb_dsv4_mtp_argmax(const float* logits, int* out, int rows, int vocab, void* stream) {
+    if (!logits || !out || rows <= 0 || vocab <= 0) return GBS_ERR_INVALID;
+    const bool vec = vocab % 4 == 0 && aligned(logits, 16);
+    hipLaunchKernelGGL(row_argmax_k, dim3(rows), dim3(PICK_NT), 0, to_stream(stream), logits, vocab, vec, out);
+    return launch_status();
+}
+
+GBS_EXPORT int gb_mtp_pick(const void* logits, int n, void* out_id, void* out_p, int j, void* stream) {
+    if (n < 1 || j < 0 || !logits || !out_id || !out_p) return GBS_ERR_INVALID;
+    const bool vec = n % 8 == 0 && aligned(logits, 16);
+    hipLaunchKernelGGL(mtp_pick_k, dim3(1), dim3(PICK_NT), 0, to_stream(stream), (const u16*)logits, n, vec, (int*)out_id, (float*)out_p, j);
     return launch_status();
 }
 

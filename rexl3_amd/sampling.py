@@ -246,6 +246,29 @@ def greedy_gather(ids: torch.Tensor, vals: torch.Tensor):
     return oi, ov
 
 
+def dsv4_argmax(logits: torch.Tensor) -> torch.Tensor:
+    """gb_dsv4_mtp_argmax over f32 logits [rows, vocab]: per row the lowest id of the largest value above -inf (0 if
+    none), int32 [rows]."""
+    _require_cuda(logits, "logits")
+    if logits.dtype != torch.float32 or logits.dim() != 2 or not logits.is_contiguous():
+        raise ValueError("logits must be a contiguous float32 [rows, vocab] tensor")
+    rows, vocab = logits.shape
+    out = torch.empty(rows, dtype=torch.int32, device=logits.device)
+    _lib.call("gb_dsv4_mtp_argmax", _ptr(logits), _ptr(out), rows, vocab, _stream(logits.device))
+    return out
+
+
+def mtp_pick(logits: torch.Tensor, out_id: torch.Tensor, out_p: torch.Tensor, j: int) -> None:
+    """gb_mtp_pick over one bf16 row [n]: out_id[j] = its argmax (lowest id on ties), out_p[j] = the maximum's softmax
+    probability."""
+    _require_cuda(logits, "logits")
+    if logits.dtype != torch.bfloat16 or logits.dim() != 1 or not logits.is_contiguous():
+        raise ValueError("logits must be a contiguous bfloat16 [n] tensor")
+    if out_id.dtype != torch.int32 or out_p.dtype != torch.float32 or out_id.numel() <= j or out_p.numel() <= j or j < 0:
+        raise ValueError("out_id int32 / out_p float32 must hold index j")
+    _lib.call("gb_mtp_pick", _ptr(logits), logits.shape[0], _ptr(out_id), _ptr(out_p), j, _stream(logits.device))
+
+
 # ------------------------------------------------------------------------------------------------ fused keyed sampler
 
 def keyed_sample_rows(logits: torch.Tensor, params: np.ndarray | torch.Tensor, depth: int = 0, valid: int | None = None,

@@ -72,6 +72,8 @@ def test_argument_checks_refuse_before_touching_memory():
     assert lib.gb_glm_keyed_pick(n, n, 65, 1, n, 0, n, n, n) == 1
     assert lib.gb_glm_keyed_pick(n, n, 8, 0, n, 0, n, n, n) == 0
     assert lib.gb_qfn_greedy_gather(n, n, 8, 1, n, n, n) == 1
+    assert lib.gb_dsv4_mtp_argmax(n, n, 1, 100, n) == 1
+    assert lib.gb_mtp_pick(n, 0, n, n, 0, n) == 1
     assert lib.gbs_keyed_sample_rows(n, 0, 1, 100, 101, n, 0, n, n, n, n, 0, n) == 1
     assert lib.gbs_keyed_sample_rows(n, 7, 1, 100, 100, n, 0, n, n, n, n, 0, n) == 1
     assert lib.gbs_sample_rows(n, 0, 1, 100, 100, n, n, n, n, 65, n, n, n, n, n, n, 0, n) == 1
