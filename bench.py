@@ -250,7 +250,8 @@ def measure(wl, args, steps, cpu_seconds, dev, lib, stream):
         ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
         lib.gbs_workspace_clear(ws.data_ptr(), wsb, stream)
         P = lambda t: C.c_void_p(t.data_ptr())  # noqa: E731
-        argvs = [(P(tts[i]), P(dts[i]), n_seq, width, vocab, P(di), P(te), P(ua), P(ur), P(acc), P(toks), P(stt), P(ws), wsb, stream)
+        argvs = [(P(tts[i]), P(dts[i]), n_seq, width, vocab, vocab, P(di), P(te), P(ua), P(ur), P(acc), P(toks), P(stt), P(ws), wsb,
+                  stream)
                  for i in range(ncopy)]
         fn = lib.gbs_spec_verify
         turn = [0]

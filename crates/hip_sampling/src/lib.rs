@@ -170,7 +170,7 @@ pub mod ffi {
                                        out_greedy: *mut i32, out_probs: *mut f32, out_logprobs: *mut f32, out_status: *mut i32,
                                        stream: *mut c_void) -> i32;
         pub fn gbs_spec_verify_workspace_bytes(n_seq: i32, width: i32, vocab: i32) -> usize;
-        pub fn gbs_spec_verify(target: *const f32, draft: *const f32, n_seq: i32, width: i32, vocab: i32, draft_ids: *const i32,
+        pub fn gbs_spec_verify(target: *const f32, draft: *const f32, n_seq: i32, width: i32, vocab: i32, stride: i32, draft_ids: *const i32,
                                temperatures: *const f32, u_accept: *const f32, u_resample: *const f32, out_accepted: *mut i32,
                                out_tokens: *mut i32, out_status: *mut i32, ws: *mut c_void, ws_bytes: usize, stream: *mut c_void) -> i32;
         pub fn gbs_version() -> *const c_char;
@@ -265,12 +265,13 @@ pub fn spec_verify_workspace_bytes(n_seq: usize, width: usize, vocab: usize) -> 
 }
 
 /// Speculative verification by rejection, exact in integer masses: n_seq sequences of `width` drafts and one bonus row
-/// (f32 target and draft logits `[n_seq * (width + 1), vocab]`).
-pub unsafe fn spec_verify(target: *const f32, draft: *const f32, n_seq: usize, width: usize, vocab: usize, draft_ids: *const i32,
+/// (f32 target and draft logits `[n_seq * (width + 1), stride]`, columns `[0, vocab)` read).
+pub unsafe fn spec_verify(target: *const f32, draft: *const f32, n_seq: usize, width: usize, vocab: usize, stride: usize,
+                          draft_ids: *const i32,
                           temperatures: *const f32, u_accept: *const f32, u_resample: *const f32, out_accepted: *mut i32,
                           out_tokens: *mut i32, out_status: *mut i32, ws: *mut c_void, ws_bytes: usize,
                           stream: *mut c_void) -> Result<(), GbsError> {
-    GbsError::check(ffi::gbs_spec_verify(target, draft, i(n_seq)?, i(width)?, i(vocab)?, draft_ids, temperatures, u_accept, u_resample,
+    GbsError::check(ffi::gbs_spec_verify(target, draft, i(n_seq)?, i(width)?, i(vocab)?, i(stride)?, draft_ids, temperatures, u_accept, u_resample,
                                          out_accepted, out_tokens, out_status, ws, ws_bytes, stream))
 }
 

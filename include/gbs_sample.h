@@ -294,8 +294,9 @@ int gbs_sample_rows_noalloc(const void* logits, int dtype, int rows, int stride,
 
 /*
  * Speculative verification by rejection (Leviathan et al. 2023 / Chen et al. 2023), exact in integer masses.
- * n_seq sequences of `width` drafts + 1 bonus row: target and draft f32 logits [n_seq * (width + 1), vocab] (row
- * s * (width + 1) + j; draft rows j == width are not read); draft_ids i32 [n_seq, width]; temperatures f32
+ * n_seq sequences of `width` drafts + 1 bonus row: target and draft f32 logits [n_seq * (width + 1), stride], columns
+ * [0, vocab) read, stride >= vocab (row s * (width + 1) + j; draft rows j == width are not read); draft_ids i32
+ * [n_seq, width]; temperatures f32
  * [n_seq * (width + 1)]; u_accept f32 [n_seq, width] and u_resample f32 [n_seq], all in [0, 1).
  * Draft j is accepted iff u_accept * q(x) < p(x), p and q the softmax at the row's temperature (temperature 0: x must be
  * the target's argmax). At the first rejection the token is drawn from max(p - q, 0) (the target's argmax at
@@ -304,7 +305,7 @@ int gbs_sample_rows_noalloc(const void* logits, int dtype, int rows, int stride,
  * out_status i32 [n_seq] (may be NULL). Workspace: gbs_spec_verify_workspace_bytes(n_seq, width, vocab), zeroed once.
  */
 size_t gbs_spec_verify_workspace_bytes(int n_seq, int width, int vocab);
-int gbs_spec_verify(const float* target, const float* draft, int n_seq, int width, int vocab, const int* draft_ids,
+int gbs_spec_verify(const float* target, const float* draft, int n_seq, int width, int vocab, int stride, const int* draft_ids,
                     const float* temperatures, const float* u_accept, const float* u_resample, int* out_accepted,
                     int* out_tokens, int* out_status, void* ws, size_t ws_bytes, void* stream);
 

@@ -287,14 +287,14 @@ __device__ __forceinline__ u128 load_u128(const u128* p) {
 }
 
 // ---- launch 1: maxima ----
-__global__ void __launch_bounds__(NT) spec_max_k(const float* __restrict__ target, const float* __restrict__ draft, int width, int vocab,
+__global__ void __launch_bounds__(NT) spec_max_k(const float* __restrict__ target, const float* __restrict__ draft, int width, int vocab, long long stride,
                                                  int chunk, bool vec, SpecWs ws) {
     __shared__ u64 s_red[NT];
     __shared__ unsigned s_flag;
     const int S = gridDim.x, sp = blockIdx.x, r = blockIdx.y;
     const bool has_draft = (r % (width + 1)) < width;
-    const float* tr = target + (size_t)r * vocab;
-    const float* dr = draft + (size_t)r * vocab;
+    const float* tr = target + (size_t)r * (size_t)stride;
+    const float* dr = draft + (size_t)r * (size_t)stride;
     const int lo = sp * chunk, hi = min(vocab, lo + chunk);
     // per thread: the largest value and its first index (elements arrive in ascending index order, and a strict > keeps
     // the first of equal values, -0 and +0 included); NaN and -inf never replace -inf
@@ -345,7 +345,7 @@ __device__ __forceinline__ bool accept_test(float u, u128 a, u128 b) { return mu
 __device__ __forceinline__ float key_value(u64 k) { return okey_to_f32(key_ok(k)); }
 
 // The sequence's decisions, by the block that completes the sequence's last row (all its rows' records are written).
-__device__ void decide_sequence(int seq, int width, int vocab, const float* __restrict__ target, const float* __restrict__ draft,
+__device__ void decide_sequence(int seq, int width, int vocab, long long stride, const float* __restrict__ target, const float* __restrict__ draft,
                                 const int* __restrict__ draft_ids, const float* __restrict__ temps, const float* __restrict__ u_accept,
                                 const float* __restrict__ u_resample, SpecWs ws) {
     const int W1 = width + 1;
@@ -373,7 +373,7 @@ __device__ void decide_sequence(int seq, int width, int vocab, const float* __re
                 if (Tj == 0.0f) acc = x == (int)key_id(ri.tkey);
                 else {
                     const float cj = temp_scale(Tj);
-                    const float tx = target[(size_t)(r0 + j) * vocab + x], dx = draft[(size_t)(r0 + j) * vocab + x];
+                    const float tx = target[(size_t)(r0 + j) * (size_t)stride + x], dx = draft[(size_t)(r0 + j) * (size_t)stride + x];
                     const u64 ep = tx > -INFINITY ? mass(tx, key_value(ri.tkey), cj) : 0ull;
                     const u64 eq = dx > -INFINITY ? mass(dx, key_value(ri.dkey), cj) : 0ull;
                     acc = accept_test(u, (u128)eq * ri.zp, (u128)ep * ri.zq);
@@ -418,7 +418,7 @@ __device__ void decide_sequence(int seq, int width, int vocab, const float* __re
 }
 
 // ---- launch 2: mass sums, then the sequence's acceptances ----
-__global__ void __launch_bounds__(NT) spec_mass_k(const float* __restrict__ target, const float* __restrict__ draft, int width, int vocab,
+__global__ void __launch_bounds__(NT) spec_mass_k(const float* __restrict__ target, const float* __restrict__ draft, int width, int vocab, long long stride,
                                                   int chunk, bool vec, const int* __restrict__ draft_ids, const float* __restrict__ temps,
                                                   const float* __restrict__ u_accept, const float* __restrict__ u_resample, SpecWs ws) {
     __shared__ u64 s_red[NT];
@@ -432,8 +432,8 @@ __global__ void __launch_bounds__(NT) spec_mass_k(const float* __restrict__ targ
     const RowInfo info = load_row_uniform(ws.rows, r);
     const float Mp = key_value(info.tkey), Mq = key_value(info.dkey);
     const float c2 = draw ? temp_scale(T) : 0.0f;
-    const float* tr = target + (size_t)r * vocab;
-    const float* dr = draft + (size_t)r * vocab;
+    const float* tr = target + (size_t)r * (size_t)stride;
+    const float* dr = draft + (size_t)r * (size_t)stride;
     const int lo = sp * chunk, hi = min(vocab, lo + chunk);
     u64 zp = 0, zq = 0;
     if (draw && info.tkey != 0ull && !info.nan) {
@@ -473,7 +473,7 @@ __global__ void __launch_bounds__(NT) spec_mass_k(const float* __restrict__ targ
         }
     }
     if (!arrive_last(&ws.seq_counters[seq], (unsigned)W1, &s_flag)) return;
-    decide_sequence(seq, width, vocab, target, draft, draft_ids, temps, u_accept, u_resample, ws);
+    decide_sequence(seq, width, vocab, stride, target, draft, draft_ids, temps, u_accept, u_resample, ws);
 }
 
 // the mass of a token of logit l in a row of maximum M; FAST: mass_fast's preconditions hold for the row
@@ -546,7 +546,7 @@ __device__ __forceinline__ u64 block_sum_u64(u64 v, u64* s) {
     return r;
 }
 
-__global__ void __launch_bounds__(RNT) spec_rows_k(const float* __restrict__ target, const float* __restrict__ draft, int width, int vocab,
+__global__ void __launch_bounds__(RNT) spec_rows_k(const float* __restrict__ target, const float* __restrict__ draft, int width, int vocab, long long stride,
                                                    bool vec, const int* __restrict__ draft_ids, const float* __restrict__ temps,
                                                    const float* __restrict__ u_accept, const float* __restrict__ u_resample, SpecWs ws) {
     __shared__ u64 s_red[RNT / WAVE];
@@ -555,8 +555,8 @@ __global__ void __launch_bounds__(RNT) spec_rows_k(const float* __restrict__ tar
     const int W1 = width + 1;
     const int seq = r / W1;
     const bool has_draft = (r % W1) < width;
-    const float* tr = target + (size_t)r * vocab;
-    const float* dr = draft + (size_t)r * vocab;
+    const float* tr = target + (size_t)r * (size_t)stride;
+    const float* dr = draft + (size_t)r * (size_t)stride;
     // forward: per thread the largest value and its first index (elements arrive in ascending index order per thread,
     // and a strict > keeps the first of equal values, -0 and +0 included); NaN and -inf never replace -inf
     float tm = -INFINITY, dm = -INFINITY;
@@ -602,7 +602,7 @@ __global__ void __launch_bounds__(RNT) spec_rows_k(const float* __restrict__ tar
         st_agent(&ws.rows[r].nan, nan ? 1u : 0u);
     }
     if (!arrive_last(&ws.seq_counters[seq], (unsigned)W1, &s_flag)) return;
-    decide_sequence(seq, width, vocab, target, draft, draft_ids, temps, u_accept, u_resample, ws);
+    decide_sequence(seq, width, vocab, stride, target, draft, draft_ids, temps, u_accept, u_resample, ws);
 }
 
 // inclusive prefix sum of a u128 over the wave
@@ -705,7 +705,7 @@ __device__ __forceinline__ void draw_tiles(const float* tr, const float* dr, int
     }
 }
 
-__global__ void __launch_bounds__(NT) spec_draw_k(const float* __restrict__ target, const float* __restrict__ draft, int width, int vocab,
+__global__ void __launch_bounds__(NT) spec_draw_k(const float* __restrict__ target, const float* __restrict__ draft, int width, int vocab, long long stride,
                                                   int tpb, bool vec, const int* __restrict__ draft_ids, const float* __restrict__ u_resample,
                                                   SpecWs ws, int* __restrict__ out_accepted, int* __restrict__ out_tokens,
                                                   int* __restrict__ out_status) {
@@ -719,8 +719,8 @@ __global__ void __launch_bounds__(NT) spec_draw_k(const float* __restrict__ targ
     const int nsub = tiles * DU * NWD;
     const SeqInfo si = load_seq(ws.seqs, seq);
     const bool drawing = si.status == GBS_ROW_OK && si.mode != 0;
-    const float* tr = target + (size_t)si.row * vocab;
-    const float* dr = draft + (size_t)si.row * vocab;
+    const float* tr = target + (size_t)si.row * (size_t)stride;
+    const float* dr = draft + (size_t)si.row * (size_t)stride;
     u128* wp = ws.wparts + (size_t)seq * nsub;
     const bool fast = mass_fast_ok(si.Mp, si.c2) && (si.mode == 2 || mass_fast_ok(si.Mq, si.c2));
     if (drawing) {
@@ -803,10 +803,10 @@ GBS_EXPORT size_t gbs_spec_verify_workspace_bytes(int n_seq, int width, int voca
     return plan(n_seq, width, vocab).bytes;
 }
 
-GBS_EXPORT int gbs_spec_verify(const float* target, const float* draft, int n_seq, int width, int vocab, const int* draft_ids,
-                               const float* temperatures, const float* u_accept, const float* u_resample, int* out_accepted,
-                               int* out_tokens, int* out_status, void* ws, size_t ws_bytes, void* stream) {
-    if (n_seq < 0 || width < 0 || vocab <= 0 || vocab > GBS_MAX_VOCAB) return GBS_ERR_INVALID;
+GBS_EXPORT int gbs_spec_verify(const float* target, const float* draft, int n_seq, int width, int vocab, int stride,
+                               const int* draft_ids, const float* temperatures, const float* u_accept, const float* u_resample,
+                               int* out_accepted, int* out_tokens, int* out_status, void* ws, size_t ws_bytes, void* stream) {
+    if (n_seq < 0 || width < 0 || vocab <= 0 || vocab > GBS_MAX_VOCAB || stride < vocab) return GBS_ERR_INVALID;
     if (n_seq == 0) return 0;
     if (!target || !temperatures || !u_resample || !out_accepted || !out_tokens || !ws || !aligned(ws, 256)) return GBS_ERR_INVALID;
     if (width > 0 && (!draft || !draft_ids || !u_accept)) return GBS_ERR_INVALID;
@@ -816,23 +816,24 @@ GBS_EXPORT int gbs_spec_verify(const float* target, const float* draft, int n_se
     const hipStream_t st = to_stream(stream);
     const int chunk = chunk_for(vocab, p.S);
     const float* dr = width > 0 ? draft : target;
-    const bool vec = vocab % 4 == 0 && aligned(target, 16) && aligned(dr, 16);
+    const bool vec = vocab % 4 == 0 && stride % 4 == 0 && aligned(target, 16) && aligned(dr, 16);
+    const long long ld = stride;
     int rc;
     if (p.R >= ROWS_KERNEL_MIN) {
-        hipLaunchKernelGGL(spec_rows_k, dim3(p.R), dim3(RNT), 0, st, target, dr, width, vocab, vec, draft_ids, temperatures, u_accept,
+        hipLaunchKernelGGL(spec_rows_k, dim3(p.R), dim3(RNT), 0, st, target, dr, width, vocab, ld, vec, draft_ids, temperatures, u_accept,
                            u_resample, w);
         rc = launch_status();
         if (rc) return rc;
     } else {
-        hipLaunchKernelGGL(spec_max_k, dim3(p.S, p.R), dim3(NT), 0, st, target, dr, width, vocab, chunk, vec, w);
+        hipLaunchKernelGGL(spec_max_k, dim3(p.S, p.R), dim3(NT), 0, st, target, dr, width, vocab, ld, chunk, vec, w);
         rc = launch_status();
         if (rc) return rc;
-        hipLaunchKernelGGL(spec_mass_k, dim3(p.S, p.R), dim3(NT), 0, st, target, dr, width, vocab, chunk, vec, draft_ids, temperatures,
+        hipLaunchKernelGGL(spec_mass_k, dim3(p.S, p.R), dim3(NT), 0, st, target, dr, width, vocab, ld, chunk, vec, draft_ids, temperatures,
                            u_accept, u_resample, w);
         rc = launch_status();
         if (rc) return rc;
     }
-    hipLaunchKernelGGL(spec_draw_k, dim3(p.S3, n_seq), dim3(NT), 0, st, target, dr, width, vocab, p.tpb, vec, draft_ids, u_resample, w,
+    hipLaunchKernelGGL(spec_draw_k, dim3(p.S3, n_seq), dim3(NT), 0, st, target, dr, width, vocab, ld, p.tpb, vec, draft_ids, u_resample, w,
                        out_accepted, out_tokens, out_status);
     return launch_status();
 }

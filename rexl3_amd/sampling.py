@@ -406,16 +406,28 @@ def sample_rows(logits: torch.Tensor, params: np.ndarray | torch.Tensor, uniform
 
 
 def spec_verify(target: torch.Tensor, draft: torch.Tensor, draft_ids: torch.Tensor, temperatures: torch.Tensor,
-                u_accept: torch.Tensor, u_resample: torch.Tensor):
-    """gbs_spec_verify: (accepted int32 [n_seq], tokens int32 [n_seq, width + 1], status int32 [n_seq])."""
+                u_accept: torch.Tensor, u_resample: torch.Tensor, vocab: int | None = None):
+    """gbs_spec_verify over f32 target / draft rows [n_seq * (width + 1), stride] (the same row stride for both, which may
+    exceed `vocab`: columns past it are never read): (accepted int32 [n_seq], tokens int32 [n_seq, width + 1], status
+    int32 [n_seq])."""
+    _require_cuda(target, "target")
     n_seq, width = draft_ids.shape
-    vocab = target.shape[-1]
+    rows, stride = target.shape
+    vocab = stride if vocab is None else vocab
     dev = target.device
+    if (target.dtype != torch.float32 or draft.dtype != torch.float32 or target.stride(1) != 1 or draft.stride(1) != 1
+            or tuple(draft.shape) != (rows, stride) or draft.stride(0) != target.stride(0) or not 0 < vocab <= stride
+            or rows != n_seq * (width + 1)):
+        raise ValueError("target and draft must be f32 [n_seq * (width + 1), stride] rows with one row stride and vocab <= stride")
+    _check(draft_ids, "draft_ids", torch.int32, (n_seq, width), dev)
+    _check(temperatures, "temperatures", torch.float32, (rows,), dev)
+    _check(u_accept, "u_accept", torch.float32, (n_seq, width), dev)
+    _check(u_resample, "u_resample", torch.float32, (n_seq,), dev)
     acc = torch.empty(n_seq, dtype=torch.int32, device=dev)
     toks = torch.empty((n_seq, width + 1), dtype=torch.int32, device=dev)
     st = torch.empty(n_seq, dtype=torch.int32, device=dev)
     wsb = _lib.load().gbs_spec_verify_workspace_bytes(n_seq, width, vocab)
     ws = WORKSPACE.get(dev, "spec", wsb)
-    _lib.call("gbs_spec_verify", _ptr(target), _ptr(draft), n_seq, width, vocab, _ptr(draft_ids), _ptr(temperatures), _ptr(u_accept),
-              _ptr(u_resample), _ptr(acc), _ptr(toks), _ptr(st), _ptr(ws), ws.numel(), _stream(dev))
+    _lib.call("gbs_spec_verify", _ptr(target), _ptr(draft), n_seq, width, vocab, target.stride(0), _ptr(draft_ids), _ptr(temperatures),
+              _ptr(u_accept), _ptr(u_resample), _ptr(acc), _ptr(toks), _ptr(st), _ptr(ws), ws.numel(), _stream(dev))
     return acc, toks, st

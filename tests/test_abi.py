@@ -80,7 +80,8 @@ def test_argument_checks_refuse_before_touching_memory():
     assert lib.gbs_sample_rows(n, 3, 1, 100, 100, n, n, n, n, 8, n, n, n, n, n, n, 0, n) == 1  # no dtype 3
     assert lib.gbs_sample_rows(n, 0, 1, 100, 100, n, n, n, n, -2, n, n, n, n, n, n, 0, n) == 1  # kmax below GBS_KMAX_MIXED
     assert lib.gbs_sample_rows(n, 0, 0, 100, 100, n, n, n, n, 8, n, n, n, n, n, n, 0, n) == 0
-    assert lib.gbs_spec_verify(n, n, 1, 7, 524289, n, n, n, n, n, n, n, n, 0, n) == 1
+    assert lib.gbs_spec_verify(n, n, 1, 7, 524289, 524289, n, n, n, n, n, n, n, n, 0, n) == 1
+    assert lib.gbs_spec_verify(n, n, 1, 7, 1000, 999, n, n, n, n, n, n, n, n, 0, n) == 1  # stride below vocab
     assert lib.gbs_accept(n, n, -1, 3, n, n) == 1
     assert lib.gbs_accept_tree(n, n, n, 1, 0, n, n, n) == 1
     assert lib.gbs_workspace_clear(n, 0, n) == 0

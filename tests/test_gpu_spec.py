@@ -116,3 +116,27 @@ def test_spec_zero_residual_draws_target_argmax():
     (a, t, s), (wa, wt, ws) = run(cfg)
     assert list(wa[:4]) == [0, 0, 0, 0]
     assert np.array_equal(s, ws) and np.array_equal(a, wa) and np.array_equal(t, wt)
+
+
+@pytest.mark.parametrize("n_seq,vocab,pad", [(8, 3001, 7), (32, 2048, 64)])
+def test_padded_rows(n_seq, vocab, pad):
+    """Target and draft rows with a row stride above `vocab` (the lm_head's padded layout): the pad columns hold NaN and
+    +inf, which must never be read; the results equal the oracle's on the unpadded rows. 32 sequences take the
+    one-block-per-row kernel, 8 the split kernels."""
+    need_gpu()
+    cfg = W.config5(seed=31 + n_seq, n_seq=n_seq, width=7, vocab=vocab)
+    R = cfg["target"].shape[0]
+    tp = np.full((R, vocab + pad), np.nan, np.float32)
+    dp = np.full((R, vocab + pad), np.inf, np.float32)
+    tp[:, vocab + 1::2] = np.inf
+    tp[:, :vocab] = cfg["target"]
+    dp[:, :vocab] = cfg["draft"]
+    log(f"padded spec rows n_seq={n_seq} vocab={vocab} stride={vocab + pad}")
+    acc, toks, st = S.spec_verify(dev(tp), dev(dp), dev(cfg["draft_ids"]), dev(cfg["temperatures"]), dev(cfg["u_accept"]),
+                                  dev(cfg["u_resample"]), vocab=vocab)
+    wa, wt, ws = O.spec_verify(cfg["target"], cfg["draft"], n_seq, 7, cfg["draft_ids"], cfg["temperatures"], cfg["u_accept"],
+                               cfg["u_resample"], threads=8)
+    assert np.array_equal(host(st), ws) and np.array_equal(host(acc), wa) and np.array_equal(host(toks), wt)
+    with pytest.raises(ValueError):
+        S.spec_verify(dev(tp), dev(dp[:, :vocab].copy()), dev(cfg["draft_ids"]), dev(cfg["temperatures"]),
+                      dev(cfg["u_accept"]), dev(cfg["u_resample"]), vocab=vocab)
