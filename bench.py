@@ -153,8 +153,13 @@ def measure(wl, args, steps, cpu_seconds, dev, lib, stream):
         ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
         lib.gbs_workspace_clear(ws.data_ptr(), wsb, stream)
         P = lambda t: None if t is None else C.c_void_p(t.data_ptr())  # noqa: E731
+        # log-probabilities are part of the north star's pipeline (its log-softmax); configs 1-4 ask for the token, its
+        # probability and the greedy id only
+        want_lp = wl in ("northstar", "mixed")
+        outputs = "ids, greedy, status, probs" + (", logprobs" if want_lp else "")
         argvs = [(P(xts[i]), 1 if is_bf16 else 0, rows, vocab, vocab, P(cts[i]), P(mts[i]), P(pt), P(ut), kmax, P(out["ids"]),
-                  P(out["greedy"]), P(out["probs"]), P(out["logprobs"]), P(out["status"]), P(ws), wsb, stream) for i in range(ncopy)]
+                  P(out["greedy"]), P(out["probs"]), P(out["logprobs"]) if want_lp else None, P(out["status"]), P(ws), wsb, stream)
+                 for i in range(ncopy)]
         fn = lib.gbs_sample_rows
         turn = [0]
 
@@ -327,8 +332,9 @@ def measure(wl, args, steps, cpu_seconds, dev, lib, stream):
         raise SystemExit(f"unknown workload {wl}")
     achieved = nbytes / (ms / 1e3) / 1e9
     ncopy = locals().get("ncopy", 1)
+    outputs = locals().get("outputs")
     return dict(name=wl, workload=workload, kernel=kernel, dtype=dtype, rows=rows, vocab=vocab, steps=steps, ms=ms, copies=ncopy,
-                rows_per_s=rows / (ms / 1e3), bytes=nbytes, achieved=achieved, cpu=cpu)
+                rows_per_s=rows / (ms / 1e3), bytes=nbytes, achieved=achieved, cpu=cpu, outputs=outputs)
 
 
 def main():
@@ -360,7 +366,7 @@ def main():
             print(f"# per-config {wl}", file=sys.stderr, flush=True)
             q = measure(wl, args, args.per_config_steps, args.per_config_cpu_seconds, dev, lib, stream)
             per_config[wl] = {"workload": q["workload"], "kernel": q["kernel"], "rows": q["rows"], "vocab": q["vocab"],
-                              "input_copies": q["copies"],
+                              "input_copies": q["copies"], **({"outputs": q["outputs"]} if q["outputs"] else {}),
                               "steps": q["steps"], "ms_per_step": round(q["ms"], 5), "rows_per_s": round(q["rows_per_s"], 1),
                               "bytes_per_launch": q["bytes"], "achieved_gbps": round(q["achieved"], 1),
                               "frac": round(q["achieved"] / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(wl),
