@@ -340,16 +340,22 @@ struct WaveTop {
         if (top_n > 2 * WAVE) s_top = nullptr;
     }
 
-    // raise the gate to the block bound of the published values (all lanes of the wave call it)
+    // raise the gate to the block bound of the published values (all lanes of the wave call it): the count-th largest
+    // published value, by one wave sort when they fit one per lane, else by a bitwise search of the counts
     __device__ __forceinline__ void block_bound() {
         const int l = lane_id();
         const u32 v0 = l < top_n ? s_top[l] : 0u;
-        const u32 v1 = l + WAVE < top_n ? s_top[l + WAVE] : 0u;
         u32 r = 0;
+        if (top_n <= WAVE) {
+            const u64 sv = wave_sort_desc(((u64)v0 << 32) | (u64)l);
+            r = count <= WAVE ? (u32)(readlane64(sv, count - 1) >> 32) : 0u;
+        } else {
+            const u32 v1 = l + WAVE < top_n ? s_top[l + WAVE] : 0u;
 #pragma unroll
-        for (int b = 31; b >= 0; --b) {
-            const u32 c = r | (1u << b);
-            if (__popcll(ballot(v0 >= c)) + __popcll(ballot(v1 >= c)) >= count) r = c;
+            for (int b = 31; b >= 0; --b) {
+                const u32 c = r | (1u << b);
+                if (__popcll(ballot(v0 >= c)) + __popcll(ballot(v1 >= c)) >= count) r = c;
+            }
         }
         if (r > 0u) {
             const u64 t = ((u64)r << 32) - 1ull;
@@ -570,13 +576,16 @@ __device__ __forceinline__ u64 block_tree_merge(u64 acc, u64 (*s_list)[WAVE]) {
 template <int NW>
 __device__ __forceinline__ u64 block_merge_lists(const u64* lists, int nl, u64 (*s_list)[WAVE]) {
     const int w = threadIdx.x / WAVE, l = lane_id();
-    u64 acc = 0;
-    u64 nxt = w < nl ? ld_agent(&lists[(size_t)w * WAVE + l]) : 0ull;
-    for (int o = w; o < nl; o += NW) {
-        const u64 cur = nxt;
-        nxt = o + NW < nl ? ld_agent(&lists[(size_t)(o + NW) * WAVE + l]) : 0ull;
-        acc = wave_merge_desc(acc, cur);
-    }
+    // wave w's first four lists (w, w + NW, ...) are loaded at once, further ones one ahead of their merge
+    constexpr int PRE = 4;
+    u64 v[PRE];
+#pragma unroll
+    for (int k = 0; k < PRE; ++k) v[k] = w + k * NW < nl ? ld_agent(&lists[(size_t)(w + k * NW) * WAVE + l]) : 0ull;
+    u64 acc = v[0];
+#pragma unroll
+    for (int k = 1; k < PRE; ++k)
+        if (w + k * NW < nl) acc = wave_merge_desc(acc, v[k]);
+    for (int o = w + PRE * NW; o < nl; o += NW) acc = wave_merge_desc(acc, ld_agent(&lists[(size_t)o * WAVE + l]));
     __syncthreads();
     return block_tree_merge<NW>(acc, s_list);
 }
