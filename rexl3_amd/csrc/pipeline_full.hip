@@ -45,19 +45,21 @@ struct Row {
 
     // Raw loads of one 4-element group, for the pipelined streaming of whole rows (vec rows only): buffer loads whose
     // range check returns zeros past the row's end, so nothing waits on a bounds test before the loads are issued.
+    // AUX: the logits' and counts' cache policy (2: non-temporal); mask words, shared by 32 elements, use the default.
     struct Raw {
         u32x4 x;  // f32: 4 values; bf16: the first two words
         u32x4 c;
         u32 m;
     };
+    template <int AUX = 0>
     __device__ __forceinline__ void load_raw(int e, const __amdgpu_buffer_rsrc_t& rx, const __amdgpu_buffer_rsrc_t& rc,
                                              const __amdgpu_buffer_rsrc_t& rm, Raw& w) const {
-        if (DT == GBS_DTYPE_F32) w.x = __builtin_amdgcn_raw_buffer_load_b128(rx, (u32)e * 4u, 0, 0);
+        if (DT == GBS_DTYPE_F32) w.x = __builtin_amdgcn_raw_buffer_load_b128(rx, (u32)e * 4u, 0, AUX);
         else {
-            const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rx, (u32)e * 2u, 0, 0);
+            const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rx, (u32)e * 2u, 0, AUX);
             w.x = u32x4{v.x, v.y, 0u, 0u};
         }
-        if (COUNTS) w.c = __builtin_amdgcn_raw_buffer_load_b128(rc, (u32)e * 4u, 0, 0);
+        if (COUNTS) w.c = __builtin_amdgcn_raw_buffer_load_b128(rc, (u32)e * 4u, 0, AUX);
         if (MASK) w.m = __builtin_amdgcn_raw_buffer_load_b32(rm, (u32)(e >> 5) * 4u, 0, 0);
     }
     // the penalised, masked logits of a raw group at e (out of range: -inf)
@@ -143,8 +145,14 @@ struct Pass0Acc {
     __device__ __forceinline__ u64 key() const { return bv > -INFINITY ? make_key(okey_f32(bv), bid) : 0ull; }
 };
 
+// A buffer resource over [base, base + bytes). Both are the same on every lane (a row's), made visibly uniform so that
+// the loads take the resource from scalar registers without a loop over lanes.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t full_rsrc(const void* base, u32 bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+    const u64 a = (u64)(uintptr_t)base;
+    const u64 ua = ((u64)(u32)__builtin_amdgcn_readfirstlane((int)(u32)(a >> 32)) << 32) |
+                   (u64)(u32)__builtin_amdgcn_readfirstlane((int)(u32)a);
+    const int ub = __builtin_amdgcn_readfirstlane((int)bytes);
+    return __builtin_amdgcn_make_buffer_rsrc((void*)(uintptr_t)ua, (short)0, ub, 0x00020000);
 }
 
 // Streams the row tile by tile (tile t: elements [t * TILE, (t + 1) * TILE), thread tid the group at t * TILE + 4 tid),
@@ -189,19 +197,112 @@ __device__ __forceinline__ void stream_tiles(const Row<DT, COUNTS, MASK>& R, int
     }
 }
 
+// Streams tiles [t0, t1) in wave-steps: step k covers elements [t0 * TILE + k * WS, + WS), WS = G * 256, and wave w
+// takes steps w, w + NWF, ... (lane l's group j at + j * 256 + 4 l); the next step's G groups per lane are in flight
+// while a step is processed. The loads are issued whether or not their step exists (a step past the block's
+// last reads at an offset past the row's end, which the buffer range check turns into zeros without a memory access),
+// so every wait counts exactly the loads issued after the buffer it needs. f(t, e, l) is called per group and
+// fe(t, q) once per step (q: the step's place in its tile, below TILE / WS); f and fe must not hold block barriers.
+// pre() is called by every thread once the first step's loads are in flight, before any group is processed (it may
+// hold block barriers).
+#ifndef GBS_FS_STEPS
+#define GBS_FS_STEPS 1
+#endif
+#ifndef GBS_FS_AUX0
+#define GBS_FS_AUX0 2
+#endif
+#ifndef GBS_FS_AUXH
+#define GBS_FS_AUXH 2
+#endif
+#ifndef GBS_FS_AUXC
+#define GBS_FS_AUXC 2
+#endif
+#ifndef GBS_FS_STEP_GROUPS
+#define GBS_FS_STEP_GROUPS 2
+#endif
+constexpr int SG = GBS_FS_STEP_GROUPS;
+constexpr int STEPS_PER_TILE_MAX = NWF;  // TILE / 256: the steps of one group per lane
+template <int G, int AUX, int DT, bool COUNTS, bool MASK, class F, class FE, class FP>
+__device__ __forceinline__ void stream_steps(const Row<DT, COUNTS, MASK>& R, int t0, int t1, F&& f, FE&& fe, FP&& pre) {
+    static_assert(TILE % (G * 256) == 0, "whole steps per tile");
+    constexpr int WS = G * 256, SPT = TILE / WS;
+    const int w = (int)threadIdx.x / WAVE, l = lane_id();
+    if (!R.vec || R.vocab % 4 != 0) {  // one group per lane and step: wave w takes elements [w * 256, + 256) of each tile
+        pre();
+        for (int t = t0; t < t1; ++t) {
+            const int e = t * TILE + (int)threadIdx.x * 4;
+            float lv[4];
+            R.group(e, lv);
+            f(t, e, lv);
+            fe(t, w);
+        }
+        return;
+    }
+    const u32 esz = DT == GBS_DTYPE_F32 ? 4u : 2u;
+    const __amdgpu_buffer_rsrc_t rx = full_rsrc(R.x, (u32)R.vocab * esz);
+    const __amdgpu_buffer_rsrc_t rc = full_rsrc(R.c, COUNTS ? (u32)R.vocab * 4u : 0u);
+    const __amdgpu_buffer_rsrc_t rm = full_rsrc(R.m, MASK ? (u32)((R.vocab + 31) / 32) * 4u : 0u);
+    using Raw = typename Row<DT, COUNTS, MASK>::Raw;
+    const int nsteps = (t1 - t0) * SPT;
+    const int base = t0 * TILE + l * 4;
+    constexpr int PAST = 1 << 29;  // an element index whose offsets lie past any row (rows hold at most 2^25 elements)
+    auto load = [&](int k, Raw (&b)[G]) {
+        const int e0 = k < nsteps ? base + k * WS : PAST;
+#pragma unroll
+        for (int j = 0; j < G; ++j) R.template load_raw<AUX>(e0 + j * 256, rx, rc, rm, b[j]);
+    };
+    auto use = [&](int k, const Raw (&b)[G]) {
+        const int e0 = base + k * WS;
+        const int t = t0 + k / SPT;
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+            float lv[4];
+            R.from_raw(b[j], e0 + j * 256, lv);
+            f(t, e0 + j * 256, lv);
+        }
+        fe(t, k % SPT);
+    };
+    // one load site: the step's buffer is copied out once it has arrived, and the next step's loads go into it before
+    // the copy is used
+    Raw B[G];
+    int k = w;
+    load(k, B);
+    pre();
+    while (k < nsteps) {
+        Raw C[G];
+#pragma unroll
+        for (int j = 0; j < G; ++j) C[j] = B[j];
+        const int kn = k + NWF;
+        load(kn, B);
+        use(k, C);
+        k = kn;
+    }
+}
+
+template <int G, int AUX, int DT, bool COUNTS, bool MASK, class F, class FE>
+__device__ __forceinline__ void stream_steps(const Row<DT, COUNTS, MASK>& R, int t0, int t1, F&& f, FE&& fe) {
+    stream_steps<G, AUX>(R, t0, t1, f, fe, [] {});
+}
+
 // the whole row
 template <int DT, bool COUNTS, bool MASK, class F>
 __device__ __forceinline__ void stream_tiles(const Row<DT, COUNTS, MASK>& R, F&& f) {
     stream_tiles(R, 0, (R.vocab + TILE - 1) / TILE, f);
 }
 
+__device__ __forceinline__ u32 wave_sum_u32(u32 v) {
+#pragma unroll
+    for (int m = 1; m < WAVE; m <<= 1) v += xor_lane(v, m);
+    return v;
+}
+
+// block totals over all threads (cross-lane moves by DPP and permlane swaps, one LDS slot per wave); every thread
+// of the block calls them and receives the total
 template <typename T>
 __device__ __forceinline__ T block_sum(T v, T* s_red) {
     const int w = threadIdx.x / WAVE;
-    for (int m = 1; m < WAVE; m <<= 1) {
-        if constexpr (sizeof(T) == 8) v += shfl_xor64(v, m);
-        else v += (T)__shfl_xor((int)v, m, WAVE);
-    }
+    if constexpr (sizeof(T) == 8) v = (T)wave_sum_u64((u64)v);
+    else v = (T)wave_sum_u32((u32)v);
     __syncthreads();
     if (lane_id() == 0) s_red[w] = v;
     __syncthreads();
@@ -213,10 +314,7 @@ __device__ __forceinline__ T block_sum(T v, T* s_red) {
 
 __device__ __forceinline__ u64 block_max_u64(u64 v, u64* s_red) {
     const int w = threadIdx.x / WAVE;
-    for (int m = 1; m < WAVE; m <<= 1) {
-        const u64 o = shfl_xor64(v, m);
-        v = o > v ? o : v;
-    }
+    v = wave_max_u64(v);
     __syncthreads();
     if (lane_id() == 0) s_red[w] = v;
     __syncthreads();
@@ -233,6 +331,12 @@ constexpr int NUNITS = 52;
 constexpr int NBINS = NUNITS * BINS_PER_UNIT;
 constexpr int CAP = NB;  // collected tokens of the crossing bin (keys in sh.maxk, masses in sh.mass)
 
+// the bin of a token: min(floor(-128 y), NBINS - 1), y = (l - M) * c2 computed as the mass is
+__device__ __forceinline__ u32 bin_of(float l, float M, float c2) {
+    const float y = (l - M) * c2;
+    return (u32)fminf(-y * (float)BINS_PER_UNIT, (float)(NBINS - 1));
+}
+
 struct Shared {
     u32 cnt[NB];
     u64 mass[NBINS];  // the radix digits' masses (NB), or the binned cut's mass per bin (NBINS)
@@ -246,6 +350,93 @@ struct Shared {
 };
 
 static_assert(NBINS == (int)FS_NBINS, "the per-row record's bin count");
+
+// The exact top-p key among the n tokens collected from the crossing bin b* (keys and masses in LDS): the one key K
+// with above + G(K) < P <= above + G(K) + E(K), G(K) the mass of the collected keys larger than K (the crossing bin
+// holds the target: above < P <= above + its mass). The bin is split into NSUB sub-bins by the same y as the bin
+// (sub = floor(NSUB * (-128 y - b*)), clamped to the last; it never decreases as the value decreases, and equal values
+// share it); a mass histogram of the sub-bins gives the one holding the target, and only its tokens are compared with
+// each other. Every thread calls it; it returns the key on every thread. LDS: s_cnt holds the sub-bins' masses, then
+// the list of the crossing sub-bin's tokens.
+constexpr int NSUB = 256;
+constexpr u32 SUB_LIST_CAP = NB - 2 * NSUB;  // u32 slots of s_cnt after the sub-bins' masses
+__device__ u64 cut_collected(const u64* keys, const u64* masses, u32 n, u64 above, u64 P, float M, float c2, u32 bstar, u32* s_cnt,
+                             u64* s_bc) {
+    const int tid = threadIdx.x, l = lane_id();
+    u64* const s_sub = (u64*)s_cnt;
+    u32* const s_list = s_cnt + 2 * NSUB;
+    auto sub_of = [&](u64 key) {
+        const float y = (okey_to_f32(key_ok(key)) - M) * c2;
+        return (u32)fminf((-y * (float)BINS_PER_UNIT - (float)bstar) * (float)NSUB, (float)(NSUB - 1));
+    };
+    for (int i = tid; i < NSUB; i += NTF) s_sub[i] = 0;
+    if (tid == 0) {
+        s_bc[2] = 0;                        // tokens of the crossing sub-bin
+        s_bc[3] = (u64)VALID_MIN_OK << 32;  // the cut, if none were found (cannot happen)
+    }
+    __syncthreads();
+    for (u32 i = tid; i < n; i += NTF) atomicAdd((unsigned long long*)&s_sub[sub_of(keys[i])], (unsigned long long)masses[i]);
+    __syncthreads();
+    if (tid < WAVE) {
+        // lane i holds sub-bins 4i .. 4i + 3
+        u64 m4[4], tot = 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            m4[q] = s_sub[4 * l + q];
+            tot += m4[q];
+        }
+        const u64 incl = above + wave_scan_u64(tot);
+        const int f = (int)__builtin_ctzll(ballot(incl >= P) | (1ull << 63));
+        if (l == f) {
+            u64 acc = incl - tot;
+            int q = 0;
+#pragma unroll
+            for (int k = 0; k < 3; ++k) {
+                if (q == k && acc + m4[k] < P) {
+                    acc += m4[k];
+                    q = k + 1;
+                }
+            }
+            s_bc[0] = (u64)(4 * f + q);
+            s_bc[1] = acc;  // the mass above the crossing sub-bin
+        }
+    }
+    __syncthreads();
+    const u32 sstar = (u32)s_bc[0];
+    for (u32 i = tid; i < n; i += NTF) {
+        if (sub_of(keys[i]) == sstar) {
+            const u32 k = atomicAdd((unsigned*)&s_bc[2], 1u);
+            if (k < SUB_LIST_CAP) s_list[k] = i;
+        }
+    }
+    __syncthreads();
+    const u32 m = (u32)s_bc[2];
+    const u64 base = s_bc[1];
+    if (m <= SUB_LIST_CAP) {
+        for (u32 t = tid; t < m; t += NTF) {
+            const u32 i = s_list[t];
+            const u64 ki = keys[i];
+            u64 g = 0;
+            for (u32 u = 0; u < m; ++u) {
+                const u32 j = s_list[u];
+                g += keys[j] > ki ? masses[j] : 0ull;
+            }
+            if (base + g < P && P <= base + g + masses[i]) s_bc[3] = ki;
+        }
+    } else {  // more tokens in one sub-bin than the list holds (equal values): compare them over the whole collection
+        for (u32 i = tid; i < n; i += NTF) {
+            const u64 ki = keys[i];
+            if (sub_of(ki) != sstar) continue;
+            u64 g = 0;
+            for (u32 j = 0; j < n; ++j) g += (keys[j] > ki && sub_of(keys[j]) == sstar) ? masses[j] : 0ull;
+            if (base + g < P && P <= base + g + masses[i]) s_bc[3] = ki;
+        }
+    }
+    __syncthreads();
+    const u64 kp = s_bc[3];
+    __syncthreads();
+    return kp;
+}
 
 // One radix selection over the keys >= lb of the row: the key K at which the descending cumulative weight (count when
 // by_mass is false, mass otherwise) first reaches `target` -- weight(keys > K) < target <= weight(keys >= K).
@@ -348,10 +539,6 @@ __device__ u64 radix_select(const Row<DT, COUNTS, MASK>& R, float M, float c2, u
 // tile and collects the keys and masses of bin b*; sorting the collected keys gives the exact top-p key (the first
 // whose cumulative mass reaches P), and the kept ones of them are added to their tiles. Returns false (nothing kept
 // of its state) when bin b* holds more than CAP tokens: the caller takes the radix path.
-__device__ __forceinline__ u32 bin_of(float l, float M, float c2) {
-    const float y = (l - M) * c2;
-    return (u32)fminf(-y * (float)BINS_PER_UNIT, (float)(NBINS - 1));
-}
 
 template <int DT, bool COUNTS, bool MASK>
 __device__ bool binned_cut(const Row<DT, COUNTS, MASK>& R, float M, float c2, float top_p, u64 Q, u64* kp_out, Shared& sh) {
@@ -449,19 +636,8 @@ __device__ bool binned_cut(const Row<DT, COUNTS, MASK>& R, float M, float c2, fl
     if (n > (u32)CAP) return false;
     u64 kp = (u64)VALID_MIN_OK << 32;  // every valid key
     if (topp) {
-        // For each collected token i, G_i = the mass of the collected tokens with larger keys (every thread reads the
-        // same key at once: LDS broadcasts). The top-p key is the one token with above + G_i < P <= above + G_i + E_i.
-        if (tid == 0) sh.bc[3] = kp;
-        __syncthreads();
-        for (u32 i = tid; i < n; i += NTF) {
-            const u64 ki = sh.maxk[i];
-            u64 g = 0;
-            for (u32 j = 0; j < n; ++j) g += sh.maxk[j] > ki ? sh.mass[j] : 0ull;
-            const u64 lo = above + g;
-            if (lo < P && P <= lo + sh.mass[i]) sh.bc[3] = ki;
-        }
-        __syncthreads();
-        kp = sh.bc[3];
+        // the top-p key among the collected tokens of bin b*
+        kp = cut_collected(sh.maxk, sh.mass, n, above, P, M, c2, bstar, sh.cnt, sh.bc);
         // the kept tokens of bin b* (key >= the top-p key, mass >= Q) into their tiles
         for (u32 j = tid; j < n; j += NTF) {
             const u64 E = sh.mass[j];
@@ -474,7 +650,7 @@ __device__ bool binned_cut(const Row<DT, COUNTS, MASK>& R, float M, float c2, fl
 }
 
 template <int DT, bool COUNTS, bool MASK>
-__device__ __forceinline__ void full_row(const void* __restrict__ logits, long long stride, int vocab, const int* __restrict__ counts,
+__device__ __attribute__((noinline)) void full_row(const void* __restrict__ logits, long long stride, int vocab, const int* __restrict__ counts,
                                          const u32* __restrict__ mask, const RowParamsDev* __restrict__ params,
                                          const float* __restrict__ uniforms, bool vec, int* __restrict__ out_ids,
                                          int* __restrict__ out_greedy, float* __restrict__ out_probs, float* __restrict__ out_logprobs,
@@ -663,7 +839,10 @@ __global__ void __launch_bounds__(NTF) sample_full_k(const void* __restrict__ lo
 //                 tile that holds the draw, and the token. A row marked for the radix path is taken by its first block
 //                 (the single-block path, full_row), and so is a row whose crossing bin held more than CAP tokens, by its
 //                 last block.
-constexpr int FS_TARGET_BLOCKS = 256;
+#ifndef GBS_FS_TARGET_BLOCKS
+#define GBS_FS_TARGET_BLOCKS 256
+#endif
+constexpr int FS_TARGET_BLOCKS = GBS_FS_TARGET_BLOCKS;  // the split path's blocks (rows below the CU count)
 #ifndef GBS_FS_DEFER_BLOCKS
 #define GBS_FS_DEFER_BLOCKS 512
 #endif
@@ -800,122 +979,73 @@ __device__ int fs_row(const unsigned* __restrict__ flags, int rows, int rank, in
     return *s_row;
 }
 
+// Pass 0 of the split form: the block's maximum key, NaN flag, allowed count and log-sum-exp over its tiles, into
+// ws.p0[row][sp] (each wave's totals by cross-lane moves, then wave 0 over the waves': one barrier). fs_hist_k makes
+// the row's record from the S partials. Not launched under per-row dispatch.
 template <int DT, bool COUNTS, bool MASK>
 __global__ void __launch_bounds__(NTF) fs_pass0_k(const void* __restrict__ logits, long long stride, int vocab,
                                                   const int* __restrict__ counts, const u32* __restrict__ mask,
                                                   const RowParamsDev* __restrict__ params, const float* __restrict__ uniforms, bool vec,
-                                                  int tpb, FsWs ws, int* __restrict__ out_ids, int* __restrict__ out_greedy,
-                                                  float* __restrict__ out_probs, float* __restrict__ out_logprobs,
-                                                  int* __restrict__ out_status, const unsigned* __restrict__ flags, int rows) {
-    __shared__ u64 s_red[NWF];
+                                                  int tpb, FsWs ws) {
+    __shared__ u64 s_k[NWF];
+    __shared__ u32 s_nn[NWF], s_na[NWF];
     __shared__ float s_lm[NWF], s_ls[NWF];
-    __shared__ unsigned s_flag;
-    __shared__ int s_sel;
-    const int S = gridDim.x, sp = blockIdx.x, wr = blockIdx.y;  // wr: the row's place in the workspace
-    if (flags && wr >= DEFER_ROWS) return;  // flagged rows past the workspace's: fs_collect_k
-    const int r = flags ? fs_row(flags, rows, wr, &s_sel) : wr;
-    if (r < 0) return;
+    const int S = gridDim.x, sp = blockIdx.x, r = blockIdx.y;
     const int tid = threadIdx.x, w = tid / WAVE, l = lane_id();
     const RowParamsDev p = params[r];
-    const float u = uniforms[r];
-    if (params_invalid(p, u)) {  // every block of the row returns; the first writes the row's results
-        if (sp == 0 && tid == 0) {
-            fs_out(r, -1, -1, GBS_ROW_INVALID_PARAMS, 0.f, 0.f, out_ids, out_greedy, out_probs, out_logprobs, out_status);
-            st_agent(&ws.rows[r].state, (u32)FS_DONE);
-        }
-        return;
-    }
+    if (params_invalid(p, uniforms[r])) return;  // fs_hist_k writes the row's results
     const Row<DT, COUNTS, MASK> R = make_row<DT, COUNTS, MASK>(logits, stride, vocab, counts, mask, p, vec, r);
     const float clp = fs_clp(p);
     const int ntiles = (vocab + TILE - 1) / TILE;
     const int t0 = sp * tpb, t1 = min(ntiles, t0 + tpb);
     Pass0Acc acc;
+#if GBS_FS_STEPS
+    stream_steps<SG, GBS_FS_AUX0>(R, t0, t1, [&](int, int e, const float (&lv)[4]) { acc.add(lv, e, clp); }, [](int, int) {});
+#else
     stream_tiles(R, t0, t1, [&](int, int e, const float (&lv)[4]) { acc.add(lv, e, clp); });
-    const u64 kmaxv = acc.key();
-    const u32 nan = acc.nan, nallowed = acc.nallowed;
-    const Lse lse = wave_lse(acc.lse, clp);
+#endif
+    const u64 k = wave_max_u64(acc.key());
+    const u32 nn = wave_or(acc.nan), na = wave_sum_u32(acc.nallowed);
+    const Lse ls = wave_lse(acc.lse, clp);
     if (l == 0) {
-        s_lm[w] = lse.m;
-        s_ls[w] = lse.s;
+        s_k[w] = k;
+        s_nn[w] = nn;
+        s_na[w] = na;
+        s_lm[w] = ls.m;
+        s_ls[w] = ls.s;
     }
-    const u32 nan_any = (u32)block_sum((u64)nan, s_red);
-    const u64 nall = block_sum((u64)nallowed, s_red);
-    const u64 top = block_max_u64(kmaxv, s_red);
-    if (tid == 0) {
-        Lse b{-INFINITY, 0.f};
-        for (int o = 0; o < NWF; ++o) b = lse_merge(b, Lse{s_lm[o], s_ls[o]}, clp);
-        FsPart0* pp = &ws.p0[(size_t)wr * S + sp];
-        st_agent(&pp->key, top);
-        st_agent(&pp->nan, nan_any);
-        st_agent(&pp->nallowed, (u32)nall);
-        st_agent((u32*)&pp->m, __float_as_uint(b.m));
-        st_agent((u32*)&pp->s, __float_as_uint(b.s));
+    __syncthreads();
+    if (w != 0) return;
+    const bool in = l < NWF;
+    const u64 bk = wave_max_u64(in ? s_k[l] : 0ull);
+    const u32 bnn = wave_or(in ? s_nn[l] : 0u), bna = wave_sum_u32(in ? s_na[l] : 0u);
+    const Lse bl = wave_lse(in ? Lse{s_lm[l], s_ls[l]} : Lse{-INFINITY, 0.f}, clp);
+    if (l == 0) {
+        FsPart0* pp = &ws.p0[(size_t)r * S + sp];
+        st_agent(&pp->key, bk);
+        st_agent(&pp->nan, bnn);
+        st_agent(&pp->nallowed, bna);
+        st_agent((u32*)&pp->m, __float_as_uint(bl.m));
+        st_agent((u32*)&pp->s, __float_as_uint(bl.s));
     }
-    if (!arrive_last(&ws.cnt0[r], (unsigned)S, &s_flag)) return;
-    // the row: the blocks' partials (one per thread), reduced
-    u64 k = 0, na = 0, nn = 0;
-    Lse rl{-INFINITY, 0.f};
-    if (tid < S) {
-        const FsPart0* pp = &ws.p0[(size_t)wr * S + tid];
-        k = ld_agent(&pp->key);
-        nn = ld_agent(&pp->nan);
-        na = ld_agent(&pp->nallowed);
-        rl = Lse{__uint_as_float(ld_agent((const u32*)&pp->m)), __uint_as_float(ld_agent((const u32*)&pp->s))};
-    }
-    if (w == 0) {  // S <= 128: lanes hold two partials at most
-        if (tid + WAVE < S) {
-            const FsPart0* pp = &ws.p0[(size_t)wr * S + tid + WAVE];
-            const u64 k2 = ld_agent(&pp->key);
-            k = k2 > k ? k2 : k;
-            nn += ld_agent(&pp->nan);
-            na += ld_agent(&pp->nallowed);
-            rl = lse_merge(rl, Lse{__uint_as_float(ld_agent((const u32*)&pp->m)), __uint_as_float(ld_agent((const u32*)&pp->s))}, clp);
-        }
-        for (int m = 1; m < WAVE; m <<= 1) {
-            const u64 ko = shfl_xor64(k, m);
-            k = ko > k ? ko : k;
-            nn += shfl_xor64(nn, m);
-            na += shfl_xor64(na, m);
-            const Lse o{__shfl_xor(rl.m, m, WAVE), __shfl_xor(rl.s, m, WAVE)};
-            rl = lse_merge(rl, o, clp);
-        }
-    }
-    if (tid != 0) return;
-    FsRow* row = &ws.rows[r];
-    u32 state = FS_CUT;
-    const float M = okey_to_f32(key_ok(k));
-    const int greedy = (int)key_id(k);
-    if (nn) {
-        fs_out(r, -1, -1, GBS_ROW_NAN_LOGIT, 0.f, 0.f, out_ids, out_greedy, out_probs, out_logprobs, out_status);
-        state = FS_DONE;
-    } else if (na == 0) {
-        fs_out(r, -1, -1, GBS_ROW_NO_CANDIDATES, 0.f, 0.f, out_ids, out_greedy, out_probs, out_logprobs, out_status);
-        state = FS_DONE;
-    } else if (p.temperature == 0.0f) {
-        fs_out(r, greedy, greedy, GBS_ROW_OK, 1.0f, fs_logprob(M, M, clp, rl.m, rl.s), out_ids, out_greedy, out_probs, out_logprobs,
-               out_status);
-        state = FS_DONE;
-    } else {
-        const bool topk_on = p.top_k > 0 && (u64)p.top_k < na;
-        if (topk_on || !mass_fast_ok(M, temp_scale(p.temperature))) state = FS_RADIX;
-    }
-    st_agent(&row->top, k);
-    st_agent((u32*)&row->lse_m, __float_as_uint(rl.m));
-    st_agent((u32*)&row->lse_s, __float_as_uint(rl.s));
-    st_agent(&row->nallowed, (u32)na);
-    st_agent(&row->bstar, (u32)NBINS);
-    st_agent(&row->above, (u64)0);
-    st_agent(&row->P, (u64)0);
-    st_agent(&row->state, state);
 }
 
+// The row's record, then the binned cut's mass histogram of the block's tiles.
+//  - The record: without per-row dispatch every block of the row makes it from pass 0's S partials (one load per lane
+//    of wave 0); block 0 stores it and writes the results of the rows that need no cut (invalid, NaN, empty, T = 0),
+//    and marks the rows that need the radix path (top-k with a cut, an infinite maximum or 1/T). Under per-row
+//    dispatch the single-pass kernel has stored it.
+//  - The histogram (rows with top-p that continue the cut): the block's bins and its sums per unit of y go to the
+//    workspace, where fs_collect_k finds the crossing bin.
 template <int DT, bool COUNTS, bool MASK>
 __global__ void __launch_bounds__(NTF) fs_hist_k(const void* __restrict__ logits, long long stride, int vocab,
                                                  const int* __restrict__ counts, const u32* __restrict__ mask,
-                                                 const RowParamsDev* __restrict__ params, bool vec, int tpb, FsWs ws,
-                                                 const unsigned* __restrict__ flags, int rows) {
+                                                 const RowParamsDev* __restrict__ params, const float* __restrict__ uniforms, bool vec,
+                                                 int tpb, FsWs ws, int* __restrict__ out_ids, int* __restrict__ out_greedy,
+                                                 float* __restrict__ out_probs, float* __restrict__ out_logprobs,
+                                                 int* __restrict__ out_status, const unsigned* __restrict__ flags, int rows) {
     __shared__ u64 s_hist[NBINS];
-    __shared__ unsigned s_flag;
+    __shared__ u64 s_rec[2];  // the row's maximum key and state
     __shared__ int s_sel;
     const int S = gridDim.x, sp = blockIdx.x, wr = blockIdx.y;
     if (flags && wr >= DEFER_ROWS) return;
@@ -923,22 +1053,87 @@ __global__ void __launch_bounds__(NTF) fs_hist_k(const void* __restrict__ logits
     if (r < 0) return;
     const int tid = threadIdx.x, l = lane_id();
     const RowParamsDev p = params[r];
+    FsRow* row = &ws.rows[r];
+    u64 top;
+    if (!flags) {
+        if (params_invalid(p, uniforms[r])) {
+            if (sp == 0 && tid == 0) {
+                fs_out(r, -1, -1, GBS_ROW_INVALID_PARAMS, 0.f, 0.f, out_ids, out_greedy, out_probs, out_logprobs, out_status);
+                st_agent(&row->state, (u32)FS_DONE);
+            }
+            return;
+        }
+        if (tid < WAVE) {
+            const float clp = fs_clp(p);
+            u64 k = 0;
+            u32 nn = 0, na = 0;
+            Lse rl{-INFINITY, 0.f};
+            for (int o = l; o < S; o += WAVE) {
+                const FsPart0* pp = &ws.p0[(size_t)wr * S + o];
+                const u64 k2 = ld_agent(&pp->key);
+                k = k2 > k ? k2 : k;
+                nn |= ld_agent(&pp->nan);
+                na += ld_agent(&pp->nallowed);
+                rl = lse_merge(rl, Lse{__uint_as_float(ld_agent((const u32*)&pp->m)), __uint_as_float(ld_agent((const u32*)&pp->s))}, clp);
+            }
+            k = wave_max_u64(k);
+            nn = wave_or(nn);
+            na = wave_sum_u32(na);
+            rl = wave_lse(rl, clp);
+            u32 state = FS_CUT;
+            const float M = okey_to_f32(key_ok(k));
+            const int greedy = (int)key_id(k);
+            if (nn || na == 0 || p.temperature == 0.0f) state = FS_DONE;
+            else if ((p.top_k > 0 && (u32)p.top_k < na) || !mass_fast_ok(M, temp_scale(p.temperature))) state = FS_RADIX;
+            if (l == 0) {
+                s_rec[0] = k;
+                s_rec[1] = state;
+                if (sp == 0) {
+                    if (nn)
+                        fs_out(r, -1, -1, GBS_ROW_NAN_LOGIT, 0.f, 0.f, out_ids, out_greedy, out_probs, out_logprobs, out_status);
+                    else if (na == 0)
+                        fs_out(r, -1, -1, GBS_ROW_NO_CANDIDATES, 0.f, 0.f, out_ids, out_greedy, out_probs, out_logprobs, out_status);
+                    else if (p.temperature == 0.0f)
+                        fs_out(r, greedy, greedy, GBS_ROW_OK, 1.0f, fs_logprob(M, M, clp, rl.m, rl.s), out_ids, out_greedy, out_probs,
+                               out_logprobs, out_status);
+                    st_agent(&row->top, k);
+                    st_agent((u32*)&row->lse_m, __float_as_uint(rl.m));
+                    st_agent((u32*)&row->lse_s, __float_as_uint(rl.s));
+                    st_agent(&row->nallowed, na);
+                    st_agent(&row->bstar, (u32)NBINS);
+                    st_agent(&row->above, (u64)0);
+                    st_agent(&row->P, (u64)0);
+                    st_agent(&row->state, state);
+                }
+            }
+        }
+        __syncthreads();
+        if (s_rec[1] != FS_CUT) return;
+        top = s_rec[0];
+    } else {
+        if (ld_agent(&row->state) != FS_CUT) return;
+        top = ld_agent(&row->top);
+    }
     if (!(p.top_p > 0.0f && p.top_p < 1.0f)) return;  // no top-p: no histogram
-    if (ld_agent(&ws.rows[r].state) != FS_CUT) return;
     const Row<DT, COUNTS, MASK> R = make_row<DT, COUNTS, MASK>(logits, stride, vocab, counts, mask, p, vec, r);
-    const float M = okey_to_f32(key_ok(ld_agent(&ws.rows[r].top)));
+    const float M = okey_to_f32(key_ok(top));
     const float c2 = temp_scale(p.temperature);
     const int ntiles = (vocab + TILE - 1) / TILE;
     const int t0 = sp * tpb, t1 = min(ntiles, t0 + tpb);
     for (int i = tid; i < NBINS; i += NTF) s_hist[i] = 0;
     __syncthreads();
-    stream_tiles(R, t0, t1, [&](int, int, const float (&lv)[4]) {
+    auto hist_group = [&](int, int, const float (&lv)[4]) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const u64 E = mass_fast(lv[q], M, c2);
             if (E) atomicAdd((unsigned long long*)&s_hist[bin_of(lv[q], M, c2)], (unsigned long long)E);
         }
-    });
+    };
+#if GBS_FS_STEPS
+    stream_steps<SG, GBS_FS_AUXH>(R, t0, t1, hist_group, [](int, int) {});
+#else
+    stream_tiles(R, t0, t1, hist_group);
+#endif
     __syncthreads();
     // the block's histogram, and its sums per unit of y (wave w sums units w, w + NWF, ...; two bins per lane)
     const int w = tid / WAVE;
@@ -948,55 +1143,6 @@ __global__ void __launch_bounds__(NTF) fs_hist_k(const void* __restrict__ logits
     for (int u = w; u < NUNITS; u += NWF) {
         const u64 v = wave_sum_u64(s_hist[u * BINS_PER_UNIT + l] + s_hist[u * BINS_PER_UNIT + WAVE + l]);
         if (l == 0) st_agent(&my_units[u], v);
-    }
-    if (!arrive_last(&ws.cnt1[r], (unsigned)S, &s_flag)) return;
-    // The row's crossing bin, from a few KB: the blocks' unit sums give the total, P and the unit where the cumulative
-    // mass from the top reaches P; then only that unit's 128 bins are summed over the blocks.
-    __shared__ u64 s_units[NUNITS];
-    __shared__ u64 s_fine[BINS_PER_UNIT];
-    __shared__ u64 s_bc[3];
-    if (tid < NUNITS) {
-        const u64* all = ws.units + (size_t)wr * S * NUNITS + tid;
-        u64 v = 0;
-        for (int o = 0; o < S; ++o) v += ld_agent(&all[(size_t)o * NUNITS]);
-        s_units[tid] = v;
-    }
-    __syncthreads();
-    if (tid < WAVE) {
-        const u64 v = l < NUNITS ? s_units[l] : 0ull;
-        const u64 Z = wave_sum_u64(v);
-        const u64 Pv = mul_ceil64(p.top_p, Z);
-        const u64 incl = wave_scan_u64(v);
-        const int f = (int)__builtin_ctzll(ballot(incl >= Pv));  // Pv <= Z: some unit reaches it
-        if (l == f) {
-            s_bc[0] = (u64)f;
-            s_bc[1] = incl - v;  // the mass of the units above
-            s_bc[2] = Pv;
-        }
-    }
-    __syncthreads();
-    const int ustar = (int)s_bc[0];
-    if (tid < BINS_PER_UNIT) {
-        const u64* all = ws.hist + (size_t)wr * S * NBINS + ustar * BINS_PER_UNIT + tid;
-        u64 v = 0;
-        for (int o = 0; o < S; ++o) v += ld_agent(&all[(size_t)o * NBINS]);
-        s_fine[tid] = v;
-    }
-    __syncthreads();
-    if (tid < WAVE) {
-        // lane i holds bins 2i, 2i + 1 of the unit: the first bin where the cumulative mass reaches P
-        const u64 a0 = s_fine[2 * l], a1 = s_fine[2 * l + 1];
-        const u64 above_u = s_bc[1], Pv = s_bc[2];
-        const u64 incl = above_u + wave_scan_u64(a0 + a1);
-        const u64 excl = incl - a0 - a1;
-        const int f = (int)__builtin_ctzll(ballot(incl >= Pv));
-        if (l == f) {
-            const bool first = excl + a0 >= Pv;
-            FsRow* row = &ws.rows[r];
-            st_agent(&row->bstar, (u32)(ustar * BINS_PER_UNIT + 2 * l + (first ? 0 : 1)));
-            st_agent(&row->above, first ? excl : excl + a0);
-            st_agent(&row->P, Pv);
-        }
     }
 }
 
@@ -1035,6 +1181,7 @@ __global__ void __launch_bounds__(NTF) fs_collect_k(const void* __restrict__ log
     if (r < 0) return;
     const int tid = threadIdx.x, w = tid / WAVE, l = lane_id();
     const RowParamsDev p = params[r];
+    const float u = uniforms[r];
     const FsRow* row = &ws.rows[r];
     const u32 state0 = ld_agent(&row->state);
     if (state0 == FS_RADIX) {
@@ -1050,14 +1197,74 @@ __global__ void __launch_bounds__(NTF) fs_collect_k(const void* __restrict__ log
     const float M = okey_to_f32(key_ok(top));
     const float c2 = temp_scale(p.temperature);
     const bool topp = p.top_p > 0.0f && p.top_p < 1.0f;
-    const u32 bstar = ld_agent(&row->bstar);
+    // the log-sum-exp, for the last block's log-probability
+    const float lse_m = __uint_as_float(ld_agent((const u32*)&row->lse_m));
+    const float lse_s = __uint_as_float(ld_agent((const u32*)&row->lse_s));
     const u64 Q = p.min_p > 0.0f ? mul_ceil64(p.min_p, MASS_ONE) : 0ull;
     const int ntiles = (vocab + TILE - 1) / TILE;
     const int t0 = sp * tpb, t1 = min(ntiles, t0 + tpb);
-    if (tid == 0) s_ncol = 0;
-    __syncthreads();
-    // kept masses of the bins above b* per tile (per-wave partials); the tokens of bin b* into LDS
-    stream_tiles(R, t0, t1, [&](int t, int e, const float (&lv)[4]) {
+    // The crossing bin b*, while the first loads are in flight: the blocks' sums per unit of y give the total, P and
+    // the unit where the cumulative mass from the top reaches P; that unit's 128 bins summed over the blocks give b*
+    // and the mass above it. No top-p: no cut (every bin is above b* = NBINS).
+    __shared__ u64 s_units[NUNITS], s_fine[BINS_PER_UNIT], s_cx[3];
+    u32 bstar = NBINS;
+    u64 above = 0, P = 0;
+    auto crossing = [&]() {
+        if (topp) {
+            for (int i = tid; i < NUNITS; i += NTF) s_units[i] = 0;
+            for (int i = tid; i < BINS_PER_UNIT; i += NTF) s_fine[i] = 0;
+        }
+        if (tid == 0) s_ncol = 0;
+        for (int i = tid; i < (t1 - t0) * NWF; i += NTF) s_tilew[i / NWF][i % NWF] = 0;
+        __syncthreads();
+        if (!topp) return;
+        const u64* U = ws.units + (size_t)wr * S * NUNITS;
+        for (int i = tid; i < S * NUNITS; i += NTF) {
+            const u64 v = ld_agent(&U[i]);
+            if (v) atomicAdd((unsigned long long*)&s_units[i % NUNITS], (unsigned long long)v);
+        }
+        __syncthreads();
+        if (tid < WAVE) {
+            const u64 v = l < NUNITS ? s_units[l] : 0ull;
+            const u64 Z = wave_sum_u64(v);
+            const u64 Pv = mul_ceil64(p.top_p, Z);
+            const u64 incl = wave_scan_u64(v);
+            const int f = min((int)__builtin_ctzll(ballot(incl >= Pv) | (1ull << 63)), NUNITS - 1);  // Pv <= Z: a unit reaches it
+            if (l == f) {
+                s_cx[0] = (u64)f;
+                s_cx[1] = incl - v;  // the mass of the units above
+                s_cx[2] = Pv;
+            }
+        }
+        __syncthreads();
+        const int ustar = (int)s_cx[0];
+        const u64* H = ws.hist + (size_t)wr * S * NBINS + (size_t)ustar * BINS_PER_UNIT;
+        for (int i = tid; i < S * BINS_PER_UNIT; i += NTF) {
+            const u64 v = ld_agent(&H[(size_t)(i / BINS_PER_UNIT) * NBINS + (i % BINS_PER_UNIT)]);
+            if (v) atomicAdd((unsigned long long*)&s_fine[i % BINS_PER_UNIT], (unsigned long long)v);
+        }
+        __syncthreads();
+        if (tid < WAVE) {
+            // lane i holds bins 2i, 2i + 1 of the unit: the first bin where the cumulative mass reaches P
+            const u64 a0 = s_fine[2 * l], a1 = s_fine[2 * l + 1];
+            const u64 Pv = s_cx[2];
+            const u64 incl = s_cx[1] + wave_scan_u64(a0 + a1);
+            const u64 excl = incl - a0 - a1;
+            const int f = (int)__builtin_ctzll(ballot(incl >= Pv) | (1ull << 63));
+            if (l == f) {
+                const bool first = excl + a0 >= Pv;
+                s_cx[0] = (u64)(ustar * BINS_PER_UNIT + 2 * l + (first ? 0 : 1));
+                s_cx[1] = first ? excl : excl + a0;
+            }
+        }
+        __syncthreads();
+        bstar = (u32)s_cx[0];
+        above = s_cx[1];
+        P = s_cx[2];
+    };
+    // kept masses of the bins above b* per tile (per-step partials); the tokens of bin b* into LDS
+    u64 sacc = 0;
+    auto collect_group = [&](int t, int e, const float (&lv)[4]) {
         u64 s = 0;
         u64 Eq[4];
         bool col[4];
@@ -1088,9 +1295,22 @@ __global__ void __launch_bounds__(NTF) fs_collect_k(const void* __restrict__ log
                 }
             }
         }
-        s = wave_sum_u64(s);
-        if (l == 0) s_tilew[t - t0][w] = s;
+        sacc += s;
+    };
+    auto collect_step = [&](int t, int q) {
+        const u64 v = wave_sum_u64(sacc);
+        if (l == 0) s_tilew[t - t0][q] = v;
+        sacc = 0;
+    };
+#if GBS_FS_STEPS
+    stream_steps<SG, GBS_FS_AUXC>(R, t0, t1, collect_group, collect_step, crossing);
+#else
+    crossing();
+    stream_tiles(R, t0, t1, [&](int t, int e, const float (&lv)[4]) {
+        collect_group(t, e, lv);
+        collect_step(t, w);
     });
+#endif
     __syncthreads();
     for (int t = t0 + tid; t < t1; t += NTF) {
         u64 v = 0;
@@ -1107,11 +1327,6 @@ __global__ void __launch_bounds__(NTF) fs_collect_k(const void* __restrict__ log
     }
     if (!arrive_last(&ws.cnt2[r], (unsigned)S, &s_flag)) return;
     // ---- the row's last block: gather the collected tokens (or hand the row to the radix path)
-    float lse_m = 0.f, lse_s = 0.f;  // for the log-probability at the end, loaded now
-    if (tid == 0) {
-        lse_m = __uint_as_float(ld_agent((const u32*)&row->lse_m));
-        lse_s = __uint_as_float(ld_agent((const u32*)&row->lse_s));
-    }
     // the blocks' counts (one load per thread), then their offsets
     if (tid < S) s_off[tid + 1] = ld_agent(&ws.ccount[(size_t)wr * S + tid]);
     __syncthreads();
@@ -1148,52 +1363,47 @@ __global__ void __launch_bounds__(NTF) fs_collect_k(const void* __restrict__ log
     __syncthreads();
     u64 kp = (u64)VALID_MIN_OK << 32;  // every valid key
     if (topp) {
-        // the collected token with above + G < P <= above + G + E, G the mass of the collected tokens with larger keys
-        const u64 above = ld_agent(&row->above), P = ld_agent(&row->P);
-        if (tid == 0) s_bc[0] = kp;
-        for (u32 j = n + tid; j < ((n + 7u) & ~7u); j += NTF) {  // pad to whole groups of 8: keys 0 never count
-            s_key[j] = 0ull;
-            s_mass[j] = 0ull;
-        }
-        __syncthreads();
-        for (u32 i = tid; i < n; i += NTF) {
-            const u64 ki = s_key[i];
-            u64 g = 0;
-            for (u32 j = 0; j < n; j += 8) {  // 8 independent LDS reads in flight (broadcast: every lane reads j)
-                u64 kk[8], mm[8];
-#pragma unroll
-                for (int q = 0; q < 8; ++q) {
-                    kk[q] = s_key[j + q];
-                    mm[q] = s_mass[j + q];
-                }
-#pragma unroll
-                for (int q = 0; q < 8; ++q) g += kk[q] > ki ? mm[q] : 0ull;
-            }
-            const u64 lo = above + g;
-            if (lo < P && P <= lo + s_mass[i]) s_bc[0] = ki;
-        }
-        __syncthreads();
-        kp = s_bc[0];
+        // the top-p key among the collected tokens of bin b*
+        kp = cut_collected(s_key, s_mass, n, above, P, M, c2, bstar, sh.cnt, s_bc);
         for (u32 j = tid; j < n; j += NTF) {
             const u64 E = s_mass[j];
             if (s_key[j] >= kp && E >= Q) atomicAdd((unsigned long long*)&s_tile[key_id(s_key[j]) / TILE], (unsigned long long)E);
         }
         __syncthreads();
     }
-    // ---- the draw: the tile that holds t, then its token (thread sums, a block scan, the owning thread's 4 elements)
-    u64 z = 0;
-    for (int t = 0; t < ntiles; ++t) z += s_tile[t];
-    const float u = uniforms[r];
-    const u64 target = (u64)mul_floor(u, (u128)z, nullptr);
-    int tsel = ntiles - 1;
-    u64 before = 0;
-    for (int t = 0; t < ntiles; ++t) {
-        if (before + s_tile[t] > target) {
-            tsel = t;
-            break;
+    // ---- the draw: the tile that holds t (wave 0 scans the tiles' kept masses, 64 at a time), then its token (thread
+    // sums, a block scan, the owning thread's 4 elements)
+    if (tid < WAVE) {
+        u64 zl = 0;
+        for (int t = l; t < ntiles; t += WAVE) zl += s_tile[t];
+        const u64 zz = wave_sum_u64(zl);
+        const u64 tg = (u64)mul_floor(u, (u128)zz, nullptr);
+        int ts = ntiles - 1;
+        u64 bf = zz - s_tile[ntiles - 1];
+        u64 run = 0;
+        for (int c = 0; c < ntiles; c += WAVE) {
+            const bool in = c + l < ntiles;
+            const u64 v = in ? s_tile[c + l] : 0ull;
+            const u64 incl = run + wave_scan_u64(v);
+            const u64 hit = ballot(in && incl > tg);
+            if (hit) {
+                const int f = (int)__builtin_ctzll(hit);
+                ts = c + f;
+                bf = readlane64(incl - v, f);
+                break;
+            }
+            run = readlane64(incl, WAVE - 1);
         }
-        before += s_tile[t];
+        if (l == 0) {
+            s_bc[4] = zz;
+            s_bc[5] = tg;
+            s_bc[6] = (u64)ts;
+            s_bc[7] = bf;
+        }
     }
+    __syncthreads();
+    const u64 z = s_bc[4], target = s_bc[5], before = s_bc[7];
+    const int tsel = (int)s_bc[6];
     auto kept_mass = [&](float v, int i) -> u64 {
         if (!valid_l(v)) return 0ull;
         if (make_key(okey_f32(v), (u32)i) < kp) return 0ull;
@@ -1269,9 +1479,9 @@ int launch_sample_full(const void* logits, int dtype, int rows, int stride, int 
             // flagged rows: the single-pass kernel has written their records (maximum, log-sum-exp, state), so no pass 0
             if (!row_flags)
                 hipLaunchKernelGGL((fs_pass0_k<D, C, Mk>), grid, dim3(NTF), 0, st, logits, (long long)stride, vocab, counts, mask, p, uniforms,
-                                   vec, pl.tpb, w, out_ids, out_greedy, out_probs, out_logprobs, out_status, row_flags, rows);
-            hipLaunchKernelGGL((fs_hist_k<D, C, Mk>), grid, dim3(NTF), 0, st, logits, (long long)stride, vocab, counts, mask, p, vec, pl.tpb,
-                               w, row_flags, rows);
+                                   vec, pl.tpb, w);
+            hipLaunchKernelGGL((fs_hist_k<D, C, Mk>), grid, dim3(NTF), 0, st, logits, (long long)stride, vocab, counts, mask, p, uniforms,
+                               vec, pl.tpb, w, out_ids, out_greedy, out_probs, out_logprobs, out_status, row_flags, rows);
             hipLaunchKernelGGL((fs_collect_k<D, C, Mk>), grid, dim3(NTF), 0, st, logits, (long long)stride, vocab, counts, mask, p,
                                uniforms, vec, pl.tpb, w, out_ids, out_greedy, out_probs, out_logprobs, out_status, row_flags, rows);
         }
