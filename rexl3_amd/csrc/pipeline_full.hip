@@ -62,7 +62,9 @@ struct Row {
         if (COUNTS) w.c = __builtin_amdgcn_raw_buffer_load_b128(rc, (u32)e * 4u, 0, AUX);
         if (MASK) w.m = __builtin_amdgcn_raw_buffer_load_b32(rm, (u32)(e >> 5) * 4u, 0, 0);
     }
-    // the penalised, masked logits of a raw group at e (out of range: -inf)
+    // the penalised, masked logits of a raw group at e (out of range: -inf). The raw loads serve rows of whole groups
+    // (vocab % 4 == 0), so a group is in range or out of it as a whole; the penalty is computed for every element and
+    // selected, without branches.
     __device__ __forceinline__ void from_raw(const Raw& w, int e, float (&l)[4]) const {
         float xv[4];
         if (DT == GBS_DTYPE_F32) {
@@ -71,11 +73,18 @@ struct Row {
             widen2<DT>(w.x.x, xv[0], xv[1]);
             widen2<DT>(w.x.y, xv[2], xv[3]);
         }
+        const bool gin = e < vocab;
         const u32 mw = MASK ? w.m >> (e & 31) : 0xFu;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const bool in = e + q < vocab && ((mw >> q) & 1u);
-            l[q] = in ? pen(xv[q], COUNTS ? (int)w.c[q] : 0) : -INFINITY;
+            float v = xv[q];
+            if (COUNTS) {
+                const int cnt = (int)w.c[q];
+                const float a = v > 0.0f ? v * rinv : v * rep;
+                const float pv = a - ((float)cnt * freq + pres);
+                v = cnt > 0 ? pv : v;
+            }
+            l[q] = gin && ((mw >> q) & 1u) ? v : -INFINITY;
         }
     }
 
@@ -145,6 +154,28 @@ struct Pass0Acc {
     __device__ __forceinline__ u64 key() const { return bv > -INFINITY ? make_key(okey_f32(bv), bid) : 0ull; }
 };
 
+// A load of what an earlier launch on the stream wrote (launch boundaries make it visible; a plain load may be served
+// by the caches).
+template <typename T>
+__device__ __forceinline__ T ld_prev(const T* p) {
+    return *p;
+}
+
+// The sum over the row's S blocks of at(o), a load of block o's value, in block order (the same in every block of the
+// row), with eight loads in flight at a time.
+template <class T, class F>
+__device__ __forceinline__ T sum_blocks(int S, F&& at) {
+    T acc = 0;
+    for (int o0 = 0; o0 < S; o0 += 8) {
+        T v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = o0 + j < S ? at(o0 + j) : T(0);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc += v[j];
+    }
+    return acc;
+}
+
 // A buffer resource over [base, base + bytes). Both are the same on every lane (a row's), made visibly uniform so that
 // the loads take the resource from scalar registers without a loop over lanes.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t full_rsrc(const void* base, u32 bytes) {
@@ -204,7 +235,7 @@ __device__ __forceinline__ void stream_tiles(const Row<DT, COUNTS, MASK>& R, int
 // so every wait counts exactly the loads issued after the buffer it needs. f(t, e, l) is called per group and
 // fe(t, q) once per step (q: the step's place in its tile, below TILE / WS); f and fe must not hold block barriers.
 // pre() is called by every thread once the first step's loads are in flight, before any group is processed (it may
-// hold block barriers).
+// hold block barriers); when it returns false (the same in every thread) nothing is processed.
 #ifndef GBS_FS_STEPS
 #define GBS_FS_STEPS 1
 #endif
@@ -228,7 +259,7 @@ __device__ __forceinline__ void stream_steps(const Row<DT, COUNTS, MASK>& R, int
     constexpr int WS = G * 256, SPT = TILE / WS;
     const int w = (int)threadIdx.x / WAVE, l = lane_id();
     if (!R.vec || R.vocab % 4 != 0) {  // one group per lane and step: wave w takes elements [w * 256, + 256) of each tile
-        pre();
+        if (!pre()) return;
         for (int t = t0; t < t1; ++t) {
             const int e = t * TILE + (int)threadIdx.x * 4;
             float lv[4];
@@ -267,7 +298,7 @@ __device__ __forceinline__ void stream_steps(const Row<DT, COUNTS, MASK>& R, int
     Raw B[G];
     int k = w;
     load(k, B);
-    pre();
+    if (!pre()) return;
     while (k < nsteps) {
         Raw C[G];
 #pragma unroll
@@ -281,7 +312,7 @@ __device__ __forceinline__ void stream_steps(const Row<DT, COUNTS, MASK>& R, int
 
 template <int G, int AUX, int DT, bool COUNTS, bool MASK, class F, class FE>
 __device__ __forceinline__ void stream_steps(const Row<DT, COUNTS, MASK>& R, int t0, int t1, F&& f, FE&& fe) {
-    stream_steps<G, AUX>(R, t0, t1, f, fe, [] {});
+    stream_steps<G, AUX>(R, t0, t1, f, fe, [] { return true; });
 }
 
 // the whole row
@@ -351,23 +382,24 @@ struct Shared {
 
 static_assert(NBINS == (int)FS_NBINS, "the per-row record's bin count");
 
-// The exact top-p key among the n tokens collected from the crossing bin b* (keys and masses in LDS): the one key K
-// with above + G(K) < P <= above + G(K) + E(K), G(K) the mass of the collected keys larger than K (the crossing bin
-// holds the target: above < P <= above + its mass). The bin is split into NSUB sub-bins by the same y as the bin
-// (sub = floor(NSUB * (-128 y - b*)), clamped to the last; it never decreases as the value decreases, and equal values
-// share it); a mass histogram of the sub-bins gives the one holding the target, and only its tokens are compared with
-// each other. Every thread calls it; it returns the key on every thread. LDS: s_cnt holds the sub-bins' masses, then
+// The exact top-p key among the n tokens collected from the bins [r_lo, r_hi] of bin_of() (keys and masses in LDS):
+// the one key K with above + G(K) < P <= above + G(K) + E(K), G(K) the mass of the collected keys larger than K (the
+// bins hold the target: above < P <= above + their mass). They are split into NSUB sub-bins by the same y as the bins
+// (sub = floor(NSUB (-128 y - r_lo) / (r_hi - r_lo + 1)), clamped; it never decreases as the value decreases, and
+// equal values share it); a mass histogram of the sub-bins gives the one holding the target, and only its tokens are
+// compared with each other. Every thread calls it; it returns the key on every thread. LDS: s_cnt holds the sub-bins' masses, then
 // the list of the crossing sub-bin's tokens.
 constexpr int NSUB = 256;
 constexpr u32 SUB_LIST_CAP = NB - 2 * NSUB;  // u32 slots of s_cnt after the sub-bins' masses
-__device__ u64 cut_collected(const u64* keys, const u64* masses, u32 n, u64 above, u64 P, float M, float c2, u32 bstar, u32* s_cnt,
-                             u64* s_bc) {
+__device__ u64 cut_collected(const u64* keys, const u64* masses, u32 n, u64 above, u64 P, float M, float c2, int r_lo, int r_hi,
+                             u32* s_cnt, u64* s_bc) {
     const int tid = threadIdx.x, l = lane_id();
     u64* const s_sub = (u64*)s_cnt;
     u32* const s_list = s_cnt + 2 * NSUB;
+    const float scale = (float)NSUB / (float)(r_hi - r_lo + 1);
     auto sub_of = [&](u64 key) {
         const float y = (okey_to_f32(key_ok(key)) - M) * c2;
-        return (u32)fminf((-y * (float)BINS_PER_UNIT - (float)bstar) * (float)NSUB, (float)(NSUB - 1));
+        return (u32)fminf(fmaxf((-y * (float)BINS_PER_UNIT - (float)r_lo) * scale, 0.0f), (float)(NSUB - 1));
     };
     for (int i = tid; i < NSUB; i += NTF) s_sub[i] = 0;
     if (tid == 0) {
@@ -637,7 +669,7 @@ __device__ bool binned_cut(const Row<DT, COUNTS, MASK>& R, float M, float c2, fl
     u64 kp = (u64)VALID_MIN_OK << 32;  // every valid key
     if (topp) {
         // the top-p key among the collected tokens of bin b*
-        kp = cut_collected(sh.maxk, sh.mass, n, above, P, M, c2, bstar, sh.cnt, sh.bc);
+        kp = cut_collected(sh.maxk, sh.mass, n, above, P, M, c2, (int)bstar, (int)bstar, sh.cnt, sh.bc);
         // the kept tokens of bin b* (key >= the top-p key, mass >= Q) into their tiles
         for (u32 j = tid; j < n; j += NTF) {
             const u64 E = sh.mass[j];
@@ -650,7 +682,7 @@ __device__ bool binned_cut(const Row<DT, COUNTS, MASK>& R, float M, float c2, fl
 }
 
 template <int DT, bool COUNTS, bool MASK>
-__device__ __attribute__((noinline)) void full_row(const void* __restrict__ logits, long long stride, int vocab, const int* __restrict__ counts,
+__device__ __forceinline__ void full_row(const void* __restrict__ logits, long long stride, int vocab, const int* __restrict__ counts,
                                          const u32* __restrict__ mask, const RowParamsDev* __restrict__ params,
                                          const float* __restrict__ uniforms, bool vec, int* __restrict__ out_ids,
                                          int* __restrict__ out_greedy, float* __restrict__ out_probs, float* __restrict__ out_logprobs,
@@ -793,17 +825,21 @@ __device__ __attribute__((noinline)) void full_row(const void* __restrict__ logi
     for (int o = 0; o < w; ++o) wbase += sh.red[o];
     const u64 excl = wbase + incl - mine;
     if (excl <= target && target < excl + mine) {
-        u64 acc = excl;
+        // the first of the thread's four elements whose running mass exceeds the target (selections, no indexing)
+        u64 acc = excl, ef = 0;
+        int qf = -1;
+        float lf = 0.f;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             acc += em[q];
-            if (acc > target) {
-                sh.bc[5] = (u64)(e + q);
-                sh.bc[6] = em[q];
-                sh.bc[7] = __float_as_uint(lv[q]);
-                break;
-            }
+            const bool hit = qf < 0 && acc > target;
+            qf = hit ? q : qf;
+            ef = hit ? em[q] : ef;
+            lf = hit ? lv[q] : lf;
         }
+        sh.bc[5] = (u64)(e + qf);
+        sh.bc[6] = ef;
+        sh.bc[7] = __float_as_uint(lf);
     }
     __syncthreads();
     const int id = (int)sh.bc[5];
@@ -824,6 +860,24 @@ __global__ void __launch_bounds__(NTF) sample_full_k(const void* __restrict__ lo
     if (flags && flags[blockIdx.x] == 0u) return;
     full_row<DT, COUNTS, MASK>(logits, stride, vocab, counts, mask, params, uniforms, vec, out_ids, out_greedy, out_probs, out_logprobs,
                                out_status, (int)blockIdx.x, sh);
+}
+
+// The rows the split path marked (top-k with a cut, an infinite maximum or 1/T, no collection window, a window that
+// missed the cut or held more than CAP tokens, flagged rows past the workspace's): one block each, the single-block
+// path; the mark is cleared for the next launch.
+template <int DT, bool COUNTS, bool MASK>
+__global__ void __launch_bounds__(NTF) fs_fallback_k(const void* __restrict__ logits, long long stride, int vocab,
+                                                     const int* __restrict__ counts, const u32* __restrict__ mask,
+                                                     const RowParamsDev* __restrict__ params, const float* __restrict__ uniforms, bool vec,
+                                                     int* __restrict__ out_ids, int* __restrict__ out_greedy, float* __restrict__ out_probs,
+                                                     float* __restrict__ out_logprobs, int* __restrict__ out_status,
+                                                     unsigned* __restrict__ marks) {
+    __shared__ Shared sh;
+    const int r = (int)blockIdx.x;
+    if (marks[r] == 0u) return;
+    full_row<DT, COUNTS, MASK>(logits, stride, vocab, counts, mask, params, uniforms, vec, out_ids, out_greedy, out_probs, out_logprobs,
+                               out_status, r, sh);
+    if (threadIdx.x == 0) marks[r] = 0u;
 }
 
 // ================================================================================================== the split path
@@ -854,23 +908,53 @@ struct FsPart0 {
     u64 key;
     u32 nan, nallowed;
     float m, s;
-    u32 pad[2];
+    int kgrid;  // the row's histogram grid top (pass 0; the same in every block of the row)
+    u32 pad;
 };
 
-struct FsWs {
-    unsigned *cnt0, *cnt1, *cnt2;  // per-row arrival counters, at fixed offsets (zero between launches)
-    FsRow* rows;                   // [65536] in the control region, indexed by row
-    FsPart0* p0;                   // [rows][S]
-    u64* hist;                     // [rows][S][NBINS]
-    u64* units;                    // [rows][S][NUNITS]: each block's histogram summed per unit of y
-    u64 *ckey, *cmass;             // [rows][S][CAP]
-    u32* ccount;                   // [rows][S]
-    u64* tiles;                    // [rows][ntiles]
-};
-
+// The split path's workspace, carved from one base pointer (so that a kernel holds one pointer and three counts instead
+// of a pointer per array): the control region (arrival counters, the per-row records), then per (row, block) partials.
 constexpr size_t FS_CTL = SAMPLE_CTL_BYTES;  // the control region shared with the single-pass kernel
 
-size_t fs_align(size_t b) { return (b + 255) & ~(size_t)255; }
+__host__ __device__ __forceinline__ size_t fs_align(size_t b) { return (b + 255) & ~(size_t)255; }
+
+struct FsWs {
+    char* base;
+    int nrows, S, ntiles;
+
+    __host__ __device__ size_t rs() const { return (size_t)nrows * S; }
+    __host__ __device__ unsigned* cnt2() const { return (unsigned*)base + 2 * 65536; }  // per-row arrival counters
+    // per-row marks of the rows the single-block path takes after the collection (zero between launches)
+    __host__ __device__ unsigned* fallback() const { return (unsigned*)base + 65536; }
+    __host__ __device__ FsRow* rec() const { return (FsRow*)(base + SAMPLE_FSROW_OFFSET); }  // [65536], indexed by row
+    __host__ __device__ size_t o_p0() const { return FS_CTL; }
+    __host__ __device__ size_t o_hist() const { return o_p0() + fs_align(rs() * sizeof(FsPart0)); }
+    __host__ __device__ size_t o_units() const { return o_hist() + fs_align(rs() * NBINS * 8); }
+    __host__ __device__ size_t o_ubound() const { return o_units() + fs_align(rs() * NUNITS * 8); }
+    __host__ __device__ size_t o_zab() const { return o_ubound() + fs_align(rs() * NUNITS * sizeof(float2)); }
+    __host__ __device__ size_t o_ckey() const { return o_zab() + fs_align(rs() * 4 * 8); }
+    __host__ __device__ size_t o_cmass() const { return o_ckey() + fs_align(rs() * CAP * 8); }
+    __host__ __device__ size_t o_ccount() const { return o_cmass() + fs_align(rs() * CAP * 8); }
+    __host__ __device__ size_t o_tiles() const { return o_ccount() + fs_align(rs() * 4); }
+    __host__ __device__ size_t bytes() const { return o_tiles() + fs_align((size_t)nrows * ntiles * 8); }
+    // [rows][S]: pass 0's partials
+    __host__ __device__ FsPart0* p0() const { return (FsPart0*)(base + o_p0()); }
+    // [rows][S][NBINS]: fs_hist_k's mass histograms, or pass 0's counts (u32, first half)
+    __host__ __device__ u64* hist() const { return (u64*)(base + o_hist()); }
+    // [rows][S][NUNITS]: fs_hist_k's histograms summed per unit of y
+    __host__ __device__ u64* units() const { return (u64*)(base + o_units()); }
+    // [rows][S][NUNITS]: pass 0's per-unit bounds of the mass (relative to the grid top)
+    __host__ __device__ float2* ubound() const { return (float2*)(base + o_ubound()); }
+    // [rows][S][4]: the collection's exact total, mass above the window, window mass
+    __host__ __device__ u64* zab() const { return (u64*)(base + o_zab()); }
+    // [rows][S][CAP]: the collected keys and masses, and their counts [rows][S]
+    __host__ __device__ u64* ckey() const { return (u64*)(base + o_ckey()); }
+    __host__ __device__ u64* cmass() const { return (u64*)(base + o_cmass()); }
+    __host__ __device__ u32* ccount() const { return (u32*)(base + o_ccount()); }
+    // [rows][ntiles]: kept masses per tile
+    __host__ __device__ u64* tiles() const { return (u64*)(base + o_tiles()); }
+};
+
 
 struct FsPlan {
     int S, tpb, ntiles;
@@ -886,30 +970,11 @@ FsPlan fs_plan(int rows, int vocab, int target_blocks = FS_TARGET_BLOCKS) {
     if (want < 1) want = 1;
     p.tpb = (p.ntiles + want - 1) / want;
     p.S = (p.ntiles + p.tpb - 1) / p.tpb;
-    const size_t rs = (size_t)rows * p.S;
-    p.bytes = FS_CTL + fs_align(rs * sizeof(FsPart0)) + fs_align(rs * NBINS * 8) +
-              fs_align(rs * NUNITS * 8) + 2 * fs_align(rs * CAP * 8) + fs_align(rs * 4) + fs_align((size_t)rows * p.ntiles * 8);
+    p.bytes = FsWs{nullptr, rows, p.S, p.ntiles}.bytes();
     return p;
 }
 
-FsWs fs_carve(void* ws, int rows, const FsPlan& p) {
-    char* c = (char*)ws;
-    FsWs w;
-    w.cnt0 = (unsigned*)c;
-    w.cnt1 = w.cnt0 + 65536;
-    w.cnt2 = w.cnt1 + 65536;
-    c += FS_CTL;
-    const size_t rs = (size_t)rows * p.S;
-    w.rows = (FsRow*)((char*)ws + SAMPLE_FSROW_OFFSET);
-    w.p0 = (FsPart0*)c; c += fs_align(rs * sizeof(FsPart0));
-    w.hist = (u64*)c; c += fs_align(rs * NBINS * 8);
-    w.units = (u64*)c; c += fs_align(rs * NUNITS * 8);
-    w.ckey = (u64*)c; c += fs_align(rs * CAP * 8);
-    w.cmass = (u64*)c; c += fs_align(rs * CAP * 8);
-    w.ccount = (u32*)c; c += fs_align(rs * 4);
-    w.tiles = (u64*)c;
-    return w;
-}
+FsWs fs_carve(void* ws, int rows, const FsPlan& p) { return FsWs{(char*)ws, rows, p.S, p.ntiles}; }
 
 template <int DT, bool COUNTS, bool MASK>
 __device__ __forceinline__ Row<DT, COUNTS, MASK> make_row(const void* logits, long long stride, int vocab, const int* counts,
@@ -980,8 +1045,16 @@ __device__ int fs_row(const unsigned* __restrict__ flags, int rows, int rank, in
 }
 
 // Pass 0 of the split form: the block's maximum key, NaN flag, allowed count and log-sum-exp over its tiles, into
-// ws.p0[row][sp] (each wave's totals by cross-lane moves, then wave 0 over the waves': one barrier). fs_hist_k makes
-// the row's record from the S partials. Not launched under per-row dispatch.
+// ws.p0()[row][sp] (each wave's totals by cross-lane moves, then wave 0 over the waves': one barrier). For rows with
+// top-p it also counts the block's tokens on the row's histogram grid (block bins b = kgrid - 1 - floor(128 l c2),
+// clamped to [0, NBINS - 1]): kgrid is a multiple of 128, GRID_MARGIN units of y above the largest value of the row's
+// first tile, which every block of the row reads, so all of them share the grid and their units (128 bins) align.
+// The counts go to the workspace with each unit's bounds of the mass, relative to 2^(kgrid / 128): bin b holds masses
+// in [2^(-(b + 1) / 128), 2^(-b / 128)); bin 0 also holds every value above the grid (its count is kept apart), the
+// last bin every value below it (lower bound 0). fs_collect_k makes the row's record and its collection window from
+// them. Not launched under per-row dispatch.
+constexpr int GRID_MARGIN = 8;
+
 template <int DT, bool COUNTS, bool MASK>
 __global__ void __launch_bounds__(NTF) fs_pass0_k(const void* __restrict__ logits, long long stride, int vocab,
                                                   const int* __restrict__ counts, const u32* __restrict__ mask,
@@ -989,20 +1062,59 @@ __global__ void __launch_bounds__(NTF) fs_pass0_k(const void* __restrict__ logit
                                                   int tpb, FsWs ws) {
     __shared__ u64 s_k[NWF];
     __shared__ u32 s_nn[NWF], s_na[NWF];
-    __shared__ float s_lm[NWF], s_ls[NWF];
+    __shared__ float s_lm[NWF], s_ls[NWF], s_pm[NWF];
+    __shared__ u32 s_cnt[NBINS];
     const int S = gridDim.x, sp = blockIdx.x, r = blockIdx.y;
     const int tid = threadIdx.x, w = tid / WAVE, l = lane_id();
     const RowParamsDev p = params[r];
-    if (params_invalid(p, uniforms[r])) return;  // fs_hist_k writes the row's results
+    if (params_invalid(p, uniforms[r])) return;  // fs_collect_k writes the row's results
     const Row<DT, COUNTS, MASK> R = make_row<DT, COUNTS, MASK>(logits, stride, vocab, counts, mask, p, vec, r);
     const float clp = fs_clp(p);
     const int ntiles = (vocab + TILE - 1) / TILE;
     const int t0 = sp * tpb, t1 = min(ntiles, t0 + tpb);
+    // the histogram: rows with top-p, a temperature and a finite 1/T (the others never use it)
+    const bool hist = p.top_p > 0.0f && p.top_p < 1.0f && p.temperature > 0.0f && __builtin_isfinite(clp);
+    const float c2x = clp * (float)BINS_PER_UNIT;
+    float kg1 = 0.f;  // kgrid - 1
+    int kgrid = 0;
+    auto grid = [&]() -> bool {
+        if (!hist) return true;
+        for (int i = tid; i < NBINS; i += NTF) s_cnt[i] = 0;
+        // the row's first tile: its largest allowed value
+        float lv[4];
+        R.group(tid * 4, lv);
+        float pm = fmaxf(fmaxf(lv[0], lv[1]), fmaxf(lv[2], lv[3]));
+        pm = pm > -INFINITY ? pm : -INFINITY;  // NaN: no value
+#pragma unroll
+        for (int m = 1; m < WAVE; m <<= 1) pm = fmaxf(pm, __uint_as_float(xor_lane(__float_as_uint(pm), m)));
+        if (l == 0) s_pm[w] = pm;
+        __syncthreads();
+        float bm = s_pm[0];
+        for (int o = 1; o < NWF; ++o) bm = fmaxf(bm, s_pm[o]);
+        // units of y above: clamped so that kgrid stays far inside int (values beyond it only widen the window)
+        const float u = fminf(fmaxf(floorf(bm * clp), -4194304.0f), 4194304.0f);
+        kgrid = ((int)u + 1 + GRID_MARGIN) * BINS_PER_UNIT;
+        kg1 = (float)(kgrid - 1);
+        return true;
+    };
     Pass0Acc acc;
+    auto group0 = [&](int, int e, const float (&lv)[4]) {
+        acc.add(lv, e, clp);
+        if (hist) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                if (valid_l(lv[q])) {
+                    const float bf = fminf(fmaxf(kg1 - floorf(lv[q] * c2x), 0.0f), (float)(NBINS - 1));
+                    atomicAdd(&s_cnt[(u32)bf], 1u);
+                }
+            }
+        }
+    };
 #if GBS_FS_STEPS
-    stream_steps<SG, GBS_FS_AUX0>(R, t0, t1, [&](int, int e, const float (&lv)[4]) { acc.add(lv, e, clp); }, [](int, int) {});
+    stream_steps<SG, GBS_FS_AUX0>(R, t0, t1, group0, [](int, int) {}, grid);
 #else
-    stream_tiles(R, t0, t1, [&](int, int e, const float (&lv)[4]) { acc.add(lv, e, clp); });
+    grid();
+    stream_tiles(R, t0, t1, group0);
 #endif
     const u64 k = wave_max_u64(acc.key());
     const u32 nn = wave_or(acc.nan), na = wave_sum_u32(acc.nallowed);
@@ -1015,113 +1127,68 @@ __global__ void __launch_bounds__(NTF) fs_pass0_k(const void* __restrict__ logit
         s_ls[w] = ls.s;
     }
     __syncthreads();
+    const size_t slot = (size_t)r * S + sp;
+    if (hist) {
+        // the counts, and per unit (wave w: units w, w + NWF, ...; two bins per lane) the bounds of its mass
+        u32* cnt = (u32*)(ws.hist() + slot * NBINS);
+        for (int i = tid; i < NBINS; i += NTF) st_agent(&cnt[i], s_cnt[i]);
+        for (int u = w; u < NUNITS; u += NWF) {
+            const int b0 = u * BINS_PER_UNIT + 2 * l;
+            const float c0 = (float)s_cnt[b0], c1 = (float)s_cnt[b0 + 1];
+            const float e0 = exp2f(-(float)b0 / (float)BINS_PER_UNIT), e1 = exp2f(-(float)(b0 + 1) / (float)BINS_PER_UNIT),
+                        e2 = exp2f(-(float)(b0 + 2) / (float)BINS_PER_UNIT);
+            float lo = c0 * e1 + (b0 + 1 == NBINS - 1 ? 0.0f : c1 * e2);
+            float hi = c0 * e0 + c1 * e1;
+#pragma unroll
+            for (int m = 1; m < WAVE; m <<= 1) {
+                lo += __uint_as_float(xor_lane(__float_as_uint(lo), m));
+                hi += __uint_as_float(xor_lane(__float_as_uint(hi), m));
+            }
+            if (l == 0) st_agent((u64*)&ws.ubound()[slot * NUNITS + u], ((u64)__float_as_uint(hi) << 32) | __float_as_uint(lo));
+        }
+    }
     if (w != 0) return;
     const bool in = l < NWF;
     const u64 bk = wave_max_u64(in ? s_k[l] : 0ull);
     const u32 bnn = wave_or(in ? s_nn[l] : 0u), bna = wave_sum_u32(in ? s_na[l] : 0u);
     const Lse bl = wave_lse(in ? Lse{s_lm[l], s_ls[l]} : Lse{-INFINITY, 0.f}, clp);
     if (l == 0) {
-        FsPart0* pp = &ws.p0[(size_t)r * S + sp];
+        FsPart0* pp = &ws.p0()[slot];
         st_agent(&pp->key, bk);
         st_agent(&pp->nan, bnn);
         st_agent(&pp->nallowed, bna);
         st_agent((u32*)&pp->m, __float_as_uint(bl.m));
         st_agent((u32*)&pp->s, __float_as_uint(bl.s));
+        st_agent(&pp->kgrid, kgrid);
+        st_agent(&pp->pad, hist ? s_cnt[0] : 0u);
     }
 }
 
-// The row's record, then the binned cut's mass histogram of the block's tiles.
-//  - The record: without per-row dispatch every block of the row makes it from pass 0's S partials (one load per lane
-//    of wave 0); block 0 stores it and writes the results of the rows that need no cut (invalid, NaN, empty, T = 0),
-//    and marks the rows that need the radix path (top-k with a cut, an infinite maximum or 1/T). Under per-row
-//    dispatch the single-pass kernel has stored it.
-//  - The histogram (rows with top-p that continue the cut): the block's bins and its sums per unit of y go to the
-//    workspace, where fs_collect_k finds the crossing bin.
+// Under per-row dispatch: the binned cut's exact mass histogram of the flagged rows (the single-pass kernel has stored
+// their records). Rows with top-p that continue the cut: the block's bins and its sums per unit of y go to the
+// workspace, where fs_collect_k finds the crossing bin.
 template <int DT, bool COUNTS, bool MASK>
 __global__ void __launch_bounds__(NTF) fs_hist_k(const void* __restrict__ logits, long long stride, int vocab,
                                                  const int* __restrict__ counts, const u32* __restrict__ mask,
-                                                 const RowParamsDev* __restrict__ params, const float* __restrict__ uniforms, bool vec,
-                                                 int tpb, FsWs ws, int* __restrict__ out_ids, int* __restrict__ out_greedy,
-                                                 float* __restrict__ out_probs, float* __restrict__ out_logprobs,
-                                                 int* __restrict__ out_status, const unsigned* __restrict__ flags, int rows) {
+                                                 const RowParamsDev* __restrict__ params, bool vec, int tpb, FsWs ws,
+                                                 const unsigned* __restrict__ flags, int rows) {
     __shared__ u64 s_hist[NBINS];
-    __shared__ u64 s_rec[2];  // the row's maximum key and state
     __shared__ int s_sel;
     const int S = gridDim.x, sp = blockIdx.x, wr = blockIdx.y;
-    if (flags && wr >= DEFER_ROWS) return;
-    const int r = flags ? fs_row(flags, rows, wr, &s_sel) : wr;
+    if (wr >= DEFER_ROWS) return;
+    const int r = fs_row(flags, rows, wr, &s_sel);
     if (r < 0) return;
-    const int tid = threadIdx.x, l = lane_id();
+    const int tid = threadIdx.x, w = tid / WAVE, l = lane_id();
     const RowParamsDev p = params[r];
-    FsRow* row = &ws.rows[r];
-    u64 top;
-    if (!flags) {
-        if (params_invalid(p, uniforms[r])) {
-            if (sp == 0 && tid == 0) {
-                fs_out(r, -1, -1, GBS_ROW_INVALID_PARAMS, 0.f, 0.f, out_ids, out_greedy, out_probs, out_logprobs, out_status);
-                st_agent(&row->state, (u32)FS_DONE);
-            }
-            return;
-        }
-        if (tid < WAVE) {
-            const float clp = fs_clp(p);
-            u64 k = 0;
-            u32 nn = 0, na = 0;
-            Lse rl{-INFINITY, 0.f};
-            for (int o = l; o < S; o += WAVE) {
-                const FsPart0* pp = &ws.p0[(size_t)wr * S + o];
-                const u64 k2 = ld_agent(&pp->key);
-                k = k2 > k ? k2 : k;
-                nn |= ld_agent(&pp->nan);
-                na += ld_agent(&pp->nallowed);
-                rl = lse_merge(rl, Lse{__uint_as_float(ld_agent((const u32*)&pp->m)), __uint_as_float(ld_agent((const u32*)&pp->s))}, clp);
-            }
-            k = wave_max_u64(k);
-            nn = wave_or(nn);
-            na = wave_sum_u32(na);
-            rl = wave_lse(rl, clp);
-            u32 state = FS_CUT;
-            const float M = okey_to_f32(key_ok(k));
-            const int greedy = (int)key_id(k);
-            if (nn || na == 0 || p.temperature == 0.0f) state = FS_DONE;
-            else if ((p.top_k > 0 && (u32)p.top_k < na) || !mass_fast_ok(M, temp_scale(p.temperature))) state = FS_RADIX;
-            if (l == 0) {
-                s_rec[0] = k;
-                s_rec[1] = state;
-                if (sp == 0) {
-                    if (nn)
-                        fs_out(r, -1, -1, GBS_ROW_NAN_LOGIT, 0.f, 0.f, out_ids, out_greedy, out_probs, out_logprobs, out_status);
-                    else if (na == 0)
-                        fs_out(r, -1, -1, GBS_ROW_NO_CANDIDATES, 0.f, 0.f, out_ids, out_greedy, out_probs, out_logprobs, out_status);
-                    else if (p.temperature == 0.0f)
-                        fs_out(r, greedy, greedy, GBS_ROW_OK, 1.0f, fs_logprob(M, M, clp, rl.m, rl.s), out_ids, out_greedy, out_probs,
-                               out_logprobs, out_status);
-                    st_agent(&row->top, k);
-                    st_agent((u32*)&row->lse_m, __float_as_uint(rl.m));
-                    st_agent((u32*)&row->lse_s, __float_as_uint(rl.s));
-                    st_agent(&row->nallowed, na);
-                    st_agent(&row->bstar, (u32)NBINS);
-                    st_agent(&row->above, (u64)0);
-                    st_agent(&row->P, (u64)0);
-                    st_agent(&row->state, state);
-                }
-            }
-        }
-        __syncthreads();
-        if (s_rec[1] != FS_CUT) return;
-        top = s_rec[0];
-    } else {
-        if (ld_agent(&row->state) != FS_CUT) return;
-        top = ld_agent(&row->top);
-    }
     if (!(p.top_p > 0.0f && p.top_p < 1.0f)) return;  // no top-p: no histogram
+    const FsRow* row = &ws.rec()[r];
+    if (ld_agent(&row->state) != FS_CUT) return;
+    const u64 top = ld_agent(&row->top);
     const Row<DT, COUNTS, MASK> R = make_row<DT, COUNTS, MASK>(logits, stride, vocab, counts, mask, p, vec, r);
     const float M = okey_to_f32(key_ok(top));
     const float c2 = temp_scale(p.temperature);
     const int ntiles = (vocab + TILE - 1) / TILE;
     const int t0 = sp * tpb, t1 = min(ntiles, t0 + tpb);
-    for (int i = tid; i < NBINS; i += NTF) s_hist[i] = 0;
-    __syncthreads();
     auto hist_group = [&](int, int, const float (&lv)[4]) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -1129,23 +1196,182 @@ __global__ void __launch_bounds__(NTF) fs_hist_k(const void* __restrict__ logits
             if (E) atomicAdd((unsigned long long*)&s_hist[bin_of(lv[q], M, c2)], (unsigned long long)E);
         }
     };
+    auto zero = [&]() {
+        for (int i = tid; i < NBINS; i += NTF) s_hist[i] = 0;
+        __syncthreads();
+        return true;
+    };
 #if GBS_FS_STEPS
-    stream_steps<SG, GBS_FS_AUXH>(R, t0, t1, hist_group, [](int, int) {});
+    stream_steps<SG, GBS_FS_AUXH>(R, t0, t1, hist_group, [](int, int) {}, zero);
 #else
+    zero();
     stream_tiles(R, t0, t1, hist_group);
 #endif
     __syncthreads();
     // the block's histogram, and its sums per unit of y (wave w sums units w, w + NWF, ...; two bins per lane)
-    const int w = tid / WAVE;
-    u64* mine = ws.hist + ((size_t)wr * S + sp) * NBINS;
+    u64* mine = ws.hist() + ((size_t)wr * S + sp) * NBINS;
     for (int i = tid; i < NBINS; i += NTF) st_agent(&mine[i], s_hist[i]);
-    u64* my_units = ws.units + ((size_t)wr * S + sp) * NUNITS;
+    u64* my_units = ws.units() + ((size_t)wr * S + sp) * NUNITS;
     for (int u = w; u < NUNITS; u += NWF) {
         const u64 v = wave_sum_u64(s_hist[u * BINS_PER_UNIT + l] + s_hist[u * BINS_PER_UNIT + WAVE + l]);
         if (l == 0) st_agent(&my_units[u], v);
     }
 }
 
+// wave-wide inclusive prefix sum of doubles (DPP row shifts, then row broadcasts, as wave_scan_u64)
+__device__ __forceinline__ double wave_scan_f64(double v) {
+    auto mv = [](double x, int ctrl, int rm) { return __longlong_as_double((long long)dpp64((u64)__double_as_longlong(x), ctrl, rm)); };
+    v += mv(v, 0x111, 0xF);
+    v += mv(v, 0x112, 0xF);
+    v += mv(v, 0x114, 0xF);
+    v += mv(v, 0x118, 0xF);
+    v += mv(v, 0x142, 0xA);
+    v += mv(v, 0x143, 0xC);
+    return v;
+}
+
+constexpr int WIN_UNITS = 4;      // the collection window's histogram units at most (more: the row takes the radix path)
+constexpr u32 FS_WINDOW_FAIL = 3;  // block-local state: no window could be made; the row's first block takes the row
+
+// The collection window of a row without per-row dispatch, from pass 0's counts on the row's grid: the bins [r_lo,
+// r_hi] of bin_of() that certainly hold the top-p cut, i.e. the mass below them is at most Z - P and the mass below
+// their top more than Z - P (Z ~ the log-sum-exp, a relative margin of 2^-14). Found from the bottom: per unit of y the
+// bounds of its mass (the blocks' sums in block order, so every block of the row finds the same window), then the bins
+// of the at most WIN_UNITS units that hold the window's ends. Every thread calls both; fs_window returns false when no
+// window is found (state FS_WINDOW_FAIL in s_w[2]). s_w: r_lo, r_hi, state.
+// Loads of the window's first stage, by threads WAVE .. WAVE + NUNITS (the caller's wave 0 loads the record meanwhile):
+// per unit the blocks' bounds summed in block order, and the count of bin 0 and the grid.
+__device__ __forceinline__ void fs_window_load(const FsWs& ws, int wr, int S, double* s_u) {
+    const int i = (int)threadIdx.x - WAVE;
+    if (i >= 0 && i < NUNITS) {
+        double lo = 0.0, hi = 0.0;
+        for (int o0 = 0; o0 < S; o0 += 8) {
+            u64 v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = o0 + j < S ? ld_prev((const u64*)&ws.ubound()[((size_t)wr * S + o0 + j) * NUNITS + i]) : 0ull;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                lo += (double)__uint_as_float((u32)v[j]);
+                hi += (double)__uint_as_float((u32)(v[j] >> 32));
+            }
+        }
+        s_u[2 * i] = lo;
+        s_u[2 * i + 1] = hi;
+    } else if (i == NUNITS) {
+        u32 c0 = 0;
+        c0 = sum_blocks<u32>(S, [&](int o) { return ld_prev(&ws.p0()[(size_t)wr * S + o].pad); });
+        s_u[2 * NUNITS] = (double)c0;
+        s_u[2 * NUNITS + 1] = (double)ld_prev(&ws.p0()[(size_t)wr * S].kgrid);
+    }
+}
+
+// The window from the loaded first stage (s_u, after a barrier).
+__device__ __attribute__((noinline)) bool fs_window(const u64* hist, int wr, int S, float M, float c2, float top_p, float lse_m,
+                                                     float lse_s, const double* s_u, u32* s_fc, int* s_w, double* s_wd) {
+    const int tid = threadIdx.x, l = lane_id();
+    const double kgrid = s_u[2 * NUNITS + 1];
+    const double F = exp2(kgrid / BINS_PER_UNIT - (double)M * (double)c2);  // the grid top's mass, relative to the maximum's
+    const double Zf = (double)lse_s, T = (1.0 - (double)top_p) * Zf, d = Zf * 0x1p-14;
+    const double Tlo = T - d > 0.0 ? T - d : 0.0, Thi = T + d;
+    const bool lse_ok = lse_m == M && Zf > 0.0 && __builtin_isfinite(Zf) && F > 0.0 && __builtin_isfinite(F);
+    if (tid < WAVE) {
+        const bool in = l < NUNITS;
+        double lo = in ? s_u[2 * l] * F : 0.0, hi = in ? s_u[2 * l + 1] * F : 0.0;
+        if (l == 0) hi += s_u[2 * NUNITS] * (1.0 - F);  // bin 0: values above the grid, masses up to the maximum's
+        const double ilo = wave_scan_f64(lo), ihi = wave_scan_f64(hi);
+        const double tlo = __longlong_as_double((long long)readlane64((u64)__double_as_longlong(ilo), WAVE - 1));
+        const double thi = __longlong_as_double((long long)readlane64((u64)__double_as_longlong(ihi), WAVE - 1));
+        const double blo = tlo - ilo, bhi = thi - ihi;  // the mass below unit l (deeper units)
+        const u64 ca = ballot(in && blo + lo > Thi), cb = ballot(in && bhi <= Tlo);
+        const int ua = ca ? 63 - __builtin_clzll(ca) : 0;
+        const int ub = cb ? (int)__builtin_ctzll(cb) : NUNITS - 1;
+        const int ulo = ua < ub ? ua : ub, uhi = ua < ub ? ub : ua;
+        if (l == 0) {
+            s_w[0] = ulo;
+            s_w[1] = uhi;
+            s_w[2] = lse_ok && uhi - ulo < WIN_UNITS ? (int)FS_CUT : (int)FS_WINDOW_FAIL;
+        }
+        if (l == uhi) {
+            s_wd[0] = blo;
+            s_wd[1] = bhi;
+        }
+    }
+    __syncthreads();
+    if (s_w[2] != (int)FS_CUT) return false;
+    const int ulo = s_w[0], uhi = s_w[1];
+    const int nb = (uhi - ulo + 1) * BINS_PER_UNIT;
+    for (int i = tid; i < nb; i += NTF) {
+        u32 c = 0;
+        c = sum_blocks<u32>(S, [&](int o) { return ld_prev(&((const u32*)(hist + ((size_t)wr * S + o) * NBINS))[ulo * BINS_PER_UNIT + i]); });
+        s_fc[i] = c;
+    }
+    __syncthreads();
+    if (tid < WAVE) {
+        // lane l: bins base + l * PB .. + PB - 1 of the units ulo..uhi (PB = 2 per unit)
+        constexpr int PBM = 2 * WIN_UNITS;
+        const int PB = nb / WAVE, base = ulo * BINS_PER_UNIT;
+        double blo[PBM], bhi[PBM], slo = 0.0, shi = 0.0;
+#pragma unroll
+        for (int q = 0; q < PBM; ++q) {
+            blo[q] = bhi[q] = 0.0;
+            if (q < PB) {
+                const int b = base + l * PB + q;
+                const double c = (double)s_fc[l * PB + q];
+                blo[q] = b == NBINS - 1 ? 0.0 : c * (double)exp2f(-(float)(b + 1) / (float)BINS_PER_UNIT) * F;
+                bhi[q] = b == 0 ? c : c * (double)exp2f(-(float)b / (float)BINS_PER_UNIT) * F;
+                slo += blo[q];
+                shi += bhi[q];
+            }
+        }
+        const double ilo = wave_scan_f64(slo), ihi = wave_scan_f64(shi);
+        const double tlo = __longlong_as_double((long long)readlane64((u64)__double_as_longlong(ilo), WAVE - 1));
+        const double thi = __longlong_as_double((long long)readlane64((u64)__double_as_longlong(ihi), WAVE - 1));
+        // the mass below this lane's last bin: the deeper lanes' and the units below uhi
+        double below_lo = s_wd[0] + (tlo - ilo), below_hi = s_wd[1] + (thi - ihi);
+        int a = -1, bb = 1 << 30;
+#pragma unroll
+        for (int q = PBM - 1; q >= 0; --q) {
+            if (q < PB) {
+                const int b = base + l * PB + q;
+                if (below_hi <= Tlo) bb = b;  // the mass below bin b is at most Z - P
+                if (a < 0 && below_lo + blo[q] > Thi) a = b;  // the mass from bin b down exceeds Z - P
+                below_lo += blo[q];
+                below_hi += bhi[q];
+            }
+        }
+        // b_a: the deepest bin whose mass from it down exceeds Z - P (none: the top of the units); b_b: the highest bin
+        // whose mass below is at most Z - P
+        int ba = a, bbv = bb;
+#pragma unroll
+        for (int m = 1; m < WAVE; m <<= 1) {
+            ba = max(ba, (int)xor_lane((u32)ba, m));
+            bbv = min(bbv, (int)xor_lane((u32)bbv, m));
+        }
+        if (ba < 0) ba = base;
+        if (bbv > base + nb - 1) bbv = base + nb - 1;
+        const int wa = ba < bbv ? ba : bbv, wb = ba < bbv ? bbv : ba;
+        if (l == 0) {
+            // grid bins [wa, wb] to bins of bin_of(): -128 y lies in (D + wa, D + 1 + wb], D = 128 M c2 - kgrid; one bin of
+            // margin each side for the rounding of the two computations of y
+            const double D = (double)BINS_PER_UNIT * (double)M * (double)c2 - kgrid;
+            const double rlo = wa == 0 ? 0.0 : floor(D + wa) - 1.0, rhi = wb == NBINS - 1 ? (double)(NBINS - 1) : floor(D + wb) + 2.0;
+            s_w[0] = (int)fmin(fmax(rlo, 0.0), (double)(NBINS - 1));
+            s_w[1] = (int)fmin(fmax(rhi, 0.0), (double)(NBINS - 1));
+        }
+    }
+    __syncthreads();
+    return true;
+}
+
+// The collection: every token's exact mass is summed (the row's total Z), the masses of the bins above the window
+// (the mass above it, and per 4096-element tile the kept ones: mass >= the min-p floor) and of the window's bins;
+// the window's tokens go to the workspace. The window: without per-row dispatch, from pass 0's counts (fs_window); under
+// it, the exact crossing bin of fs_hist_k's histograms. Without per-row dispatch each block first makes the row's record
+// from pass 0's S partials (block 0 writes the results of the rows that need no cut). The row's last block checks that
+// the window holds the cut (mass above < P = ceil(top_p Z) <= mass above + window mass), finds the exact top-p key
+// among the window's tokens, adds the kept ones to their tiles and draws. A row marked for the radix path (top-k with a
+// cut, an infinite maximum or 1/T), or without a window, is taken by its first block (the single-block path,
+// full_row); a row whose window held more than CAP tokens or missed the cut, by its last block.
 template <int DT, bool COUNTS, bool MASK>
 __global__ void __launch_bounds__(NTF) fs_collect_k(const void* __restrict__ logits, long long stride, int vocab,
                                                     const int* __restrict__ counts, const u32* __restrict__ mask,
@@ -1165,15 +1391,19 @@ __global__ void __launch_bounds__(NTF) fs_collect_k(const void* __restrict__ log
     __shared__ u32 s_off[FS_MAX_SPLITS + 1];
     __shared__ unsigned s_flag;
     __shared__ int s_sel;
+    __shared__ u64 s_rec[4];            // the row's maximum key, state, log-sum-exp pair
+    __shared__ u64 s_z[3];              // exact total, mass above the window, window mass
+    __shared__ int s_w[3];              // the window's bins r_lo, r_hi; state
+    __shared__ double s_u[2 * NUNITS + 2], s_wd[2];
+    __shared__ u32 s_fc[WIN_UNITS * BINS_PER_UNIT];
+    __shared__ u64 s_cx[3];
     const int S = gridDim.x, sp = blockIdx.x, wr = blockIdx.y;
     if (flags && wr >= DEFER_ROWS) {
-        // the flagged rows past the workspace's, shared out over this row of blocks, each taken whole
+        // the flagged rows past the workspace's, shared out over this row of blocks: each is marked for fs_fallback_k
         for (int k = DEFER_ROWS + sp;; k += S) {
             const int q = fs_row(flags, rows, k, &s_sel);
             if (q < 0) break;
-            full_row<DT, COUNTS, MASK>(logits, stride, vocab, counts, mask, params, uniforms, vec, out_ids, out_greedy, out_probs,
-                                       out_logprobs, out_status, q, sh);
-            __syncthreads();
+            if (threadIdx.x == 0) ws.fallback()[q] = 1u;
         }
         return;
     }
@@ -1182,48 +1412,102 @@ __global__ void __launch_bounds__(NTF) fs_collect_k(const void* __restrict__ log
     const int tid = threadIdx.x, w = tid / WAVE, l = lane_id();
     const RowParamsDev p = params[r];
     const float u = uniforms[r];
-    const FsRow* row = &ws.rows[r];
-    const u32 state0 = ld_agent(&row->state);
-    if (state0 == FS_RADIX) {
-        // marked by pass 0 (top-k with a cut, an infinite maximum or 1/T): the row's first block takes the radix path
-        if (sp == 0)
-            full_row<DT, COUNTS, MASK>(logits, stride, vocab, counts, mask, params, uniforms, vec, out_ids, out_greedy, out_probs,
-                                       out_logprobs, out_status, r, sh);
-        return;
-    }
-    if (state0 != FS_CUT) return;
-    const Row<DT, COUNTS, MASK> R = make_row<DT, COUNTS, MASK>(logits, stride, vocab, counts, mask, p, vec, r);
-    const u64 top = ld_agent(&row->top);
-    const float M = okey_to_f32(key_ok(top));
     const float c2 = temp_scale(p.temperature);
     const bool topp = p.top_p > 0.0f && p.top_p < 1.0f;
-    // the log-sum-exp, for the last block's log-probability
-    const float lse_m = __uint_as_float(ld_agent((const u32*)&row->lse_m));
-    const float lse_s = __uint_as_float(ld_agent((const u32*)&row->lse_s));
     const u64 Q = p.min_p > 0.0f ? mul_ceil64(p.min_p, MASS_ONE) : 0ull;
     const int ntiles = (vocab + TILE - 1) / TILE;
     const int t0 = sp * tpb, t1 = min(ntiles, t0 + tpb);
-    // The crossing bin b*, while the first loads are in flight: the blocks' sums per unit of y give the total, P and
-    // the unit where the cumulative mass from the top reaches P; that unit's 128 bins summed over the blocks give b*
-    // and the mass above it. No top-p: no cut (every bin is above b* = NBINS).
-    __shared__ u64 s_units[NUNITS], s_fine[BINS_PER_UNIT], s_cx[3];
-    u32 bstar = NBINS;
-    u64 above = 0, P = 0;
-    auto crossing = [&]() {
-        if (topp) {
-            for (int i = tid; i < NUNITS; i += NTF) s_units[i] = 0;
-            for (int i = tid; i < BINS_PER_UNIT; i += NTF) s_fine[i] = 0;
+    const Row<DT, COUNTS, MASK> R = make_row<DT, COUNTS, MASK>(logits, stride, vocab, counts, mask, p, vec, r);
+    if (!flags && params_invalid(p, u)) {
+        if (sp == 0 && tid == 0) fs_out(r, -1, -1, GBS_ROW_INVALID_PARAMS, 0.f, 0.f, out_ids, out_greedy, out_probs, out_logprobs, out_status);
+        return;
+    }
+    // The row's record and window, while the first loads are in flight.
+    float M = 0.f, lse_m = 0.f, lse_s = 0.f;
+    u64 top = 0;
+    int r_lo = NBINS, r_hi = NBINS - 1;  // the window's bins (none: every bin is above it)
+    u32 state = FS_CUT;
+    auto prepare = [&]() -> bool {
+        if (tid == 0) {
+            s_ncol = 0;
+            s_z[0] = s_z[1] = s_z[2] = 0;
         }
-        if (tid == 0) s_ncol = 0;
         for (int i = tid; i < (t1 - t0) * NWF; i += NTF) s_tilew[i / NWF][i % NWF] = 0;
-        __syncthreads();
-        if (!topp) return;
-        const u64* U = ws.units + (size_t)wr * S * NUNITS;
-        for (int i = tid; i < S * NUNITS; i += NTF) {
-            const u64 v = ld_agent(&U[i]);
-            if (v) atomicAdd((unsigned long long*)&s_units[i % NUNITS], (unsigned long long)v);
+        if (flags) {
+            // the record, and (rows with top-p) fs_hist_k's sums per unit of y over the blocks, in block order
+            if (tid == 0) {
+                const FsRow* row = &ws.rec()[r];
+                s_rec[0] = ld_prev(&row->top);
+                s_rec[1] = ld_prev(&row->state);
+                s_rec[2] = ld_prev((const u32*)&row->lse_m);
+                s_rec[3] = ld_prev((const u32*)&row->lse_s);
+            } else if (topp && tid >= WAVE && tid < WAVE + NUNITS) {
+                const u64* U = ws.units() + (size_t)wr * S * NUNITS + (tid - WAVE);
+                u64 v = 0;
+                v = sum_blocks<u64>(S, [&](int o) { return ld_prev(&U[(size_t)o * NUNITS]); });
+                ((u64*)s_u)[tid - WAVE] = v;
+            }
+        } else if (tid >= WAVE) {
+            if (topp) fs_window_load(ws, wr, S, s_u);
+        } else {
+            // the record from pass 0's partials (every block of the row makes the same one)
+            const float clp = fs_clp(p);
+            u64 k = 0;
+            u32 nn = 0, na = 0;
+            Lse rl{-INFINITY, 0.f};
+            for (int o = l; o < S; o += WAVE) {
+                const FsPart0 pt = ld_prev(&ws.p0()[(size_t)wr * S + o]);  // the whole partial in one round of loads
+                k = pt.key > k ? pt.key : k;
+                nn |= pt.nan;
+                na += pt.nallowed;
+                rl = lse_merge(rl, Lse{pt.m, pt.s}, clp);
+            }
+            k = wave_max_u64(k);
+            nn = wave_or(nn);
+            na = wave_sum_u32(na);
+            rl = wave_lse(rl, clp);
+            const float Mk = okey_to_f32(key_ok(k));
+            u32 st = FS_CUT;
+            if (nn || na == 0 || p.temperature == 0.0f) st = FS_DONE;
+            else if ((p.top_k > 0 && (u32)p.top_k < na) || !mass_fast_ok(Mk, c2)) st = FS_RADIX;
+            if (l == 0) {
+                s_rec[0] = k;
+                s_rec[1] = st;
+                s_rec[2] = __float_as_uint(rl.m);
+                s_rec[3] = __float_as_uint(rl.s);
+                if (sp == 0) {
+                    const int greedy = (int)key_id(k);
+                    if (nn)
+                        fs_out(r, -1, -1, GBS_ROW_NAN_LOGIT, 0.f, 0.f, out_ids, out_greedy, out_probs, out_logprobs, out_status);
+                    else if (na == 0)
+                        fs_out(r, -1, -1, GBS_ROW_NO_CANDIDATES, 0.f, 0.f, out_ids, out_greedy, out_probs, out_logprobs, out_status);
+                    else if (p.temperature == 0.0f)
+                        fs_out(r, greedy, greedy, GBS_ROW_OK, 1.0f, fs_logprob(Mk, Mk, clp, rl.m, rl.s), out_ids, out_greedy, out_probs,
+                               out_logprobs, out_status);
+                }
+            }
         }
         __syncthreads();
+        top = s_rec[0];
+        state = (u32)s_rec[1];
+        lse_m = __uint_as_float((u32)s_rec[2]);
+        lse_s = __uint_as_float((u32)s_rec[3]);
+        M = okey_to_f32(key_ok(top));
+        if (state != FS_CUT || !topp) return state == FS_CUT;
+        if (!flags) {
+            if (!fs_window(ws.hist(), wr, S, M, c2, p.top_p, lse_m, lse_s, s_u, s_fc, s_w, s_wd)) {
+                state = FS_WINDOW_FAIL;
+                return false;
+            }
+            r_lo = s_w[0];
+            r_hi = s_w[1];
+            return true;
+        }
+        // under per-row dispatch: the crossing bin b* of fs_hist_k's exact histograms (the blocks' sums per unit of y
+        // give the total, P and the unit where the cumulative mass from the top reaches P; that unit's 128 bins summed
+        // over the blocks give b*)
+        const u64* const s_units = (const u64*)s_u;
+        u64* const s_fine = (u64*)s_fc;
         if (tid < WAVE) {
             const u64 v = l < NUNITS ? s_units[l] : 0ull;
             const u64 Z = wave_sum_u64(v);
@@ -1238,10 +1522,11 @@ __global__ void __launch_bounds__(NTF) fs_collect_k(const void* __restrict__ log
         }
         __syncthreads();
         const int ustar = (int)s_cx[0];
-        const u64* H = ws.hist + (size_t)wr * S * NBINS + (size_t)ustar * BINS_PER_UNIT;
-        for (int i = tid; i < S * BINS_PER_UNIT; i += NTF) {
-            const u64 v = ld_agent(&H[(size_t)(i / BINS_PER_UNIT) * NBINS + (i % BINS_PER_UNIT)]);
-            if (v) atomicAdd((unsigned long long*)&s_fine[i % BINS_PER_UNIT], (unsigned long long)v);
+        if (tid < BINS_PER_UNIT) {
+            const u64* H = ws.hist() + (size_t)wr * S * NBINS + (size_t)ustar * BINS_PER_UNIT + tid;
+            u64 v = 0;
+            v = sum_blocks<u64>(S, [&](int o) { return ld_prev(&H[(size_t)o * NBINS]); });
+            s_fine[tid] = v;
         }
         __syncthreads();
         if (tid < WAVE) {
@@ -1251,48 +1536,37 @@ __global__ void __launch_bounds__(NTF) fs_collect_k(const void* __restrict__ log
             const u64 incl = s_cx[1] + wave_scan_u64(a0 + a1);
             const u64 excl = incl - a0 - a1;
             const int f = (int)__builtin_ctzll(ballot(incl >= Pv) | (1ull << 63));
-            if (l == f) {
-                const bool first = excl + a0 >= Pv;
-                s_cx[0] = (u64)(ustar * BINS_PER_UNIT + 2 * l + (first ? 0 : 1));
-                s_cx[1] = first ? excl : excl + a0;
-            }
+            if (l == f) s_cx[0] = (u64)(ustar * BINS_PER_UNIT + 2 * l + (excl + a0 >= Pv ? 0 : 1));
         }
         __syncthreads();
-        bstar = (u32)s_cx[0];
-        above = s_cx[1];
-        P = s_cx[2];
+        r_lo = r_hi = (int)s_cx[0];
+        return true;
     };
-    // kept masses of the bins above b* per tile (per-step partials); the tokens of bin b* into LDS
-    u64 sacc = 0;
+    // per token: the exact mass into the total; above the window (kept: mass >= the min-p floor) into the tile's
+    // partial, and into the mass above when there is a floor (else the mass above is the tiles' sum); in the window
+    // into the wave's part of the LDS collection (CAP / NWF keys per wave; a wave that overflows marks the block)
+    constexpr u32 WCAP = CAP / NWF;
+    u64 sacc = 0, zacc = 0, aacc = 0;
+    u32 wcount = 0;  // the wave's collected tokens (wave-uniform)
     auto collect_group = [&](int t, int e, const float (&lv)[4]) {
         u64 s = 0;
-        u64 Eq[4];
-        bool col[4];
-        int ncol = 0;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            Eq[q] = mass_fast(lv[q], M, c2);
-            const u32 b = topp ? bin_of(lv[q], M, c2) : 0u;
-            const bool ok = valid_l(lv[q]);
-            if (ok && b < bstar && Eq[q] >= Q) s += Eq[q];
-            col[q] = ok && b == bstar;
-            ncol += col[q] ? 1 : 0;
-        }
-        if (ballot(ncol > 0)) {
-            const u64 inc = wave_scan_u64((u64)ncol);
-            u32 base = 0;
-            if (l == WAVE - 1) base = atomicAdd(&s_ncol, (u32)inc);
-            base = (u32)__builtin_amdgcn_readlane((int)base, WAVE - 1);
-            u32 idx = base + (u32)(inc - (u64)ncol);
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                if (col[q]) {
-                    if (idx < (u32)CAP) {
-                        s_key[idx] = make_key(okey_f32(lv[q]), (u32)(e + q));
-                        s_mass[idx] = Eq[q];
-                    }
-                    ++idx;
+            const u64 E = mass_fast(lv[q], M, c2);  // 0 for -inf
+            const int b = topp ? (int)bin_of(lv[q], M, c2) : 0;
+            zacc += E;
+            const bool above = b < r_lo;
+            s += above && E >= Q ? E : 0ull;
+            if (Q) aacc += above ? E : 0ull;
+            const bool col = valid_l(lv[q]) && !above && b <= r_hi;
+            const u64 mk = ballot(col);
+            if (mk) {
+                const u32 idx = wcount + mbcnt(mk);
+                if (col && idx < WCAP) {
+                    s_key[w * WCAP + idx] = make_key(okey_f32(lv[q]), (u32)(e + q));
+                    s_mass[w * WCAP + idx] = E;
                 }
+                wcount += (u32)__popcll(mk);
             }
         }
         sacc += s;
@@ -1303,32 +1577,76 @@ __global__ void __launch_bounds__(NTF) fs_collect_k(const void* __restrict__ log
         sacc = 0;
     };
 #if GBS_FS_STEPS
-    stream_steps<SG, GBS_FS_AUXC>(R, t0, t1, collect_group, collect_step, crossing);
+    stream_steps<SG, GBS_FS_AUXC>(R, t0, t1, collect_group, collect_step, prepare);
 #else
-    crossing();
-    stream_tiles(R, t0, t1, [&](int t, int e, const float (&lv)[4]) {
-        collect_group(t, e, lv);
-        collect_step(t, w);
-    });
+    if (prepare())
+        stream_tiles(R, t0, t1, [&](int t, int e, const float (&lv)[4]) {
+            collect_group(t, e, lv);
+            collect_step(t, w);
+        });
 #endif
+    if (state != FS_CUT) {
+        // marked for the radix path, or no window: the row's first block marks it for fs_fallback_k
+        if ((state == FS_RADIX || state == FS_WINDOW_FAIL) && sp == 0 && tid == 0) ws.fallback()[r] = 1u;
+        return;
+    }
+    // the block's totals (exact total, mass above when there is a floor, window mass) and the waves' collections, packed
+    // in wave order into the workspace (a block whose wave overflowed counts CAP + 1 tokens)
+    __shared__ u32 s_wc[NWF];
+    {
+        u64 wm = 0;
+        const u32 mine = wcount < WCAP ? wcount : WCAP;
+        for (u32 i = l; i < mine; i += WAVE) wm += s_mass[w * WCAP + i];
+        const u64 z = wave_sum_u64(zacc), a = wave_sum_u64(aacc);
+        wm = wave_sum_u64(wm);
+        if (l == 0) {
+            atomicAdd((unsigned long long*)&s_z[0], (unsigned long long)z);
+            atomicAdd((unsigned long long*)&s_z[1], (unsigned long long)a);
+            atomicAdd((unsigned long long*)&s_z[2], (unsigned long long)wm);
+            s_wc[w] = wcount;
+        }
+    }
     __syncthreads();
     for (int t = t0 + tid; t < t1; t += NTF) {
         u64 v = 0;
 #pragma unroll
         for (int k = 0; k < NWF; ++k) v += s_tilew[t - t0][k];
-        st_agent(&ws.tiles[(size_t)wr * ntiles + t], v);
+        st_agent(&ws.tiles()[(size_t)wr * ntiles + t], v);
     }
-    const u32 nb = s_ncol;
     const size_t slot = (size_t)wr * S + sp;
-    if (tid == 0) st_agent(&ws.ccount[slot], nb);
-    for (u32 i = tid; i < nb && i < (u32)CAP; i += NTF) {
-        st_agent(&ws.ckey[slot * CAP + i], s_key[i]);
-        st_agent(&ws.cmass[slot * CAP + i], s_mass[i]);
+    {
+        u32 before = 0, nb = 0;
+        bool over = false;
+        for (int o = 0; o < NWF; ++o) {
+            before += o < w ? s_wc[o] : 0u;
+            nb += s_wc[o];
+            over |= s_wc[o] > WCAP;
+        }
+        const u32 mine = wcount < WCAP ? wcount : WCAP;
+        for (u32 i = l; i < mine; i += WAVE) {
+            st_agent(&ws.ckey()[slot * CAP + before + i], s_key[w * WCAP + i]);
+            st_agent(&ws.cmass()[slot * CAP + before + i], s_mass[w * WCAP + i]);
+        }
+        if (tid == 0) {
+            st_agent(&ws.ccount()[slot], over ? (u32)CAP + 1u : nb);
+            st_agent(&ws.zab()[slot * 4 + 0], s_z[0]);
+            st_agent(&ws.zab()[slot * 4 + 1], s_z[1]);
+            st_agent(&ws.zab()[slot * 4 + 2], s_z[2]);
+        }
     }
-    if (!arrive_last(&ws.cnt2[r], (unsigned)S, &s_flag)) return;
-    // ---- the row's last block: gather the collected tokens (or hand the row to the radix path)
-    // the blocks' counts (one load per thread), then their offsets
-    if (tid < S) s_off[tid + 1] = ld_agent(&ws.ccount[(size_t)wr * S + tid]);
+    if (!arrive_last(&ws.cnt2()[r], (unsigned)S, &s_flag)) return;
+    // ---- the row's last block: the totals and the blocks' counts (one load each per thread), then their offsets
+    if (tid == 0) s_z[0] = s_z[1] = s_z[2] = 0;
+    __syncthreads();
+    if (tid < S) {  // all four loads in flight before any is used
+        const u32 cnt = ld_agent(&ws.ccount()[(size_t)wr * S + tid]);
+        const u64* zb = &ws.zab()[((size_t)wr * S + tid) * 4];
+        const u64 z0 = ld_agent(&zb[0]), z1 = ld_agent(&zb[1]), z2 = ld_agent(&zb[2]);
+        s_off[tid + 1] = cnt;
+        atomicAdd((unsigned long long*)&s_z[0], (unsigned long long)z0);
+        atomicAdd((unsigned long long*)&s_z[1], (unsigned long long)z1);
+        atomicAdd((unsigned long long*)&s_z[2], (unsigned long long)z2);
+    }
     __syncthreads();
     if (tid == 0) {
         u32 off = 0;
@@ -1340,31 +1658,44 @@ __global__ void __launch_bounds__(NTF) fs_collect_k(const void* __restrict__ log
     }
     __syncthreads();
     const u32 n = s_off[S];
-    if (n > (u32)CAP) {  // every block's count is at most the total: no block overflowed unless the total did
-        // more tokens in the crossing bin than the collection holds: this block takes the radix path for the row
-        full_row<DT, COUNTS, MASK>(logits, stride, vocab, counts, mask, params, uniforms, vec, out_ids, out_greedy, out_probs,
-                                   out_logprobs, out_status, r, sh);
+    const u64 Ztot = s_z[0], wmass = s_z[2];
+    const u64 P = topp ? mul_ceil64(p.top_p, Ztot) : 0ull;
+    // collected token i is block o's token i - s_off[o], with s_off[o] <= i < s_off[o + 1] (a binary search): all of
+    // them in one round of loads, with the tiles' kept masses
+    if (n <= (u32)CAP) {
+        for (u32 i = tid; i < n; i += NTF) {
+            int lo = 0, hi = S;
+            while (hi - lo > 1) {
+                const int mid = (lo + hi) >> 1;
+                if (s_off[mid] <= i) lo = mid;
+                else hi = mid;
+            }
+            const size_t src = ((size_t)wr * S + lo) * CAP + (i - s_off[lo]);
+            s_key[i] = ld_agent(&ws.ckey()[src]);
+            s_mass[i] = ld_agent(&ws.cmass()[src]);
+        }
+    }
+    for (int t = tid; t < ntiles; t += NTF) s_tile[t] = ld_agent(&ws.tiles()[(size_t)wr * ntiles + t]);
+    __syncthreads();
+    if (Q == 0 && topp) {  // no floor: the mass above the window is the tiles' sum
+        if (tid < WAVE) {
+            u64 a = 0;
+            for (int t = l; t < ntiles; t += WAVE) a += s_tile[t];
+            a = wave_sum_u64(a);
+            if (l == 0) s_z[1] = a;
+        }
+        __syncthreads();
+    }
+    const u64 above = s_z[1];
+    if (n > (u32)CAP || (topp && !(above < P && P <= above + wmass))) {
+        // more tokens in the window than the collection holds, or the window missed the cut: fs_fallback_k takes the row
+        if (tid == 0) ws.fallback()[r] = 1u;
         return;
     }
-    // collected token i is block o's token i - s_off[o], with s_off[o] <= i < s_off[o + 1] (a binary search): all of
-    // them in one round of loads
-    for (u32 i = tid; i < n; i += NTF) {
-        int lo = 0, hi = S;
-        while (hi - lo > 1) {
-            const int mid = (lo + hi) >> 1;
-            if (s_off[mid] <= i) lo = mid;
-            else hi = mid;
-        }
-        const size_t src = ((size_t)wr * S + lo) * CAP + (i - s_off[lo]);
-        s_key[i] = ld_agent(&ws.ckey[src]);
-        s_mass[i] = ld_agent(&ws.cmass[src]);
-    }
-    for (int t = tid; t < ntiles; t += NTF) s_tile[t] = ld_agent(&ws.tiles[(size_t)wr * ntiles + t]);
-    __syncthreads();
     u64 kp = (u64)VALID_MIN_OK << 32;  // every valid key
     if (topp) {
         // the top-p key among the collected tokens of bin b*
-        kp = cut_collected(s_key, s_mass, n, above, P, M, c2, bstar, sh.cnt, s_bc);
+        kp = cut_collected(s_key, s_mass, n, above, P, M, c2, r_lo, r_hi, sh.cnt, s_bc);
         for (u32 j = tid; j < n; j += NTF) {
             const u64 E = s_mass[j];
             if (s_key[j] >= kp && E >= Q) atomicAdd((unsigned long long*)&s_tile[key_id(s_key[j]) / TILE], (unsigned long long)E);
@@ -1426,17 +1757,21 @@ __global__ void __launch_bounds__(NTF) fs_collect_k(const void* __restrict__ log
     for (int o = 0; o < w; ++o) wbase += s_red[o];
     const u64 excl = wbase + incl - mine;
     if (excl <= target && target < excl + mine) {
-        u64 acc = excl;
+        // the first of the thread's four elements whose running mass exceeds the target (selections, no indexing)
+        u64 acc = excl, ef = 0;
+        int qf = -1;
+        float lf = 0.f;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             acc += em[q];
-            if (acc > target) {
-                s_bc[1] = (u64)(e + q);
-                s_bc[2] = em[q];
-                s_bc[3] = __float_as_uint(lv[q]);
-                break;
-            }
+            const bool hit = qf < 0 && acc > target;
+            qf = hit ? q : qf;
+            ef = hit ? em[q] : ef;
+            lf = hit ? lv[q] : lf;
         }
+        s_bc[1] = (u64)(e + qf);
+        s_bc[2] = ef;
+        s_bc[3] = __float_as_uint(lf);
     }
     __syncthreads();
     if (tid == 0) {
@@ -1477,13 +1812,18 @@ int launch_sample_full(const void* logits, int dtype, int rows, int stride, int 
         if (split) {
             const dim3 grid(pl.S, row_flags ? DEFER_ROWS + 1 : rows);
             // flagged rows: the single-pass kernel has written their records (maximum, log-sum-exp, state), so no pass 0
+            // without per-row dispatch pass 0 (maximum, log-sum-exp, counts on the row's grid) and the collection; under
+            // it the single-pass kernel has written the flagged rows' records, and the exact histogram gives the window
             if (!row_flags)
                 hipLaunchKernelGGL((fs_pass0_k<D, C, Mk>), grid, dim3(NTF), 0, st, logits, (long long)stride, vocab, counts, mask, p, uniforms,
                                    vec, pl.tpb, w);
-            hipLaunchKernelGGL((fs_hist_k<D, C, Mk>), grid, dim3(NTF), 0, st, logits, (long long)stride, vocab, counts, mask, p, uniforms,
-                               vec, pl.tpb, w, out_ids, out_greedy, out_probs, out_logprobs, out_status, row_flags, rows);
+            else
+                hipLaunchKernelGGL((fs_hist_k<D, C, Mk>), grid, dim3(NTF), 0, st, logits, (long long)stride, vocab, counts, mask, p, vec,
+                                   pl.tpb, w, row_flags, rows);
             hipLaunchKernelGGL((fs_collect_k<D, C, Mk>), grid, dim3(NTF), 0, st, logits, (long long)stride, vocab, counts, mask, p,
                                uniforms, vec, pl.tpb, w, out_ids, out_greedy, out_probs, out_logprobs, out_status, row_flags, rows);
+            hipLaunchKernelGGL((fs_fallback_k<D, C, Mk>), dim3(rows), dim3(NTF), 0, st, logits, (long long)stride, vocab, counts, mask,
+                               p, uniforms, vec, out_ids, out_greedy, out_probs, out_logprobs, out_status, w.fallback());
         }
         else
             hipLaunchKernelGGL((sample_full_k<D, C, Mk>), dim3(rows), dim3(NTF), 0, st, logits, (long long)stride, vocab, counts, mask,

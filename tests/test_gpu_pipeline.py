@@ -339,6 +339,37 @@ def test_full_path_binned_cut_edges():
     compare(g, w, "config3 full size")
 
 
+def test_full_path_collection_window_edges():
+    """The split full path's collection window, made from pass 0's counts on a grid set by the row's first tile: a first
+    tile far below the row's maximum (the grid's top bin holds most of the row), a first tile with no allowed token, a
+    maximum in the first tile far above the rest (the cut at the top), a flat row (the window overflows: the single-block
+    path), min-p with a floor, penalties and masks, f32 and bf16."""
+    need_gpu()
+    rng = np.random.default_rng(41)
+    B, V = 10, 61_440
+    x = (rng.standard_normal((B, V)) * 1.5).astype(np.float32)
+    x[0, :4096] -= 30.0
+    x[1, :4096] = -np.inf
+    x[2, 17] = 40.0
+    x[3] = 0.25
+    x[4, 5000:5100] = 9.0
+    counts = np.zeros((B, V), dtype=np.int32)
+    counts[5:8, rng.choice(V, 3000, replace=False)] = rng.integers(1, 5, 3000)
+    mask = np.full((B, (V + 31) // 32), 0xFFFFFFFF, dtype=np.uint32)
+    mask[6, :128] = 0          # the first tile masked
+    mask[7, ::3] = 0x0F0F0F0F
+    p = S.row_params(B, temperature=0.8, top_p=0.9, min_p=0.0, top_k=0, repetition=1.1, presence=0.5, frequency=0.3)
+    p["min_p"][8] = 0.02
+    p["top_p"][9] = 0.3
+    u = W.uniforms_f32(43, B)
+    for dtype in ("f32", "bf16"):
+        xx = x if dtype == "f32" else (x.view(np.uint32) >> 16).astype(np.uint16)
+        cfg = dict(logits=xx, dtype=dtype, params=p, uniforms=u, counts=counts, mask=mask)
+        log(f"window edges {dtype}")
+        g, w = run_both(cfg, kmax=0)
+        compare(g, w, f"window edges {dtype}")
+
+
 def test_full_and_fast_paths_alternate_on_one_workspace():
     """The fast path (kmax 64) and the split full path (kmax 0, fewer rows than CUs: several blocks per row, three
     launches with last-block hand-offs) share one workspace; their counters sit in one control region and every
