@@ -42,10 +42,10 @@ constexpr int NT = GBS_SPEC_NT;
 constexpr int TARGET_BLOCKS = GBS_SPEC_BLOCKS;
 constexpr int MIN_CHUNK = 2048;
 constexpr int U = GBS_SPEC_U;        // 4-element groups per thread in flight, per row
-constexpr int GSTEP = NT * 4;        // elements between a thread's groups (the draw)
 constexpr int DU = 4;                // the draw: 4-element groups per thread per tile
 constexpr int TILE = NT * 4 * DU;    // the draw: elements per tile
 constexpr int NWD = NT / WAVE;       // the draw: waves per block (one partial sum per wave and tile)
+constexpr int SUB = WAVE * 4 * DU;   // the draw: elements of a sub-tile (a wave's part of a tile)
 constexpr int DRAW_BLOCKS = 768;     // the draw: blocks in all (one round on the chip)
 #ifndef GBS_SPEC_ROWS_MIN
 #define GBS_SPEC_ROWS_MIN 192
@@ -91,7 +91,7 @@ struct SpecWs {
     u64* sumparts;           // [R][S][2]
     RowInfo* rows;           // [R]
     SeqInfo* seqs;           // [n_seq]
-    u128* wparts;            // [n_seq][tiles][DU][NWD]: the draw's sub-tile weights
+    u128* wparts;            // [n_seq][tiles][NWD]: the draw's sub-tile weights
 };
 
 // The counters that must be zero between launches sit at fixed offsets in the first SPEC_CTL_BYTES (room for 65535
@@ -116,7 +116,7 @@ Plan plan(int n_seq, int width, int vocab) {
     p.S3 = (tiles + p.tpb - 1) / p.tpb;
     p.bytes = SPEC_CTL_BYTES + align256((size_t)p.R * p.S * 16) + align256((size_t)p.R * p.S * 4) + align256((size_t)p.R * p.S * 16) +
               align256((size_t)p.R * sizeof(RowInfo)) + align256((size_t)n_seq * sizeof(SeqInfo)) +
-              align256((size_t)n_seq * tiles * DU * NWD * 16);
+              align256((size_t)n_seq * tiles * NWD * 16);
     return p;
 }
 
@@ -498,12 +498,12 @@ __device__ __forceinline__ u128 draw_weight(int mode, const float* tr, const flo
     return pair_weight(mode, tr[i], mode == 2 ? -INFINITY : dr[i], Mp, Mq, c2, zp, zq);
 }
 
-// sum of a u128 over the wave, in lane 0 (other lanes: partial sums)
+// sum of a u128 over the wave, in every lane (cross-lane moves by DPP and permlane swaps)
 __device__ __forceinline__ u128 wave_sum_u128(u128 v) {
     u64 lo = (u64)v, hi = (u64)(v >> 64);
 #pragma unroll
     for (int m = 1; m < WAVE; m <<= 1) {
-        const u64 olo = shfl_xor64(lo, m), ohi = shfl_xor64(hi, m);
+        const u64 olo = xor_lane64(lo, m), ohi = xor_lane64(hi, m);
         const u64 s = lo + olo;
         hi = hi + ohi + (s < lo ? 1ull : 0ull);
         lo = s;
@@ -644,11 +644,11 @@ __device__ __forceinline__ u128 block_scan_u128(u128 v, u128& total, u128* s_wt)
 // ---- launch 3: the draw ----
 // Grid (blocks per sequence, n_seq). The row that a sequence draws from (its first rejected row: the residual; or its
 // last row: the bonus from p) is cut into tiles of TILE elements; block b takes tiles [b * tpb, (b + 1) * tpb), the
-// next tile's loads in flight while one is summed. A wave covers 256 contiguous elements of a tile per 4-element group
-// index j, so the wave sums of (tile, j, wave) are the weights of consecutive 256-element sub-tiles: sub-tile
-// p = (tile * DU + j) * NWD + wave holds elements [256 p, 256 p + 256). The sequence's last block finds the sub-tile
-// that holds t = floor(u * total) by a block scan over them, then the element by a block scan over the sub-tile (one
-// element per thread).
+// next tile's loads in flight while one is summed. Wave w covers the SUB = 256 DU contiguous elements [w SUB, (w + 1)
+// SUB) of a tile (group j of a lane at j * 256 + 4 lane), so the wave sums of (tile, wave) are the weights of
+// consecutive SUB-element sub-tiles: sub-tile p = tile * NWD + wave holds elements [SUB p, SUB (p + 1)). The
+// sequence's last block finds the sub-tile that holds t = floor(u * total) by a block scan over them, then the element
+// by a block scan over the sub-tile (DU elements per thread).
 template <int MODE, bool FAST>
 __device__ __forceinline__ void draw_tiles(const float* tr, const float* dr, int vocab, int t0, int t1, bool vec, float Mp, float Mq,
                                            float c2, u64 zp, u64 zq, u128* wparts) {
@@ -657,7 +657,7 @@ __device__ __forceinline__ void draw_tiles(const float* tr, const float* dr, int
     auto issue = [&](int tile, float (&t)[DU * 4], float (&d)[DU * 4]) {
 #pragma unroll
         for (int j = 0; j < DU; ++j) {
-            const int e = tile * TILE + j * GSTEP + tid * 4;
+            const int e = tile * TILE + w * SUB + j * (WAVE * 4) + l * 4;
             if (vec) {
                 const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(rt, (u32)e * 4u, 0, 2);
                 u32x4 b = {0u, 0u, 0u, 0u};
@@ -686,21 +686,21 @@ __device__ __forceinline__ void draw_tiles(const float* tr, const float* dr, int
             d[i] = dn[i];
         }
         if (tile + 1 < t1) issue(tile + 1, tn, dn);
+        u128 part = 0;
 #pragma unroll
         for (int j = 0; j < DU; ++j) {
-            const int e = tile * TILE + j * GSTEP + tid * 4;
-            u128 part = 0;
+            const int e = tile * TILE + w * SUB + j * (WAVE * 4) + l * 4;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const bool in = e + q < vocab;  // buffer loads past the row's end return 0, not -inf
                 part += pair_weight<FAST>(MODE, in ? t[j * 4 + q] : -INFINITY, in ? d[j * 4 + q] : -INFINITY, Mp, Mq, c2, zp, zq);
             }
-            part = wave_sum_u128(part);
-            if (l == 0) {
-                u64* o = (u64*)&wparts[((size_t)tile * DU + j) * NWD + w];
-                st_agent(o, (u64)part);
-                st_agent(o + 1, (u64)(part >> 64));
-            }
+        }
+        part = wave_sum_u128(part);
+        if (l == 0) {
+            u64* o = (u64*)&wparts[(size_t)tile * NWD + w];
+            st_agent(o, (u64)part);
+            st_agent(o + 1, (u64)(part >> 64));
         }
     }
 }
@@ -716,7 +716,7 @@ __global__ void __launch_bounds__(NT) spec_draw_k(const float* __restrict__ targ
     __shared__ int s_tok;
     const int S = gridDim.x, sp = blockIdx.x, seq = blockIdx.y;
     const int tiles = (vocab + TILE - 1) / TILE;
-    const int nsub = tiles * DU * NWD;
+    const int nsub = tiles * NWD;
     const SeqInfo si = load_seq(ws.seqs, seq);
     const bool drawing = si.status == GBS_ROW_OK && si.mode != 0;
     const float* tr = target + (size_t)si.row * (size_t)stride;
@@ -739,7 +739,7 @@ __global__ void __launch_bounds__(NT) spec_draw_k(const float* __restrict__ targ
             s_tok = si.argmax;        // and draws the target's argmax
         }
         // thread k sums the sub-tiles [k * SPT, (k + 1) * SPT) (loaded in parallel); a block scan; t
-        constexpr int SPT = (128 * DU * NWD + NT - 1) / NT;  // sub-tiles per thread at the largest vocabulary
+        constexpr int SPT = ((GBS_MAX_VOCAB + TILE - 1) / TILE * NWD + NT - 1) / NT;  // sub-tiles per thread at the largest vocabulary
         u128 sub[SPT];
         u128 v = 0;
 #pragma unroll
@@ -767,16 +767,34 @@ __global__ void __launch_bounds__(NT) spec_draw_k(const float* __restrict__ targ
         __syncthreads();
         const int p = (int)s_flag;
         const u128 rem = s_rem;
-        // sub-tile p: one element per thread, coalesced; a block scan; the element whose range holds rem
-        const int e = p * NT + tid;
-        const bool in = p < nsub && e < vocab;
-        const float te = in ? tr[e] : -INFINITY;
-        const float de = (in && si.mode == 1) ? dr[e] : -INFINITY;
-        const u128 we = fast ? pair_weight<true>(si.mode, te, de, si.Mp, si.Mq, si.c2, si.zp, si.zq)
-                             : pair_weight(si.mode, te, de, si.Mp, si.Mq, si.c2, si.zp, si.zq);
+        // sub-tile p: DU consecutive elements per thread; a block scan of the threads' sums; the element whose range holds
+        // rem (selections, no indexing)
+        static_assert(SUB == NT * DU, "a sub-tile is DU elements per thread");
+        const int e0 = p * SUB + tid * DU;
+        u128 we[DU], wsum = 0;
+#pragma unroll
+        for (int q = 0; q < DU; ++q) {
+            const int e = e0 + q;
+            const bool in = p < nsub && e < vocab;
+            const float te = in ? tr[e] : -INFINITY;
+            const float de = (in && si.mode == 1) ? dr[e] : -INFINITY;
+            we[q] = fast ? pair_weight<true>(si.mode, te, de, si.Mp, si.Mq, si.c2, si.zp, si.zq)
+                         : pair_weight(si.mode, te, de, si.Mp, si.Mq, si.c2, si.zp, si.zq);
+            wsum += we[q];
+        }
         u128 sub_total;
-        const u128 before = block_scan_u128(we, sub_total, s_wt);
-        if (p < nsub && we != 0 && before <= rem && rem - before < we) s_tok = e;
+        const u128 before = block_scan_u128(wsum, sub_total, s_wt);
+        if (p < nsub && wsum != 0 && before <= rem && rem - before < wsum) {
+            u128 acc = before;
+            int qf = -1;
+#pragma unroll
+            for (int q = 0; q < DU; ++q) {
+                const bool hit = qf < 0 && rem - acc < we[q];
+                qf = hit ? q : qf;
+                acc += qf < 0 ? we[q] : (u128)0;
+            }
+            s_tok = e0 + qf;
+        }
         __syncthreads();
         token = s_tok;
     }
