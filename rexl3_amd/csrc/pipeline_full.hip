@@ -470,6 +470,117 @@ __device__ u64 cut_collected(const u64* keys, const u64* masses, u32 n, u64 abov
     return kp;
 }
 
+// The same cut on one wave (the other waves of the block take no part): the sub-bins' histogram by LDS atomics, the
+// crossing sub-bin by a wave scan, its tokens compacted by ballots, and the comparison among them. Returns the key in
+// every lane. LDS as cut_collected.
+__device__ u64 cut_collected_wave(const u64* keys, const u64* masses, u32 n, u64 above, u64 P, float M, float c2, int r_lo,
+                                  int r_hi, u32* s_cnt) {
+    const int l = lane_id();
+    u64* const s_sub = (u64*)s_cnt;
+    u32* const s_list = s_cnt + 2 * NSUB;
+    const float scale = (float)NSUB / (float)(r_hi - r_lo + 1);
+    auto sub_of = [&](u64 key) {
+        const float y = (okey_to_f32(key_ok(key)) - M) * c2;
+        return (u32)fminf(fmaxf((-y * (float)BINS_PER_UNIT - (float)r_lo) * scale, 0.0f), (float)(NSUB - 1));
+    };
+#pragma unroll
+    for (int q = 0; q < NSUB / WAVE; ++q) s_sub[q * WAVE + l] = 0;
+    for (u32 i = l; i < n; i += WAVE) atomicAdd((unsigned long long*)&s_sub[sub_of(keys[i])], (unsigned long long)masses[i]);
+    // lane i holds sub-bins 4i .. 4i + 3
+    u64 m4[4], tot = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        m4[q] = s_sub[4 * l + q];
+        tot += m4[q];
+    }
+    const u64 incl = above + wave_scan_u64(tot);
+    const int f = (int)__builtin_ctzll(ballot(incl >= P) | (1ull << 63));
+    u64 acc = incl - tot;
+    int q0 = 0;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        if (q0 == k && acc + m4[k] < P) {
+            acc += m4[k];
+            q0 = k + 1;
+        }
+    }
+    const u32 sstar = (u32)__builtin_amdgcn_readlane(4 * l + q0, f);
+    const u64 base = readlane64(acc, f);  // the mass above the crossing sub-bin
+    // its tokens, in order of the collection
+    u32 m = 0;
+    for (u32 i0 = 0; i0 < n; i0 += WAVE) {
+        const u32 i = i0 + (u32)l;
+        const bool in = i < n && sub_of(keys[i]) == sstar;
+        const u64 mk = ballot(in);
+        const u32 idx = m + mbcnt(mk);
+        if (in && idx < SUB_LIST_CAP) s_list[idx] = i;
+        m += (u32)__popcll(mk);
+    }
+    u64 kp = (u64)VALID_MIN_OK << 32;  // if none were found (cannot happen)
+    if (m <= SUB_LIST_CAP) {
+        for (u32 t0 = 0; t0 < m; t0 += WAVE) {
+            const u32 t = t0 + (u32)l;
+            bool hit = false;
+            u64 ki = 0;
+            if (t < m) {
+                const u32 i = s_list[t];
+                ki = keys[i];
+                u64 g = 0;
+                for (u32 v = 0; v < m; ++v) {
+                    const u32 j = s_list[v];
+                    g += keys[j] > ki ? masses[j] : 0ull;
+                }
+                hit = base + g < P && P <= base + g + masses[i];
+            }
+            const u64 hb = ballot(hit);
+            if (hb) kp = readlane64(ki, (int)__builtin_ctzll(hb));
+        }
+    } else {  // more tokens in one sub-bin than the list holds (equal values): compare them over the whole collection
+        for (u32 i0 = 0; i0 < n; i0 += WAVE) {
+            const u32 i = i0 + (u32)l;
+            bool hit = false;
+            u64 ki = 0;
+            if (i < n && sub_of(keys[i]) == sstar) {
+                ki = keys[i];
+                u64 g = 0;
+                for (u32 j = 0; j < n; ++j) g += (keys[j] > ki && sub_of(keys[j]) == sstar) ? masses[j] : 0ull;
+                hit = base + g < P && P <= base + g + masses[i];
+            }
+            const u64 hb = ballot(hit);
+            if (hb) kp = readlane64(ki, (int)__builtin_ctzll(hb));
+        }
+    }
+    return kp;
+}
+
+// Adds the kept collected tokens (key >= kp, mass >= Q) to their tiles' masses, on one wave. Collected tokens come in
+// runs of one tile (each wave of the collection appends in ascending element order), so the wave sums its 64 tokens
+// per run of equal tiles (a prefix sum over the lanes) and only a run's last lane adds to LDS: lanes do not contend for
+// one tile's address.
+// nw waves take part, this one as wave wi (chunks of 64 tokens wi, wi + nw, ...).
+__device__ __forceinline__ void add_kept_to_tiles_wave(const u64* keys, const u64* masses, u32 n, u64 kp, u64 Q, u64* s_tile, int wi = 0,
+                                                       int nw = 1) {
+    const int l = lane_id();
+    for (u32 j0 = (u32)wi * WAVE; j0 < n; j0 += (u32)nw * WAVE) {
+        const u32 j = j0 + (u32)l;
+        const bool in = j < n;
+        const u64 k = in ? keys[j] : 0ull, E = in ? masses[j] : 0ull;
+        const u64 v = in && k >= kp && E >= Q ? E : 0ull;
+        const int t = in ? (int)(key_id(k) / TILE) : -1;
+        const int tn = __shfl_down(t, 1, WAVE), tp = __shfl_up(t, 1, WAVE);
+        const bool last = in && (l == WAVE - 1 || tn != t);
+        const u64 starts = ballot(in && (l == 0 || tp != t));
+        const u64 incl = wave_scan_u64(v);
+        // the run's first lane s: the highest start at or below this lane; the run's sum is incl(l) - incl(s - 1)
+        const u64 below = starts & (l == WAVE - 1 ? ~0ull : ((2ull << l) - 1ull));
+        const int st = below ? 63 - __builtin_clzll(below) : 0;
+        const u64 before = shfl64(incl, st > 0 ? st - 1 : 0);
+        const u64 run = incl - (st > 0 ? before : 0ull);
+        if (last && run) atomicAdd((unsigned long long*)&s_tile[t], (unsigned long long)run);
+    }
+}
+
+
 // One radix selection over the keys >= lb of the row: the key K at which the descending cumulative weight (count when
 // by_mass is false, mass otherwise) first reaches `target` -- weight(keys > K) < target <= weight(keys >= K).
 // With frac_p > 0 the target is ceil(frac_p * total weight), the total being the first pass's sum.
@@ -1635,82 +1746,102 @@ __global__ void __launch_bounds__(NTF) fs_collect_k(const void* __restrict__ log
         }
     }
     if (!arrive_last(&ws.cnt2()[r], (unsigned)S, &s_flag)) return;
-    // ---- the row's last block: the totals and the blocks' counts (one load each per thread), then their offsets
-    if (tid == 0) s_z[0] = s_z[1] = s_z[2] = 0;
-    __syncthreads();
-    if (tid < S) {  // all four loads in flight before any is used
-        const u32 cnt = ld_agent(&ws.ccount()[(size_t)wr * S + tid]);
-        const u64* zb = &ws.zab()[((size_t)wr * S + tid) * 4];
-        const u64 z0 = ld_agent(&zb[0]), z1 = ld_agent(&zb[1]), z2 = ld_agent(&zb[2]);
-        s_off[tid + 1] = cnt;
-        atomicAdd((unsigned long long*)&s_z[0], (unsigned long long)z0);
-        atomicAdd((unsigned long long*)&s_z[1], (unsigned long long)z1);
-        atomicAdd((unsigned long long*)&s_z[2], (unsigned long long)z2);
-    }
-    __syncthreads();
-    if (tid == 0) {
-        u32 off = 0;
-        s_off[0] = 0;
-        for (int o = 0; o < S; ++o) {
-            off += s_off[o + 1];
-            s_off[o + 1] = off;
+    // ---- the row's last block. Wave 0 loads the totals, the blocks' counts and the tiles' kept masses and checks the
+    // window; a collection of at most SMALL_N tokens is gathered and cut on wave 0 alone (no barriers), a larger one by
+    // the whole block. Then every wave scans the draw's tile.
+    constexpr u32 SMALL_N = 2 * WAVE;
+    if (w == 0) {
+        // lanes o and o + 64 (S <= 128): the blocks' counts and totals; the tiles (ntiles <= 128); all loads issued
+        // before any is used
+        const int o1 = l, o2 = l + WAVE;
+        const u32 c1 = o1 < S ? ld_agent(&ws.ccount()[(size_t)wr * S + o1]) : 0u;
+        const u32 c2v = o2 < S ? ld_agent(&ws.ccount()[(size_t)wr * S + o2]) : 0u;
+        u64 zz[2][3];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int o = h ? o2 : o1;
+            const u64* zb = &ws.zab()[((size_t)wr * S + o) * 4];
+#pragma unroll
+            for (int k = 0; k < 3; ++k) zz[h][k] = o < S ? ld_agent(&zb[k]) : 0ull;
+        }
+        const u64 tl1 = l < ntiles ? ld_agent(&ws.tiles()[(size_t)wr * ntiles + l]) : 0ull;
+        const u64 tl2 = l + WAVE < ntiles ? ld_agent(&ws.tiles()[(size_t)wr * ntiles + l + WAVE]) : 0ull;
+        if (l < ntiles) s_tile[l] = tl1;
+        if (l + WAVE < ntiles) s_tile[l + WAVE] = tl2;
+        // the blocks' offsets: an inclusive scan over o1 then o2
+        const u64 i1 = wave_scan_u64(c1), t1c = readlane64(i1, WAVE - 1);
+        const u64 i2 = t1c + wave_scan_u64(c2v);
+        if (l == 0) s_off[0] = 0;
+        if (o1 < S) s_off[o1 + 1] = (u32)i1;
+        if (o2 < S) s_off[o2 + 1] = (u32)i2;
+        const u64 nn = readlane64(i2, WAVE - 1);
+        const u32 n = nn > (u64)CAP ? (u32)CAP + 1u : (u32)nn;
+        const u64 Ztot = wave_sum_u64(zz[0][0] + zz[1][0]), wmass = wave_sum_u64(zz[0][2] + zz[1][2]);
+        u64 above = wave_sum_u64(zz[0][1] + zz[1][1]);
+        if (Q == 0 && topp) above = wave_sum_u64(tl1 + tl2);  // no floor: the mass above the window is the tiles' sum
+        const u64 P = topp ? mul_ceil64(p.top_p, Ztot) : 0ull;
+        const bool ok = n <= (u32)CAP && (!topp || (above < P && P <= above + wmass));
+        if (!ok && l == 0) ws.fallback()[r] = 1u;  // more tokens than the collection holds, or a missed cut: fs_fallback_k
+        if (l == 0) {
+            s_bc[1] = ok ? (u64)n : ~0ull;
+            s_bc[2] = above;
+            s_bc[3] = P;
         }
     }
     __syncthreads();
-    const u32 n = s_off[S];
-    const u64 Ztot = s_z[0], wmass = s_z[2];
-    const u64 P = topp ? mul_ceil64(p.top_p, Ztot) : 0ull;
-    // collected token i is block o's token i - s_off[o], with s_off[o] <= i < s_off[o + 1] (a binary search): all of
-    // them in one round of loads, with the tiles' kept masses
-    if (n <= (u32)CAP) {
-        for (u32 i = tid; i < n; i += NTF) {
-            int lo = 0, hi = S;
-            while (hi - lo > 1) {
-                const int mid = (lo + hi) >> 1;
-                if (s_off[mid] <= i) lo = mid;
-                else hi = mid;
-            }
-            const size_t src = ((size_t)wr * S + lo) * CAP + (i - s_off[lo]);
-            s_key[i] = ld_agent(&ws.ckey()[src]);
-            s_mass[i] = ld_agent(&ws.cmass()[src]);
+    if (s_bc[1] == ~0ull) return;
+    const u32 n = (u32)s_bc[1];
+    const u64 above = s_bc[2], P = s_bc[3];
+    // collected token i is block o's token i - s_off[o], s_off[o] <= i < s_off[o + 1] (a binary search)
+    auto fetch = [&](u32 i, u64& k, u64& m) {
+        int lo = 0, hi = S;
+        while (hi - lo > 1) {
+            const int mid = (lo + hi) >> 1;
+            if (s_off[mid] <= i) lo = mid;
+            else hi = mid;
         }
-    }
-    for (int t = tid; t < ntiles; t += NTF) s_tile[t] = ld_agent(&ws.tiles()[(size_t)wr * ntiles + t]);
-    __syncthreads();
-    if (Q == 0 && topp) {  // no floor: the mass above the window is the tiles' sum
-        if (tid < WAVE) {
-            u64 a = 0;
-            for (int t = l; t < ntiles; t += WAVE) a += s_tile[t];
-            a = wave_sum_u64(a);
-            if (l == 0) s_z[1] = a;
-        }
-        __syncthreads();
-    }
-    const u64 above = s_z[1];
-    if (n > (u32)CAP || (topp && !(above < P && P <= above + wmass))) {
-        // more tokens in the window than the collection holds, or the window missed the cut: fs_fallback_k takes the row
-        if (tid == 0) ws.fallback()[r] = 1u;
-        return;
-    }
+        const size_t src = ((size_t)wr * S + lo) * CAP + (i - s_off[lo]);
+        k = ld_agent(&ws.ckey()[src]);
+        m = ld_agent(&ws.cmass()[src]);
+    };
     u64 kp = (u64)VALID_MIN_OK << 32;  // every valid key
-    if (topp) {
-        // the top-p key among the collected tokens of bin b*
-        kp = cut_collected(s_key, s_mass, n, above, P, M, c2, r_lo, r_hi, sh.cnt, s_bc);
-        for (u32 j = tid; j < n; j += NTF) {
-            const u64 E = s_mass[j];
-            if (s_key[j] >= kp && E >= Q) atomicAdd((unsigned long long*)&s_tile[key_id(s_key[j]) / TILE], (unsigned long long)E);
+    if (n <= SMALL_N) {
+        if (w == 0) {
+            u64 kk[SMALL_N / WAVE], mm[SMALL_N / WAVE];
+#pragma unroll
+            for (int q = 0; q < (int)(SMALL_N / WAVE); ++q) {
+                kk[q] = mm[q] = 0;
+                const u32 i = q * WAVE + (u32)l;
+                if (i < n) fetch(i, kk[q], mm[q]);
+            }
+#pragma unroll
+            for (int q = 0; q < (int)(SMALL_N / WAVE); ++q) {
+                const u32 i = q * WAVE + (u32)l;
+                if (i < n) {
+                    s_key[i] = kk[q];
+                    s_mass[i] = mm[q];
+                }
+            }
+            if (topp) {
+                kp = cut_collected_wave(s_key, s_mass, n, above, P, M, c2, r_lo, r_hi, sh.cnt);
+                add_kept_to_tiles_wave(s_key, s_mass, n, kp, Q, s_tile);
+            }
         }
+    } else {
+        for (u32 i = tid; i < n; i += NTF) fetch(i, s_key[i], s_mass[i]);
+        __syncthreads();
+        kp = cut_collected(s_key, s_mass, n, above, P, M, c2, r_lo, r_hi, sh.cnt, s_bc);
+        add_kept_to_tiles_wave(s_key, s_mass, n, kp, Q, s_tile, w, NWF);
         __syncthreads();
     }
-    // ---- the draw: the tile that holds t (wave 0 scans the tiles' kept masses, 64 at a time), then its token (thread
-    // sums, a block scan, the owning thread's 4 elements)
-    if (tid < WAVE) {
+    if (w == 0) {
+        // the draw's tile: a scan of the tiles' kept masses, 64 at a time
         u64 zl = 0;
         for (int t = l; t < ntiles; t += WAVE) zl += s_tile[t];
-        const u64 zz = wave_sum_u64(zl);
-        const u64 tg = (u64)mul_floor(u, (u128)zz, nullptr);
+        const u64 zt = wave_sum_u64(zl);
+        const u64 tg = (u64)mul_floor(u, (u128)zt, nullptr);
         int ts = ntiles - 1;
-        u64 bf = zz - s_tile[ntiles - 1];
+        u64 bf = zt - s_tile[ntiles - 1];
         u64 run = 0;
         for (int c = 0; c < ntiles; c += WAVE) {
             const bool in = c + l < ntiles;
@@ -1726,13 +1857,15 @@ __global__ void __launch_bounds__(NTF) fs_collect_k(const void* __restrict__ log
             run = readlane64(incl, WAVE - 1);
         }
         if (l == 0) {
-            s_bc[4] = zz;
+            s_bc[0] = kp;
+            s_bc[4] = zt;
             s_bc[5] = tg;
             s_bc[6] = (u64)ts;
             s_bc[7] = bf;
         }
     }
     __syncthreads();
+    kp = s_bc[0];
     const u64 z = s_bc[4], target = s_bc[5], before = s_bc[7];
     const int tsel = (int)s_bc[6];
     auto kept_mass = [&](float v, int i) -> u64 {
