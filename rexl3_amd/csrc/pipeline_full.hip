@@ -228,9 +228,9 @@ __device__ __forceinline__ void stream_tiles(const Row<DT, COUNTS, MASK>& R, int
     }
 }
 
-// Streams tiles [t0, t1) in wave-steps: step k covers elements [t0 * TILE + k * WS, + WS), WS = G * 256, and wave w
-// takes steps w, w + NWF, ... (lane l's group j at + j * 256 + 4 l); the next step's G groups per lane are in flight
-// while a step is processed. The loads are issued whether or not their step exists (a step past the block's
+// Streams tiles [t0, t1) in wave-steps: step k covers elements [t0 * TILE + k * WS, + WS), WS = G * 256; wave w takes
+// step w, then the next unclaimed one (lane l's group j at + j * 256 + 4 l); the next step's G groups per lane are in
+// flight while a step is processed. The loads are issued whether or not their step exists (a step past the block's
 // last reads at an offset past the row's end, which the buffer range check turns into zeros without a memory access),
 // so every wait counts exactly the loads issued after the buffer it needs. f(t, e, l) is called per group and
 // fe(t, q) once per step (q: the step's place in its tile, below TILE / WS); f and fe must not hold block barriers.
@@ -294,16 +294,27 @@ __device__ __forceinline__ void stream_steps(const Row<DT, COUNTS, MASK>& R, int
         fe(t, k % SPT);
     };
     // one load site: the step's buffer is copied out once it has arrived, and the next step's loads go into it before
-    // the copy is used
+    // the copy is used. Wave w's first step is w. With four steps per wave or more, later steps go to whichever wave
+    // asks first (an LDS counter), so that waves the memory system serves late do not hold the block (config 3: 82.3 ->
+    // 79.4 us); with fewer, wave w takes w + NWF, w + 2 NWF, ... (the counter's barrier and round trips cost more than
+    // they balance).
+    const bool dyn = nsteps >= 4 * NWF;
+    __shared__ int s_next;
+    if (threadIdx.x == 0) s_next = NWF;
     Raw B[G];
     int k = w;
     load(k, B);
     if (!pre()) return;
+    if (dyn) __syncthreads();  // the counter is set
     while (k < nsteps) {
         Raw C[G];
 #pragma unroll
         for (int j = 0; j < G; ++j) C[j] = B[j];
-        const int kn = k + NWF;
+        int kn = k + NWF;
+        if (dyn) {
+            if (l == 0) kn = atomicAdd(&s_next, 1);
+            kn = __builtin_amdgcn_readfirstlane(kn);
+        }
         load(kn, B);
         use(k, C);
         k = kn;
