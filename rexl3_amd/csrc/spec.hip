@@ -8,11 +8,17 @@
 // exceeds t; after `width` acceptances the bonus token is drawn from p of the last row the same way. Temperature 0:
 // p is the argmax (ties to the lowest id).
 //
-// Three launches, each (splits, rows) with a last-block hand-off:
+// Two forms. With fewer rows than fill the chip (two-read form), three launches, each (splits, rows) with a last-block
+// hand-off:
 //   1. row maxima (order keys, so the argmax ties to the lowest id) and NaN flags of target and draft rows;
 //   2. the rows' integer mass sums; the last row of a sequence to finish decides the sequence's acceptances;
 //   3. the residual (or bonus) weights of the one row per sequence that needs a draw, per chunk; the last block finds the
 //      chunk that holds the draw and scans it.
+// With many rows (one-read form): one block per row reads it once for the maxima and float bounds on the mass sums,
+// which decide nearly every draft; an exact pass sums the masses of the rows that still need them (each drawing
+// sequence's draw row, and any row whose test the bounds left open); then launch 3.
+#include <cfloat>
+
 #include "gbs_modeu.hpp"
 
 using namespace gbs;
@@ -47,6 +53,10 @@ constexpr int TILE = NT * 4 * DU;    // the draw: elements per tile
 constexpr int NWD = NT / WAVE;       // the draw: waves per block (one partial sum per wave and tile)
 constexpr int SUB = WAVE * 4 * DU;   // the draw: elements of a sub-tile (a wave's part of a tile)
 constexpr int DRAW_BLOCKS = 768;     // the draw: blocks in all (one round on the chip)
+#ifndef GBS_SPEC_XNT
+#define GBS_SPEC_XNT 256
+#endif
+constexpr int XNT = GBS_SPEC_XNT;  // the one-read form's exact pass: threads per block
 #ifndef GBS_SPEC_ROWS_MIN
 #define GBS_SPEC_ROWS_MIN 192
 #endif
@@ -69,10 +79,15 @@ int chunk_for(int vocab, int S) {
 
 struct RowInfo {
     u64 tkey, dkey;  // row maxima as order keys (0 = no finite-or-inf element)
-    u64 zp, zq;      // integer mass sums
+    u64 zp, zq;      // integer mass sums (the one-read form: not written)
     unsigned nan;
-    unsigned pad[3];
+    unsigned state;  // the one-read form: the draft's test by the float sums, ACC_YES / ACC_NO / ACC_OPEN
+    float fp, fq;    // the one-read form: float sums of 2^((l - M) c2) over the target and the draft row
+    u64 ep, eq;      // the one-read form: the draft token's masses (a draft row at T > 0 whose test ran)
 };
+
+// the one-read form's test of a draft from float bounds on the mass sums
+constexpr unsigned ACC_YES = 0, ACC_NO = 1, ACC_OPEN = 2;
 
 struct SeqInfo {
     int status, accepted, row, mode;  // mode 0: token fixed; 1: residual draw; 2: bonus draw
@@ -80,6 +95,7 @@ struct SeqInfo {
     float Mp, Mq, c2;                 // the draw row's maxima and 1/T scale
     int pad;
     u64 zp, zq;                       // the draw row's mass sums
+    int j0, j1, pending, pad2;        // the one-read form: rows j0..j1 of the sequence need exact sums (pending)
 };
 
 struct SpecWs {
@@ -92,6 +108,7 @@ struct SpecWs {
     RowInfo* rows;           // [R]
     SeqInfo* seqs;           // [n_seq]
     u128* wparts;            // [n_seq][tiles][NWD]: the draw's sub-tile weights
+    u64* zparts;             // [R][SZ][2]: the one-read form's exact sums, per block of the exact pass
 };
 
 // The counters that must be zero between launches sit at fixed offsets in the first SPEC_CTL_BYTES (room for 65535
@@ -100,7 +117,7 @@ struct SpecWs {
 constexpr size_t SPEC_CTL_BYTES = 3 * (size_t)65536 * 4;
 
 struct Plan {
-    int R, S, S3, tpb;
+    int R, S, S3, tpb, SZ;
     size_t bytes;
 };
 
@@ -114,13 +131,14 @@ Plan plan(int n_seq, int width, int vocab) {
     want = want < 1 ? 1 : (want > tiles ? tiles : want);
     p.tpb = (tiles + want - 1) / want;
     p.S3 = (tiles + p.tpb - 1) / p.tpb;
+    p.SZ = min((DRAW_BLOCKS + n_seq - 1) / n_seq, (vocab + MIN_CHUNK - 1) / MIN_CHUNK);
     p.bytes = SPEC_CTL_BYTES + align256((size_t)p.R * p.S * 16) + align256((size_t)p.R * p.S * 4) + align256((size_t)p.R * p.S * 16) +
               align256((size_t)p.R * sizeof(RowInfo)) + align256((size_t)n_seq * sizeof(SeqInfo)) +
-              align256((size_t)n_seq * tiles * NWD * 16);
+              align256((size_t)n_seq * tiles * NWD * 16) + align256((size_t)p.R * p.SZ * 16);
     return p;
 }
 
-SpecWs carve(void* ws, int n_seq, const Plan& p) {
+SpecWs carve(void* ws, int n_seq, int vocab, const Plan& p) {
     char* c = (char*)ws;
     SpecWs w;
     w.row_counters = (unsigned*)c; c += (size_t)65536 * 4;
@@ -131,7 +149,8 @@ SpecWs carve(void* ws, int n_seq, const Plan& p) {
     w.sumparts = (u64*)c; c += align256((size_t)p.R * p.S * 16);
     w.rows = (RowInfo*)c; c += align256((size_t)p.R * sizeof(RowInfo));
     w.seqs = (SeqInfo*)c; c += align256((size_t)n_seq * sizeof(SeqInfo));
-    w.wparts = (u128*)c;
+    w.wparts = (u128*)c; c += align256((size_t)n_seq * ((vocab + TILE - 1) / TILE) * NWD * 16);
+    w.zparts = (u64*)c;
     return w;
 }
 
@@ -511,14 +530,24 @@ __device__ __forceinline__ u128 wave_sum_u128(u128 v) {
     return ((u128)hi << 64) | lo;
 }
 
-// ---- launches 1 + 2 in one, for many rows: one block per row ----
-// The block reads its target and draft row twice: forward for the maxima and NaN flag, then backward for the integer
-// mass sums (the bytes read last in the forward sweep are the likeliest to be served by the cache). It writes the row's
-// record itself (no hand-off of partials); the block that completes a sequence's last row decides the sequence.
+// ---- the one-read form, for many rows: one block per row ----
+// The block reads its target and draft row once. Besides the maxima and the NaN flag it sums 2^((l - M) c2) in float
+// (per thread against a running maximum, rescaled to the row's maximum at the end). That float sum F bounds the exact
+// mass sum: Z = sum of mass(l) with mass(l) = floor(2^44 2^y) for y the float (l - M) c2 (n <= -52 or y < -64 give 0),
+// so 2^44 F (1 - e) - V <= Z <= 2^44 F (1 + e) + V, where e bounds the relative error of F against the exact
+// sum of 2^y (the exponent's rounding, 2^-23 |y| per element, the exponential's, each rescaling's and each addition's,
+// in all below 2^-14 for rows of up to 2^18 elements) and V (one unit of truncation per element) the truncations.
+// The test of a draft decides from these bounds when they do not straddle the boundary floor(u Eq Zp) < Ep Zq;
+// otherwise (and where the bounds need finite M and c2) it is left open. The block that completes a sequence's last
+// row decides what it can: a first rejection or the bonus row without an open test before it is final; the rows from
+// the first open test to the first certain rejection (or the bonus row) get exact sums from spec_exact_k, which
+// then decides the sequence. The draw needs its row's exact sums in every case, so a sequence drawing at T > 0 always
+// has one row in the exact pass.
 #ifndef GBS_SPEC_RNT
 #define GBS_SPEC_RNT 1024
 #endif
 constexpr int RNT = GBS_SPEC_RNT;  // threads of the one-block-per-row kernel
+constexpr double ACC_REL = 1.0 / 2048.0;  // e above: eight times the largest relative error of the float sums
 
 template <int NTH>
 __device__ __forceinline__ u64 block_max_u64(u64 v, u64* s) {
@@ -546,10 +575,152 @@ __device__ __forceinline__ u64 block_sum_u64(u64 v, u64* s) {
     return r;
 }
 
+template <int NTH>
+__device__ __forceinline__ float block_sum_f32(float v, float* s) {
+    const int w = (int)threadIdx.x / WAVE, l = lane_id();
+#pragma unroll
+    for (int m = 1; m < WAVE; m <<= 1) v += __uint_as_float(xor_lane(__float_as_uint(v), m));
+    if (l == 0) s[w] = v;
+    __syncthreads();
+    float r = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NTH / WAVE; ++k) r += s[k];
+    __syncthreads();
+    return r;
+}
+
+// one element of a thread's float sum of 2^((v - m) c2) against its running maximum m. m starts at -FLT_MAX, so that a
+// -inf value adds exp2(-inf) = 0 and no inf - inf arises; a larger value rescales the sum by 2^((m - v) c2).
+__device__ __forceinline__ void online_add(float v, float c2, float& m, float& s) {
+    const float d = v - m;
+    const float e = __builtin_amdgcn_exp2f(-fabsf(d) * c2);
+    s = d > 0.0f ? fmaf(s, e, 1.0f) : s + e;
+    m = fmaxf(m, v);
+}
+
+// The draft's test from float sums Fp, Fq of the rows (ACC_YES: floor(u Eq Zp) < Ep Zq for every Zp, Zq the bounds
+// allow; ACC_NO: for none; else ACC_OPEN). Ep = 0 always rejects and Eq = 0 (with Ep > 0) always accepts, since Zq >= 2^44.
+__device__ __forceinline__ unsigned accept_bounds(float u, u64 ep, u64 eq, float fp, float fq, int vocab) {
+    if (ep == 0ull) return ACC_NO;
+    if (eq == 0ull) return ACC_YES;
+    if (!(isfinite(fp) && isfinite(fq) && fp >= 1.0f && fq >= 1.0f)) return ACC_OPEN;
+    const double one = 17592186044416.0;  // 2^44: the maximum's mass, and a lower bound of every sum
+    const double V = (double)vocab;
+    const double hp = (double)fp * one * (1.0 + ACC_REL) + V, hq = (double)fq * one * (1.0 + ACC_REL) + V;
+    const double lp = fmax((double)fp * one * (1.0 - ACC_REL) - V, one), lq = fmax((double)fq * one * (1.0 - ACC_REL) - V, one);
+    const double ud = (double)u, epd = (double)ep, eqd = (double)eq;
+    constexpr double R = 1.0 / 1099511627776.0;  // 2^-40, over the doubles' rounding
+    // floor(u Eq Zp) <= u Eq Zp <= u Eq hp < Ep lq <= Ep Zq
+    if (ud * eqd * hp * (1.0 + R) < epd * lq * (1.0 - R)) return ACC_YES;
+    // floor(u Eq Zp) >= floor(u Eq lp) >= Ep hq + 1 > Ep Zq when u Eq lp - 1 >= Ep hq
+    if (ud * eqd * lp * (1.0 - R) - 1.0 >= epd * hq * (1.0 + R)) return ACC_NO;
+    return ACC_OPEN;
+}
+
+// The sequence's decisions in the one-read form, by the block that completes the sequence's last row. Thread j checks
+// row j (its parameters, flags and the draft's bounded test); the first row whose test is not ACC_YES is j0, the first
+// ACC_NO (or the bonus row) j1. With j0 == j1 the accepted count is final; the draw then needs row j1's exact sums
+// (pending), unless its temperature is 0. With j0 < j1 the tests from j0 on wait for exact sums (pending).
+__device__ void decide_rows(int seq, int width, int vocab, long long stride, const float* __restrict__ target, const float* __restrict__ draft,
+                            const int* __restrict__ draft_ids, const float* __restrict__ temps, const float* __restrict__ u_accept,
+                            const float* __restrict__ u_resample, SpecWs ws) {
+    const int W1 = width + 1;
+    __shared__ int s_all, s_first, s_rej;
+    if (threadIdx.x == 0) {
+        s_all = 0;
+        s_first = width;
+        s_rej = width;
+    }
+    __syncthreads();
+    const int r0 = seq * W1;
+    for (int j = (int)threadIdx.x; j <= width; j += (int)blockDim.x) {
+        const RowInfo ri = load_row(ws.rows, r0 + j);
+        const float Tj = temps[r0 + j];
+        bool bad = !temp_ok(Tj);
+        if (j == 0) bad |= !(u_resample[seq] >= 0.0f && u_resample[seq] < 1.0f);
+        if (j < width) {
+            const float u = u_accept[(size_t)seq * width + j];
+            const int x = draft_ids[(size_t)seq * width + j];
+            bad |= !(u >= 0.0f && u < 1.0f) || x < 0 || x >= vocab;
+            unsigned state = ACC_NO;
+            if (!bad && !ri.nan && ri.tkey != 0ull && ri.dkey != 0ull) {
+                if (Tj == 0.0f) state = x == (int)key_id(ri.tkey) ? ACC_YES : ACC_NO;
+                else {
+                    const float cj = temp_scale(Tj);
+                    const float Mp = key_value(ri.tkey), Mq = key_value(ri.dkey);
+                    const float tx = target[(size_t)(r0 + j) * (size_t)stride + x], dx = draft[(size_t)(r0 + j) * (size_t)stride + x];
+                    const u64 ep = tx > -INFINITY ? mass(tx, Mp, cj) : 0ull;
+                    const u64 eq = dx > -INFINITY ? mass(dx, Mq, cj) : 0ull;
+                    const float fp = ld_agent((const float*)&ws.rows[r0 + j].fp), fq = ld_agent((const float*)&ws.rows[r0 + j].fq);
+                    state = (mass_fast_ok(Mp, cj) && mass_fast_ok(Mq, cj)) ? accept_bounds(u, ep, eq, fp, fq, vocab) : ACC_OPEN;
+                    st_agent(&ws.rows[r0 + j].ep, ep);
+                    st_agent(&ws.rows[r0 + j].eq, eq);
+                }
+            }
+            st_agent(&ws.rows[r0 + j].state, state);
+            if (state != ACC_YES) atomicMin(&s_first, j);
+            if (state == ACC_NO) atomicMin(&s_rej, j);
+        }
+        int f = bad ? 1 : 0;
+        f |= ri.nan != 0u ? 2 : 0;
+        f |= (ri.tkey == 0ull || (j < width && ri.dkey == 0ull)) ? 4 : 0;
+        if (f) atomicOr(&s_all, f);
+    }
+    __syncthreads();
+    if (threadIdx.x != 0) return;
+    SeqInfo si{};
+    si.status = GBS_ROW_OK;
+    const int all = s_all;
+    if (all & 1) si.status = GBS_ROW_INVALID_PARAMS;
+    else if (all & 2) si.status = GBS_ROW_NAN_LOGIT;
+    else if (all & 4) si.status = GBS_ROW_NO_CANDIDATES;
+    if (si.status == GBS_ROW_OK) {
+        si.j0 = s_first;
+        si.j1 = s_rej;
+        const int k = si.j0;
+        const RowInfo ri = load_row(ws.rows, r0 + k);
+        const float Tk = temps[r0 + k];
+        if (si.j0 == si.j1) {  // the accepted count is final: row k's record, without its sums at T > 0
+            si.accepted = k;
+            si.row = r0 + k;
+            si.argmax = (int)key_id(ri.tkey);
+            si.mode = Tk == 0.0f ? 0 : (k < width ? 1 : 2);
+            si.token = Tk == 0.0f ? si.argmax : -1;
+            if (Tk != 0.0f) {
+                si.Mp = key_value(ri.tkey);
+                si.Mq = k < width ? key_value(ri.dkey) : si.Mp;
+                si.c2 = temp_scale(Tk);
+            }
+        }
+        si.pending = (si.j0 != si.j1 || Tk != 0.0f) ? 1 : 0;
+    }
+    store_seq(ws.seqs, seq, si);
+    st_agent(&ws.seqs[seq].j0, si.j0);
+    st_agent(&ws.seqs[seq].j1, si.j1);
+    st_agent(&ws.seqs[seq].pending, si.pending);
+}
+
+template <bool DRAW>
+__device__ __forceinline__ void rows_sweep(const float* tr, const float* dr, bool has_draft, int vocab, bool vec, float c2, float& tm, int& ti,
+                                           float& dm, int& di, bool& nanf, float& om_t, float& s_t, float& om_d, float& s_d) {
+    stream_rows<false, RNT>(tr, dr, has_draft, vocab, 0, vocab, vec, [&](float t, float d, int i) {
+        nanf |= __builtin_isunordered(t, d);
+        ti = t > tm ? i : ti;
+        tm = t > tm ? t : tm;
+        di = d > dm ? i : di;
+        dm = d > dm ? d : dm;
+        if (DRAW) {
+            online_add(t, c2, om_t, s_t);
+            online_add(d, c2, om_d, s_d);
+        }
+    });
+}
+
 __global__ void __launch_bounds__(RNT) spec_rows_k(const float* __restrict__ target, const float* __restrict__ draft, int width, int vocab, long long stride,
                                                    bool vec, const int* __restrict__ draft_ids, const float* __restrict__ temps,
                                                    const float* __restrict__ u_accept, const float* __restrict__ u_resample, SpecWs ws) {
     __shared__ u64 s_red[RNT / WAVE];
+    __shared__ float s_redf[RNT / WAVE];
     __shared__ unsigned s_flag;
     const int r = blockIdx.x;
     const int W1 = width + 1;
@@ -557,53 +728,176 @@ __global__ void __launch_bounds__(RNT) spec_rows_k(const float* __restrict__ tar
     const bool has_draft = (r % W1) < width;
     const float* tr = target + (size_t)r * (size_t)stride;
     const float* dr = draft + (size_t)r * (size_t)stride;
-    // forward: per thread the largest value and its first index (elements arrive in ascending index order per thread,
-    // and a strict > keeps the first of equal values, -0 and +0 included); NaN and -inf never replace -inf
-    float tm = -INFINITY, dm = -INFINITY;
+    const float T = temps[r];
+    const bool draw = temp_ok(T) && T > 0.0f;
+    const float c2 = draw ? temp_scale(T) : 0.0f;
+    // per thread: the largest value and its first index (elements arrive in ascending index order per thread, and a
+    // strict > keeps the first of equal values, -0 and +0 included; NaN and -inf never replace -inf), and at T > 0 the
+    // float sums against running maxima
+    float tm = -INFINITY, dm = -INFINITY, om_t = -FLT_MAX, om_d = -FLT_MAX, s_t = 0.0f, s_d = 0.0f;
     int ti = 0, di = 0;
     bool nanf = false;
-    stream_rows<false, RNT>(tr, dr, has_draft, vocab, 0, vocab, vec, [&](float t, float d, int i) {
-        nanf |= __builtin_isunordered(t, d);
-        ti = t > tm ? i : ti;
-        tm = t > tm ? t : tm;
-        di = d > dm ? i : di;
-        dm = d > dm ? d : dm;
-    });
+    if (draw) rows_sweep<true>(tr, dr, has_draft, vocab, vec, c2, tm, ti, dm, di, nanf, om_t, s_t, om_d, s_d);
+    else rows_sweep<false>(tr, dr, has_draft, vocab, vec, c2, tm, ti, dm, di, nanf, om_t, s_t, om_d, s_d);
     const u64 tkey = block_max_u64<RNT>(tm == -INFINITY ? 0ull : make_key(okey_f32(tm), (u32)ti), s_red);
     const u64 dkey = block_max_u64<RNT>(dm == -INFINITY ? 0ull : make_key(okey_f32(dm), (u32)di), s_red);
     const bool nan = block_max_u64<RNT>(nanf ? 1ull : 0ull, s_red) != 0ull;
-    // backward: the mass sums at the row's temperature (none at T = 0, for an invalid T, a NaN or an empty row)
-    const float T = temps[r];
-    const bool draw = temp_ok(T) && T > 0.0f;
-    u64 zp = 0, zq = 0;
+    float fp = 0.0f, fq = 0.0f;
     if (draw && tkey != 0ull && !nan) {
-        const float c2 = temp_scale(T);
-        const float Mp = key_value(tkey);
-        const bool two = has_draft && dkey != 0ull;
-        const float Mq = two ? key_value(dkey) : Mp;  // a missing draft row streams -inf, of mass 0 under either maximum
-        if (mass_fast_ok(Mp, c2) && mass_fast_ok(Mq, c2))
-            stream_rows<true, RNT>(tr, dr, two, vocab, 0, vocab, vec, [&](float t, float d, int) {
-                zp += mass_fast(t, Mp, c2);
-                zq += mass_fast(d, Mq, c2);
-            });
-        else
-            stream_rows<true, RNT>(tr, dr, two, vocab, 0, vocab, vec, [&](float t, float d, int) {
-                zp += t > -INFINITY ? mass(t, Mp, c2) : 0ull;
-                zq += d > -INFINITY ? mass(d, Mq, c2) : 0ull;
-            });
-        zp = block_sum_u64<RNT>(zp, s_red);
-        zq = block_sum_u64<RNT>(zq, s_red);
+        // each thread's sum rescaled to the row's maximum (a thread that saw no finite value holds 0)
+        const float Mp = key_value(tkey), Mq = dkey != 0ull ? key_value(dkey) : Mp;
+        fp = block_sum_f32<RNT>(s_t > 0.0f ? s_t * __builtin_amdgcn_exp2f((om_t - Mp) * c2) : 0.0f, s_redf);
+        fq = block_sum_f32<RNT>(s_d > 0.0f ? s_d * __builtin_amdgcn_exp2f((om_d - Mq) * c2) : 0.0f, s_redf);
     }
     if (threadIdx.x == 0) {
         st_agent(&ws.rows[r].tkey, tkey);
         st_agent(&ws.rows[r].dkey, dkey);
-        st_agent(&ws.rows[r].zp, zp);
-        st_agent(&ws.rows[r].zq, zq);
         st_agent(&ws.rows[r].nan, nan ? 1u : 0u);
+        st_agent((u32*)&ws.rows[r].fp, __float_as_uint(fp));
+        st_agent((u32*)&ws.rows[r].fq, __float_as_uint(fq));
     }
     if (!arrive_last(&ws.seq_counters[seq], (unsigned)W1, &s_flag)) return;
-    decide_sequence(seq, width, vocab, stride, target, draft, draft_ids, temps, u_accept, u_resample, ws);
+    decide_rows(seq, width, vocab, stride, target, draft, draft_ids, temps, u_accept, u_resample, ws);
 }
+
+// ---- the one-read form's exact pass ----
+// Grid (SZ, n_seq). For a pending sequence, block b sums the exact masses of chunk b of rows j0..j1 (at T > 0); the
+// sequence's last block adds the chunks up, settles the open tests in order with the exact rule and writes the
+// sequence's draw record, as decide_sequence does in the two-read form.
+__global__ void __launch_bounds__(XNT) spec_exact_k(const float* __restrict__ target, const float* __restrict__ draft, int width, int vocab,
+                                                   long long stride, int chunk, bool vec, const int* __restrict__ draft_ids,
+                                                   const float* __restrict__ temps, const float* __restrict__ u_accept, SpecWs ws) {
+    __shared__ u64 s_red[XNT / WAVE];
+    __shared__ unsigned s_flag;
+    __shared__ int s_done;
+    const int S = gridDim.x, sp = blockIdx.x, seq = blockIdx.y;
+    const int W1 = width + 1, r0 = seq * W1;
+    const SeqInfo si = load_seq(ws.seqs, seq);
+    const int pending = uni(ld_agent(&ws.seqs[seq].pending));
+    const int j0 = uni(ld_agent(&ws.seqs[seq].j0)), j1 = uni(ld_agent(&ws.seqs[seq].j1));
+    const bool work = si.status == GBS_ROW_OK && pending != 0;
+    const int lo = sp * chunk, hi = min(vocab, lo + chunk);
+    if (work && j0 == j1) {
+        // one row, its record written but for the sums: each block sums its chunk, the last block adds them up
+        const bool two = si.mode == 1;
+        const float* tr = target + (size_t)si.row * (size_t)stride;
+        const float* dr = draft + (size_t)si.row * (size_t)stride;
+        const float Mp = si.Mp, Mq = si.Mq, c2 = si.c2;
+        u64 zp = 0, zq = 0;
+        if (mass_fast_ok(Mp, c2) && mass_fast_ok(Mq, c2))
+            stream_rows<false, XNT>(tr, dr, two, vocab, lo, hi, vec, [&](float t, float d, int) {
+                zp += mass_fast(t, Mp, c2);
+                zq += mass_fast(d, Mq, c2);
+            });
+        else
+            stream_rows<false, XNT>(tr, dr, two, vocab, lo, hi, vec, [&](float t, float d, int) {
+                zp += t > -INFINITY ? mass(t, Mp, c2) : 0ull;
+                zq += d > -INFINITY ? mass(d, Mq, c2) : 0ull;
+            });
+        zp = block_sum_u64<XNT>(zp, s_red);
+        zq = block_sum_u64<XNT>(zq, s_red);
+        if (threadIdx.x == 0) {
+            st_agent(&ws.zparts[((size_t)si.row * S + sp) * 2], zp);
+            st_agent(&ws.zparts[((size_t)si.row * S + sp) * 2 + 1], zq);
+        }
+        if (!arrive_last(&ws.row_counters[seq], (unsigned)S, &s_flag)) return;
+        u64 a = 0, b = 0;
+        for (int o = (int)threadIdx.x; o < S; o += XNT) {
+            a += ld_agent(&ws.zparts[((size_t)si.row * S + o) * 2]);
+            b += ld_agent(&ws.zparts[((size_t)si.row * S + o) * 2 + 1]);
+        }
+        a = block_sum_u64<XNT>(a, s_red);
+        b = block_sum_u64<XNT>(b, s_red);
+        if (threadIdx.x == 0) {
+            st_agent(&ws.seqs[seq].zp, a);
+            st_agent(&ws.seqs[seq].zq, b);
+        }
+        return;
+    }
+    if (work) {
+        for (int j = j0; j <= j1; ++j) {
+            const int r = r0 + j;
+            const float T = temps[r];
+            if (T == 0.0f) continue;
+            const RowInfo info = load_row_uniform(ws.rows, r);
+            const bool two = j < width;
+            const float Mp = key_value(info.tkey), Mq = two ? key_value(info.dkey) : Mp;
+            const float c2 = temp_scale(T);
+            const float* tr = target + (size_t)r * (size_t)stride;
+            const float* dr = draft + (size_t)r * (size_t)stride;
+            u64 zp = 0, zq = 0;
+            if (mass_fast_ok(Mp, c2) && mass_fast_ok(Mq, c2))
+                stream_rows<false, XNT>(tr, dr, two, vocab, lo, hi, vec, [&](float t, float d, int) {
+                    zp += mass_fast(t, Mp, c2);
+                    zq += mass_fast(d, Mq, c2);
+                });
+            else
+                stream_rows<false, XNT>(tr, dr, two, vocab, lo, hi, vec, [&](float t, float d, int) {
+                    zp += t > -INFINITY ? mass(t, Mp, c2) : 0ull;
+                    zq += d > -INFINITY ? mass(d, Mq, c2) : 0ull;
+                });
+            zp = block_sum_u64<XNT>(zp, s_red);
+            zq = block_sum_u64<XNT>(zq, s_red);
+            if (threadIdx.x == 0) {
+                st_agent(&ws.zparts[((size_t)r * S + sp) * 2], zp);
+                st_agent(&ws.zparts[((size_t)r * S + sp) * 2 + 1], zq);
+            }
+        }
+    }
+    if (!arrive_last(&ws.row_counters[seq], (unsigned)S, &s_flag)) return;
+    if (!work) return;
+    if (threadIdx.x == 0) s_done = 0;
+    __syncthreads();
+    for (int j = j0; j <= j1; ++j) {
+        const int r = r0 + j;
+        const float T = temps[r];
+        u64 a = 0, b = 0;
+        if (T != 0.0f) {
+            for (int o = (int)threadIdx.x; o < S; o += XNT) {
+                a += ld_agent(&ws.zparts[((size_t)r * S + o) * 2]);
+                b += ld_agent(&ws.zparts[((size_t)r * S + o) * 2 + 1]);
+            }
+            a = block_sum_u64<XNT>(a, s_red);
+            b = block_sum_u64<XNT>(b, s_red);
+        }
+        if (threadIdx.x == 0) {
+            bool acc = false;
+            if (j < width) {
+                const unsigned state = ld_agent(&ws.rows[r].state);
+                acc = state == ACC_YES;
+                if (state == ACC_OPEN) {
+                    const u64 ep = ld_agent(&ws.rows[r].ep), eq = ld_agent(&ws.rows[r].eq);
+                    acc = accept_test(u_accept[(size_t)seq * width + j], (u128)eq * a, (u128)ep * b);
+                }
+            }
+            if (!acc) {
+                const RowInfo ri = load_row(ws.rows, r);
+                SeqInfo si{};
+                si.status = GBS_ROW_OK;
+                si.accepted = j;
+                si.row = r;
+                si.argmax = (int)key_id(ri.tkey);
+                if (T == 0.0f) {
+                    si.mode = 0;
+                    si.token = si.argmax;
+                } else {
+                    si.mode = j < width ? 1 : 2;
+                    si.token = -1;
+                    si.Mp = key_value(ri.tkey);
+                    si.Mq = key_value(ri.dkey);
+                    si.c2 = temp_scale(T);
+                    si.zp = a;
+                    si.zq = b;
+                }
+                store_seq(ws.seqs, seq, si);
+                s_done = 1;
+            }
+        }
+        __syncthreads();
+        if (s_done) break;
+    }
+}
+
 
 // inclusive prefix sum of a u128 over the wave
 __device__ __forceinline__ u128 wave_scan_u128(u128 v) {
@@ -830,7 +1124,7 @@ GBS_EXPORT int gbs_spec_verify(const float* target, const float* draft, int n_se
     if (width > 0 && (!draft || !draft_ids || !u_accept)) return GBS_ERR_INVALID;
     const Plan p = plan(n_seq, width, vocab);
     if (p.R > 65535 || ws_bytes < p.bytes) return GBS_ERR_INVALID;
-    const SpecWs w = carve(ws, n_seq, p);
+    const SpecWs w = carve(ws, n_seq, vocab, p);
     const hipStream_t st = to_stream(stream);
     const int chunk = chunk_for(vocab, p.S);
     const float* dr = width > 0 ? draft : target;
@@ -840,6 +1134,10 @@ GBS_EXPORT int gbs_spec_verify(const float* target, const float* draft, int n_se
     if (p.R >= ROWS_KERNEL_MIN) {
         hipLaunchKernelGGL(spec_rows_k, dim3(p.R), dim3(RNT), 0, st, target, dr, width, vocab, ld, vec, draft_ids, temperatures, u_accept,
                            u_resample, w);
+        rc = launch_status();
+        if (rc) return rc;
+        hipLaunchKernelGGL(spec_exact_k, dim3(p.SZ, n_seq), dim3(XNT), 0, st, target, dr, width, vocab, ld, chunk_for(vocab, p.SZ), vec, draft_ids,
+                           temperatures, u_accept, w);
         rc = launch_status();
         if (rc) return rc;
     } else {
