@@ -53,10 +53,6 @@ constexpr int TILE = NT * 4 * DU;    // the draw: elements per tile
 constexpr int NWD = NT / WAVE;       // the draw: waves per block (one partial sum per wave and tile)
 constexpr int SUB = WAVE * 4 * DU;   // the draw: elements of a sub-tile (a wave's part of a tile)
 constexpr int DRAW_BLOCKS = 768;     // the draw: blocks in all (one round on the chip)
-#ifndef GBS_SPEC_XNT
-#define GBS_SPEC_XNT 256
-#endif
-constexpr int XNT = GBS_SPEC_XNT;  // the one-read form's exact pass: threads per block
 #ifndef GBS_SPEC_ROWS_MIN
 #define GBS_SPEC_ROWS_MIN 192
 #endif
@@ -98,6 +94,18 @@ struct SeqInfo {
     int j0, j1, pending, pad2;        // the one-read form: rows j0..j1 of the sequence need exact sums (pending)
 };
 
+// the one-read form's exact pass, per sub-tile of a draw row: sums of the masses of the tokens whose residual weight is
+// certainly Ep Zq - Eq Zp (A: Ep, B: Eq; the bonus draw: A alone)
+struct SubRec {
+    u64 A, B;
+};
+// and per block, its undecided tokens: masses and sub-tile
+struct AmbRec {
+    u64 ep, eq;
+    u32 p, pad;
+};
+constexpr int AMB_CAP = 128;  // undecided tokens a block of the exact pass keeps
+
 struct SpecWs {
     unsigned* row_counters;  // [R]
     unsigned* seq_counters;  // [n_seq] (launch 2)
@@ -109,6 +117,9 @@ struct SpecWs {
     SeqInfo* seqs;           // [n_seq]
     u128* wparts;            // [n_seq][tiles][NWD]: the draw's sub-tile weights
     u64* zparts;             // [R][SZ][2]: the one-read form's exact sums, per block of the exact pass
+    SubRec* subrecs;         // [n_seq][tiles][NWD]: the one-read form's sub-tile sums for the draw (many rows only)
+    AmbRec* ambs;            // [n_seq][S3][AMB_CAP]: its undecided tokens, per block
+    u32* ambcnt;             // [n_seq][S3]: their counts (above AMB_CAP: more than were kept)
 };
 
 // The counters that must be zero between launches sit at fixed offsets in the first SPEC_CTL_BYTES (room for 65535
@@ -131,10 +142,13 @@ Plan plan(int n_seq, int width, int vocab) {
     want = want < 1 ? 1 : (want > tiles ? tiles : want);
     p.tpb = (tiles + want - 1) / want;
     p.S3 = (tiles + p.tpb - 1) / p.tpb;
-    p.SZ = min((DRAW_BLOCKS + n_seq - 1) / n_seq, (vocab + MIN_CHUNK - 1) / MIN_CHUNK);
+    p.SZ = p.S3;  // the one-read form's exact pass runs on the draw's grid
     p.bytes = SPEC_CTL_BYTES + align256((size_t)p.R * p.S * 16) + align256((size_t)p.R * p.S * 4) + align256((size_t)p.R * p.S * 16) +
               align256((size_t)p.R * sizeof(RowInfo)) + align256((size_t)n_seq * sizeof(SeqInfo)) +
-              align256((size_t)n_seq * tiles * NWD * 16) + align256((size_t)p.R * p.SZ * 16);
+              align256((size_t)n_seq * tiles * NWD * 16) + align256((size_t)p.R * p.SZ * 16) +
+              (p.R >= ROWS_KERNEL_MIN ? align256((size_t)n_seq * tiles * NWD * sizeof(SubRec)) +
+                                            align256((size_t)n_seq * p.S3 * AMB_CAP * sizeof(AmbRec)) + align256((size_t)n_seq * p.S3 * 4)
+                                      : 0);
     return p;
 }
 
@@ -150,7 +164,10 @@ SpecWs carve(void* ws, int n_seq, int vocab, const Plan& p) {
     w.rows = (RowInfo*)c; c += align256((size_t)p.R * sizeof(RowInfo));
     w.seqs = (SeqInfo*)c; c += align256((size_t)n_seq * sizeof(SeqInfo));
     w.wparts = (u128*)c; c += align256((size_t)n_seq * ((vocab + TILE - 1) / TILE) * NWD * 16);
-    w.zparts = (u64*)c;
+    w.zparts = (u64*)c; c += align256((size_t)p.R * p.SZ * 16);
+    w.subrecs = (SubRec*)c; c += align256((size_t)n_seq * ((vocab + TILE - 1) / TILE) * NWD * sizeof(SubRec));
+    w.ambs = (AmbRec*)c; c += align256((size_t)n_seq * p.S3 * AMB_CAP * sizeof(AmbRec));
+    w.ambcnt = (u32*)c;
     return w;
 }
 
@@ -760,145 +777,6 @@ __global__ void __launch_bounds__(RNT) spec_rows_k(const float* __restrict__ tar
     decide_rows(seq, width, vocab, stride, target, draft, draft_ids, temps, u_accept, u_resample, ws);
 }
 
-// ---- the one-read form's exact pass ----
-// Grid (SZ, n_seq). For a pending sequence, block b sums the exact masses of chunk b of rows j0..j1 (at T > 0); the
-// sequence's last block adds the chunks up, settles the open tests in order with the exact rule and writes the
-// sequence's draw record, as decide_sequence does in the two-read form.
-__global__ void __launch_bounds__(XNT) spec_exact_k(const float* __restrict__ target, const float* __restrict__ draft, int width, int vocab,
-                                                   long long stride, int chunk, bool vec, const int* __restrict__ draft_ids,
-                                                   const float* __restrict__ temps, const float* __restrict__ u_accept, SpecWs ws) {
-    __shared__ u64 s_red[XNT / WAVE];
-    __shared__ unsigned s_flag;
-    __shared__ int s_done;
-    const int S = gridDim.x, sp = blockIdx.x, seq = blockIdx.y;
-    const int W1 = width + 1, r0 = seq * W1;
-    const SeqInfo si = load_seq(ws.seqs, seq);
-    const int pending = uni(ld_agent(&ws.seqs[seq].pending));
-    const int j0 = uni(ld_agent(&ws.seqs[seq].j0)), j1 = uni(ld_agent(&ws.seqs[seq].j1));
-    const bool work = si.status == GBS_ROW_OK && pending != 0;
-    const int lo = sp * chunk, hi = min(vocab, lo + chunk);
-    if (work && j0 == j1) {
-        // one row, its record written but for the sums: each block sums its chunk, the last block adds them up
-        const bool two = si.mode == 1;
-        const float* tr = target + (size_t)si.row * (size_t)stride;
-        const float* dr = draft + (size_t)si.row * (size_t)stride;
-        const float Mp = si.Mp, Mq = si.Mq, c2 = si.c2;
-        u64 zp = 0, zq = 0;
-        if (mass_fast_ok(Mp, c2) && mass_fast_ok(Mq, c2))
-            stream_rows<false, XNT>(tr, dr, two, vocab, lo, hi, vec, [&](float t, float d, int) {
-                zp += mass_fast(t, Mp, c2);
-                zq += mass_fast(d, Mq, c2);
-            });
-        else
-            stream_rows<false, XNT>(tr, dr, two, vocab, lo, hi, vec, [&](float t, float d, int) {
-                zp += t > -INFINITY ? mass(t, Mp, c2) : 0ull;
-                zq += d > -INFINITY ? mass(d, Mq, c2) : 0ull;
-            });
-        zp = block_sum_u64<XNT>(zp, s_red);
-        zq = block_sum_u64<XNT>(zq, s_red);
-        if (threadIdx.x == 0) {
-            st_agent(&ws.zparts[((size_t)si.row * S + sp) * 2], zp);
-            st_agent(&ws.zparts[((size_t)si.row * S + sp) * 2 + 1], zq);
-        }
-        if (!arrive_last(&ws.row_counters[seq], (unsigned)S, &s_flag)) return;
-        u64 a = 0, b = 0;
-        for (int o = (int)threadIdx.x; o < S; o += XNT) {
-            a += ld_agent(&ws.zparts[((size_t)si.row * S + o) * 2]);
-            b += ld_agent(&ws.zparts[((size_t)si.row * S + o) * 2 + 1]);
-        }
-        a = block_sum_u64<XNT>(a, s_red);
-        b = block_sum_u64<XNT>(b, s_red);
-        if (threadIdx.x == 0) {
-            st_agent(&ws.seqs[seq].zp, a);
-            st_agent(&ws.seqs[seq].zq, b);
-        }
-        return;
-    }
-    if (work) {
-        for (int j = j0; j <= j1; ++j) {
-            const int r = r0 + j;
-            const float T = temps[r];
-            if (T == 0.0f) continue;
-            const RowInfo info = load_row_uniform(ws.rows, r);
-            const bool two = j < width;
-            const float Mp = key_value(info.tkey), Mq = two ? key_value(info.dkey) : Mp;
-            const float c2 = temp_scale(T);
-            const float* tr = target + (size_t)r * (size_t)stride;
-            const float* dr = draft + (size_t)r * (size_t)stride;
-            u64 zp = 0, zq = 0;
-            if (mass_fast_ok(Mp, c2) && mass_fast_ok(Mq, c2))
-                stream_rows<false, XNT>(tr, dr, two, vocab, lo, hi, vec, [&](float t, float d, int) {
-                    zp += mass_fast(t, Mp, c2);
-                    zq += mass_fast(d, Mq, c2);
-                });
-            else
-                stream_rows<false, XNT>(tr, dr, two, vocab, lo, hi, vec, [&](float t, float d, int) {
-                    zp += t > -INFINITY ? mass(t, Mp, c2) : 0ull;
-                    zq += d > -INFINITY ? mass(d, Mq, c2) : 0ull;
-                });
-            zp = block_sum_u64<XNT>(zp, s_red);
-            zq = block_sum_u64<XNT>(zq, s_red);
-            if (threadIdx.x == 0) {
-                st_agent(&ws.zparts[((size_t)r * S + sp) * 2], zp);
-                st_agent(&ws.zparts[((size_t)r * S + sp) * 2 + 1], zq);
-            }
-        }
-    }
-    if (!arrive_last(&ws.row_counters[seq], (unsigned)S, &s_flag)) return;
-    if (!work) return;
-    if (threadIdx.x == 0) s_done = 0;
-    __syncthreads();
-    for (int j = j0; j <= j1; ++j) {
-        const int r = r0 + j;
-        const float T = temps[r];
-        u64 a = 0, b = 0;
-        if (T != 0.0f) {
-            for (int o = (int)threadIdx.x; o < S; o += XNT) {
-                a += ld_agent(&ws.zparts[((size_t)r * S + o) * 2]);
-                b += ld_agent(&ws.zparts[((size_t)r * S + o) * 2 + 1]);
-            }
-            a = block_sum_u64<XNT>(a, s_red);
-            b = block_sum_u64<XNT>(b, s_red);
-        }
-        if (threadIdx.x == 0) {
-            bool acc = false;
-            if (j < width) {
-                const unsigned state = ld_agent(&ws.rows[r].state);
-                acc = state == ACC_YES;
-                if (state == ACC_OPEN) {
-                    const u64 ep = ld_agent(&ws.rows[r].ep), eq = ld_agent(&ws.rows[r].eq);
-                    acc = accept_test(u_accept[(size_t)seq * width + j], (u128)eq * a, (u128)ep * b);
-                }
-            }
-            if (!acc) {
-                const RowInfo ri = load_row(ws.rows, r);
-                SeqInfo si{};
-                si.status = GBS_ROW_OK;
-                si.accepted = j;
-                si.row = r;
-                si.argmax = (int)key_id(ri.tkey);
-                if (T == 0.0f) {
-                    si.mode = 0;
-                    si.token = si.argmax;
-                } else {
-                    si.mode = j < width ? 1 : 2;
-                    si.token = -1;
-                    si.Mp = key_value(ri.tkey);
-                    si.Mq = key_value(ri.dkey);
-                    si.c2 = temp_scale(T);
-                    si.zp = a;
-                    si.zq = b;
-                }
-                store_seq(ws.seqs, seq, si);
-                s_done = 1;
-            }
-        }
-        __syncthreads();
-        if (s_done) break;
-    }
-}
-
-
 // inclusive prefix sum of a u128 over the wave
 __device__ __forceinline__ u128 wave_scan_u128(u128 v) {
     const int l = lane_id();
@@ -999,11 +877,402 @@ __device__ __forceinline__ void draw_tiles(const float* tr, const float* dr, int
     }
 }
 
+// The draw from sub-tile weights: thread k holds the weights of sub-tiles [k SPT, (k + 1) SPT) in sub. A block scan
+// finds the sub-tile that holds t = floor(u * total), then a block scan over that sub-tile's elements (DU per thread,
+// exact weights) the element. A zero total draws the target's argmax. All threads call it and get the token.
+template <int SPT>
+__device__ int pick_token(const u128 (&sub)[SPT], int nsub, int vocab, float u, const SeqInfo& si, const float* tr, const float* dr, bool fast,
+                          u128* s_wt, u128* s_rem_p, unsigned* s_flag_p, int* s_tok_p) {
+    static_assert(NT == WAVE * 4, "a sub-tile (256 elements) is one element per thread");
+    u128& s_rem = *s_rem_p;
+    unsigned& s_flag = *s_flag_p;
+    int& s_tok = *s_tok_p;
+    const int tid = (int)threadIdx.x;
+    if (tid == 0) {
+        s_flag = (unsigned)nsub;  // a zero total selects no sub-tile
+        s_tok = si.argmax;        // and draws the target's argmax
+    }
+    u128 v = 0;
+#pragma unroll
+    for (int k = 0; k < SPT; ++k) v += sub[k];
+    u128 total;
+    const u128 ex = block_scan_u128(v, total, s_wt);
+    const u128 t = mul_floor(u, total, nullptr);
+    if (v != 0 && ex <= t && t - ex < v) {  // this thread's sub-tiles hold t: find which
+        u128 before = ex;
+        int kk = -1;
+#pragma unroll
+        for (int k = 0; k < SPT; ++k) {
+            if (kk < 0) {
+                if (t - before < sub[k]) kk = k;
+                else before += sub[k];
+            }
+        }
+        s_flag = (unsigned)(tid * SPT + kk);
+        s_rem = t - before;
+    }
+    __syncthreads();
+    const int p = (int)s_flag;
+    const u128 rem = s_rem;
+    // sub-tile p: DU consecutive elements per thread; a block scan of the threads' sums; the element whose range holds
+    // rem (selections, no indexing)
+    static_assert(SUB == NT * DU, "a sub-tile is DU elements per thread");
+    const int e0 = p * SUB + tid * DU;
+    u128 we[DU], wsum = 0;
+#pragma unroll
+    for (int q = 0; q < DU; ++q) {
+        const int e = e0 + q;
+        const bool in = p < nsub && e < vocab;
+        const float te = in ? tr[e] : -INFINITY;
+        const float de = (in && si.mode == 1) ? dr[e] : -INFINITY;
+        we[q] = fast ? pair_weight<true>(si.mode, te, de, si.Mp, si.Mq, si.c2, si.zp, si.zq)
+                     : pair_weight(si.mode, te, de, si.Mp, si.Mq, si.c2, si.zp, si.zq);
+        wsum += we[q];
+    }
+    u128 sub_total;
+    const u128 before = block_scan_u128(wsum, sub_total, s_wt);
+    if (p < nsub && wsum != 0 && before <= rem && rem - before < wsum) {
+        u128 acc = before;
+        int qf = -1;
+#pragma unroll
+        for (int q = 0; q < DU; ++q) {
+            const bool hit = qf < 0 && rem - acc < we[q];
+            qf = hit ? q : qf;
+            acc += qf < 0 ? we[q] : (u128)0;
+        }
+        s_tok = e0 + qf;
+    }
+    __syncthreads();
+    return s_tok;
+}
+
+// ---- the one-read form's exact pass ----
+// Grid (S3, n_seq), the draw's grid. A pending sequence whose accepted count is final (j0 == j1) has one row left,
+// the row it draws from; block b takes that row's tiles [b tpb, (b + 1) tpb) in the draw's layout (sub-tile p = tile
+// NWD + wave holds elements [SUB p, SUB (p + 1))) and sums its exact masses, Zp and Zq. In the same sweep it prepares
+// the draw's sub-tile weights, which need Zp and Zq: the bonus draw's weight is Ep alone (a sub-tile's sum A of Ep);
+// the residual's, max(Ep Zq - Eq Zp, 0), is Ep Zq - Eq Zp for a token with Ep / Eq >= Hp / Lq (A and B sum its Ep and Eq)
+// and 0 for one with Ep / Eq <= Lp / Hq, where [Lp, Hp] and [Lq, Hq] bound Zp and Zq (the row's float sums). The few
+// tokens in between keep their (Ep, Eq), up to KAMB per sub-tile; a sub-tile with more is summed again by the last
+// block. The sequence's last block adds the sums up, weights each sub-tile exactly as A Zq - B Zp plus its kept
+// tokens' weights, draws, and leaves the draw kernel only the outputs. Rows whose bounds are unusable, too many
+// re-summed sub-tiles, and sequences with open tests before the draw row (j0 < j1: exact sums for rows j0..j1, in
+// chunks of tpb tiles, then the tests in order) leave the draw to the draw kernel, with the draw row's exact sums.
+
+template <int MODE, bool FAST>
+__device__ __forceinline__ void exact_tiles(const float* tr, const float* dr, int vocab, int t0, int t1, bool vec, float Mp, float Mq, float c2,
+                                            float rho_hi, float rho_lo, SubRec* recs, AmbRec* ambs, unsigned* s_namb, u64& zp, u64& zq) {
+    const int tid = (int)threadIdx.x, w = tid / WAVE, l = lane_id();
+    const __amdgpu_buffer_rsrc_t rt = rsrc(tr, (u32)vocab * 4u), rd = rsrc(MODE == 1 ? dr : tr, (u32)vocab * 4u);
+    auto issue = [&](int tile, float (&t)[DU * 4], float (&d)[DU * 4]) {
+#pragma unroll
+        for (int j = 0; j < DU; ++j) {
+            const int e = tile * TILE + w * SUB + j * (WAVE * 4) + l * 4;
+            if (vec) {
+                const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(rt, (u32)e * 4u, 0, 2);
+                u32x4 b = {0u, 0u, 0u, 0u};
+                if (MODE == 1) b = __builtin_amdgcn_raw_buffer_load_b128(rd, (u32)e * 4u, 0, 2);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    t[j * 4 + q] = __uint_as_float(a[q]);
+                    d[j * 4 + q] = __uint_as_float(b[q]);
+                }
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    t[j * 4 + q] = e + q < vocab ? tr[e + q] : -INFINITY;
+                    d[j * 4 + q] = (MODE == 1 && e + q < vocab) ? dr[e + q] : -INFINITY;
+                }
+            }
+        }
+    };
+    constexpr float LO = 1.0f - 1.0f / 524288.0f, HI = 1.0f + 1.0f / 524288.0f;  // 1 -+ 2^-19, over the float roundings
+    float tn[DU * 4], dn[DU * 4];
+    if (t0 < t1) issue(t0, tn, dn);
+    for (int tile = t0; tile < t1; ++tile) {
+        float t[DU * 4], d[DU * 4];
+#pragma unroll
+        for (int i = 0; i < DU * 4; ++i) {
+            t[i] = tn[i];
+            d[i] = dn[i];
+        }
+        if (tile + 1 < t1) issue(tile + 1, tn, dn);
+        const int p = tile * NWD + w;
+        u64 A = 0, B = 0;
+#pragma unroll
+        for (int j = 0; j < DU; ++j) {
+            const int e = tile * TILE + w * SUB + j * (WAVE * 4) + l * 4;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const bool in = e + q < vocab;  // buffer loads past the row's end return 0, not -inf
+                const u64 ep = row_mass<FAST>(in ? t[j * 4 + q] : -INFINITY, Mp, c2);
+                zp += ep;
+                if (MODE == 2) {
+                    A += ep;
+                } else {
+                    const u64 eq = row_mass<FAST>(in ? d[j * 4 + q] : -INFINITY, Mq, c2);
+                    zq += eq;
+                    const float a = (float)ep, b = (float)eq;
+                    const bool pos = a * LO >= b * rho_hi;
+                    const bool neg = a * HI <= b * rho_lo;
+                    A += pos ? ep : 0ull;
+                    B += pos ? eq : 0ull;
+                    const bool amb = !pos && !neg;
+                    if (ballot(amb) != 0ull && amb) {
+                        const unsigned slot = atomicAdd(s_namb, 1u);
+                        if (slot < (unsigned)AMB_CAP) {
+                            st_agent(&ambs[slot].ep, ep);
+                            st_agent(&ambs[slot].eq, eq);
+                            st_agent(&ambs[slot].p, (u32)p);
+                        }
+                    }
+                }
+            }
+        }
+        A = wave_sum_u64(A);
+        B = wave_sum_u64(B);
+        if (l == 0) {
+            st_agent(&recs[p].A, A);
+            st_agent(&recs[p].B, B);
+        }
+    }
+}
+
+__global__ void __launch_bounds__(NT) spec_exact_k(const float* __restrict__ target, const float* __restrict__ draft, int width, int vocab,
+                                                   long long stride, int tpb, bool vec, const int* __restrict__ draft_ids,
+                                                   const float* __restrict__ temps, const float* __restrict__ u_accept,
+                                                   const float* __restrict__ u_resample, SpecWs ws) {
+    __shared__ u64 s_red[NT / WAVE];
+    __shared__ u128 s_wt[NT / WAVE];
+    __shared__ u128 s_rem;
+    __shared__ unsigned s_flag;
+    __shared__ int s_done, s_tok;
+    __shared__ unsigned s_namb, s_ovf;
+    __shared__ unsigned s_acnt[(GBS_MAX_VOCAB + TILE - 1) / TILE + 1];  // per block: kept undecided tokens, then their prefix
+    __shared__ u64 s_wlo[(GBS_MAX_VOCAB + TILE - 1) / TILE * NWD], s_whi[(GBS_MAX_VOCAB + TILE - 1) / TILE * NWD];
+    const int S = gridDim.x, sp = blockIdx.x, seq = blockIdx.y;
+    const int W1 = width + 1, r0 = seq * W1;
+    const int tiles = (vocab + TILE - 1) / TILE;
+    const int nsub = tiles * NWD;
+    const SeqInfo si = load_seq(ws.seqs, seq);
+    const int pending = uni(ld_agent(&ws.seqs[seq].pending));
+    const int j0 = uni(ld_agent(&ws.seqs[seq].j0)), j1 = uni(ld_agent(&ws.seqs[seq].j1));
+    const bool work = si.status == GBS_ROW_OK && pending != 0;
+    if (work && j0 == j1) {
+        const int mode = si.mode;
+        const float* tr = target + (size_t)si.row * (size_t)stride;
+        const float* dr = draft + (size_t)si.row * (size_t)stride;
+        const float Mp = si.Mp, Mq = si.Mq, c2 = si.c2;
+        const bool fast = mass_fast_ok(Mp, c2) && mass_fast_ok(Mq, c2);
+        // the ratio bounds from the row's float sums (as accept_bounds takes them)
+        const float fp = __uint_as_float(uni(ld_agent((const u32*)&ws.rows[si.row].fp)));
+        const float fq = __uint_as_float(uni(ld_agent((const u32*)&ws.rows[si.row].fq)));
+        const bool bounds = fast && isfinite(fp) && isfinite(fq) && fp >= 1.0f && fq >= 1.0f;
+        const bool fused = mode == 2 || bounds;
+        float rho_hi = 0.0f, rho_lo = 0.0f;
+        if (mode == 1 && bounds) {
+            const double one = 17592186044416.0, V = (double)vocab;
+            const double hp = (double)fp * one * (1.0 + ACC_REL) + V, hq = (double)fq * one * (1.0 + ACC_REL) + V;
+            const double lp = fmax((double)fp * one * (1.0 - ACC_REL) - V, one), lq = fmax((double)fq * one * (1.0 - ACC_REL) - V, one);
+            rho_hi = (float)(hp / lq);
+            rho_lo = (float)(lp / hq);
+        }
+        SubRec* recs = ws.subrecs + (size_t)seq * nsub;
+        AmbRec* ambs = ws.ambs + (size_t)seq * S * AMB_CAP;
+        const int t0 = sp * tpb, t1 = min(tiles, t0 + tpb);
+        u64 zp = 0, zq = 0;
+        if (threadIdx.x == 0) s_namb = 0;
+        __syncthreads();
+        if (fused) {
+            AmbRec* mine = ambs + (size_t)sp * AMB_CAP;
+            if (mode == 1) exact_tiles<1, true>(tr, dr, vocab, t0, t1, vec, Mp, Mq, c2, rho_hi, rho_lo, recs, mine, &s_namb, zp, zq);
+            else if (fast) exact_tiles<2, true>(tr, dr, vocab, t0, t1, vec, Mp, Mq, c2, 0.0f, 0.0f, recs, mine, &s_namb, zp, zq);
+            else exact_tiles<2, false>(tr, dr, vocab, t0, t1, vec, Mp, Mq, c2, 0.0f, 0.0f, recs, mine, &s_namb, zp, zq);
+        } else {
+            const int lo = min(vocab, t0 * TILE), hi = min(vocab, t1 * TILE);
+            stream_rows<false>(tr, dr, mode == 1, vocab, lo, hi, vec, [&](float t, float d, int) {
+                zp += t > -INFINITY ? mass(t, Mp, c2) : 0ull;
+                zq += d > -INFINITY ? mass(d, Mq, c2) : 0ull;
+            });
+        }
+        zp = block_sum_u64<NT>(zp, s_red);
+        zq = block_sum_u64<NT>(zq, s_red);
+        if (threadIdx.x == 0) {
+            st_agent(&ws.zparts[((size_t)si.row * S + sp) * 2], zp);
+            st_agent(&ws.zparts[((size_t)si.row * S + sp) * 2 + 1], zq);
+            st_agent(&ws.ambcnt[(size_t)seq * S + sp], s_namb);
+        }
+        if (!arrive_last(&ws.row_counters[seq], (unsigned)S, &s_flag)) return;
+        u64 a = 0, b = 0;
+        for (int o = (int)threadIdx.x; o < S; o += NT) {
+            a += ld_agent(&ws.zparts[((size_t)si.row * S + o) * 2]);
+            b += ld_agent(&ws.zparts[((size_t)si.row * S + o) * 2 + 1]);
+        }
+        a = block_sum_u64<NT>(a, s_red);
+        b = block_sum_u64<NT>(b, s_red);
+        SeqInfo sx = si;
+        sx.zp = a;
+        sx.zq = b;
+        if (!fused) {
+            if (threadIdx.x == 0) {
+                st_agent(&ws.seqs[seq].zp, a);
+                st_agent(&ws.seqs[seq].zq, b);
+            }
+            return;
+        }
+        // the sub-tile weights, in LDS: A Zq - B Zp (the bonus draw: A), then each kept undecided token's exact weight
+        // max(Ep Zq - Eq Zp, 0) added to its sub-tile's (64-bit LDS atomics, the carry into the high half)
+        if (threadIdx.x == 0) s_ovf = 0;
+        for (int p = (int)threadIdx.x; p < nsub; p += NT) {
+            const u64 A = ld_agent(&recs[p].A);
+            const u128 wgt = mode == 2 ? (u128)A : (u128)A * b - (u128)ld_agent(&recs[p].B) * a;
+            s_wlo[p] = (u64)wgt;
+            s_whi[p] = (u64)(wgt >> 64);
+        }
+        for (int o = (int)threadIdx.x; o < S; o += NT) s_acnt[o] = ld_agent(&ws.ambcnt[(size_t)seq * S + o]);
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            unsigned run = 0, ovf = 0;
+            for (int o = 0; o < S; ++o) {
+                const unsigned c = s_acnt[o];
+                ovf |= c > (unsigned)AMB_CAP ? 1u : 0u;
+                s_acnt[o] = run;
+                run += c;
+            }
+            s_acnt[S] = run;
+            s_ovf = ovf;
+        }
+        __syncthreads();
+        if (s_ovf != 0u) {  // a block kept fewer undecided tokens than it met: the draw kernel draws, with the exact sums
+            if (threadIdx.x == 0) {
+                st_agent(&ws.seqs[seq].zp, a);
+                st_agent(&ws.seqs[seq].zq, b);
+            }
+            return;
+        }
+        const int total = (int)s_acnt[S];
+        for (int g = (int)threadIdx.x; g < total; g += NT) {
+            int o = 0;
+            while (o + 1 < S && s_acnt[o + 1] <= (unsigned)g) ++o;
+            const AmbRec* e = &ambs[(size_t)o * AMB_CAP + (g - (int)s_acnt[o])];
+            const u64 ep = ld_agent(&e->ep), eq = ld_agent(&e->eq);
+            const int p = (int)ld_agent(&e->p);
+            const u128 x = (u128)ep * b, y = (u128)eq * a;
+            if (x > y) {
+                const u128 d = x - y;
+                const u64 lo = (u64)d;
+                const u64 old = atomicAdd((unsigned long long*)&s_wlo[p], (unsigned long long)lo);
+                const u64 carry = old + lo < old ? 1ull : 0ull;
+                atomicAdd((unsigned long long*)&s_whi[p], (unsigned long long)((u64)(d >> 64) + carry));
+            }
+        }
+        __syncthreads();
+        constexpr int SPT = ((GBS_MAX_VOCAB + TILE - 1) / TILE * NWD + NT - 1) / NT;
+        u128 sub[SPT];
+#pragma unroll
+        for (int k = 0; k < SPT; ++k) {
+            const int p = (int)threadIdx.x * SPT + k;
+            sub[k] = p < nsub ? (((u128)s_whi[p] << 64) | s_wlo[p]) : (u128)0;
+        }
+        const int token = pick_token(sub, nsub, vocab, u_resample[seq], sx, tr, dr, fast, s_wt, &s_rem, &s_flag, &s_tok);
+        if (threadIdx.x == 0) {
+            sx.mode = 0;
+            sx.token = token;
+            store_seq(ws.seqs, seq, sx);
+        }
+        return;
+    }
+    if (work) {
+        const int lo = min(vocab, sp * tpb * TILE), hi = min(vocab, lo + tpb * TILE);
+        for (int j = j0; j <= j1; ++j) {
+            const int r = r0 + j;
+            const float T = temps[r];
+            if (T == 0.0f) continue;
+            const RowInfo info = load_row_uniform(ws.rows, r);
+            const bool two = j < width;
+            const float Mp = key_value(info.tkey), Mq = two ? key_value(info.dkey) : Mp;
+            const float c2 = temp_scale(T);
+            const float* tr = target + (size_t)r * (size_t)stride;
+            const float* dr = draft + (size_t)r * (size_t)stride;
+            u64 zp = 0, zq = 0;
+            if (mass_fast_ok(Mp, c2) && mass_fast_ok(Mq, c2))
+                stream_rows<false>(tr, dr, two, vocab, lo, hi, vec, [&](float t, float d, int) {
+                    zp += mass_fast(t, Mp, c2);
+                    zq += mass_fast(d, Mq, c2);
+                });
+            else
+                stream_rows<false>(tr, dr, two, vocab, lo, hi, vec, [&](float t, float d, int) {
+                    zp += t > -INFINITY ? mass(t, Mp, c2) : 0ull;
+                    zq += d > -INFINITY ? mass(d, Mq, c2) : 0ull;
+                });
+            zp = block_sum_u64<NT>(zp, s_red);
+            zq = block_sum_u64<NT>(zq, s_red);
+            if (threadIdx.x == 0) {
+                st_agent(&ws.zparts[((size_t)r * S + sp) * 2], zp);
+                st_agent(&ws.zparts[((size_t)r * S + sp) * 2 + 1], zq);
+            }
+        }
+    }
+    if (!arrive_last(&ws.row_counters[seq], (unsigned)S, &s_flag)) return;
+    if (!work) return;
+    if (threadIdx.x == 0) s_done = 0;
+    __syncthreads();
+    for (int j = j0; j <= j1; ++j) {
+        const int r = r0 + j;
+        const float T = temps[r];
+        u64 a = 0, b = 0;
+        if (T != 0.0f) {
+            for (int o = (int)threadIdx.x; o < S; o += NT) {
+                a += ld_agent(&ws.zparts[((size_t)r * S + o) * 2]);
+                b += ld_agent(&ws.zparts[((size_t)r * S + o) * 2 + 1]);
+            }
+            a = block_sum_u64<NT>(a, s_red);
+            b = block_sum_u64<NT>(b, s_red);
+        }
+        if (threadIdx.x == 0) {
+            bool acc = false;
+            if (j < width) {
+                const unsigned state = ld_agent(&ws.rows[r].state);
+                acc = state == ACC_YES;
+                if (state == ACC_OPEN) {
+                    const u64 ep = ld_agent(&ws.rows[r].ep), eq = ld_agent(&ws.rows[r].eq);
+                    acc = accept_test(u_accept[(size_t)seq * width + j], (u128)eq * a, (u128)ep * b);
+                }
+            }
+            if (!acc) {
+                const RowInfo ri = load_row(ws.rows, r);
+                SeqInfo si{};
+                si.status = GBS_ROW_OK;
+                si.accepted = j;
+                si.row = r;
+                si.argmax = (int)key_id(ri.tkey);
+                if (T == 0.0f) {
+                    si.mode = 0;
+                    si.token = si.argmax;
+                } else {
+                    si.mode = j < width ? 1 : 2;
+                    si.token = -1;
+                    si.Mp = key_value(ri.tkey);
+                    si.Mq = key_value(ri.dkey);
+                    si.c2 = temp_scale(T);
+                    si.zp = a;
+                    si.zq = b;
+                }
+                store_seq(ws.seqs, seq, si);
+                s_done = 1;
+            }
+        }
+        __syncthreads();
+        if (s_done) break;
+    }
+}
+
+
+
 __global__ void __launch_bounds__(NT) spec_draw_k(const float* __restrict__ target, const float* __restrict__ draft, int width, int vocab, long long stride,
                                                   int tpb, bool vec, const int* __restrict__ draft_ids, const float* __restrict__ u_resample,
                                                   SpecWs ws, int* __restrict__ out_accepted, int* __restrict__ out_tokens,
                                                   int* __restrict__ out_status) {
-    static_assert(NT == WAVE * 4, "a sub-tile (256 elements) is one element per thread");
     __shared__ u128 s_rem;
     __shared__ u128 s_wt[NT / WAVE];
     __shared__ unsigned s_flag;
@@ -1027,70 +1296,14 @@ __global__ void __launch_bounds__(NT) spec_draw_k(const float* __restrict__ targ
     if (!arrive_last(&ws.draw_counters[seq], (unsigned)S, &s_flag)) return;
     int token = si.token;
     if (drawing) {
-        const int tid = (int)threadIdx.x;
-        if (tid == 0) {
-            s_flag = (unsigned)nsub;  // a zero total selects no sub-tile
-            s_tok = si.argmax;        // and draws the target's argmax
-        }
-        // thread k sums the sub-tiles [k * SPT, (k + 1) * SPT) (loaded in parallel); a block scan; t
-        constexpr int SPT = ((GBS_MAX_VOCAB + TILE - 1) / TILE * NWD + NT - 1) / NT;  // sub-tiles per thread at the largest vocabulary
+        constexpr int SPT = ((GBS_MAX_VOCAB + TILE - 1) / TILE * NWD + NT - 1) / NT;
         u128 sub[SPT];
-        u128 v = 0;
 #pragma unroll
         for (int k = 0; k < SPT; ++k) {
-            const int p = tid * SPT + k;
+            const int p = (int)threadIdx.x * SPT + k;
             sub[k] = p < nsub ? load_u128(&wp[p]) : (u128)0;
-            v += sub[k];
         }
-        u128 total;
-        const u128 ex = block_scan_u128(v, total, s_wt);
-        const u128 t = mul_floor(u_resample[seq], total, nullptr);
-        if (v != 0 && ex <= t && t - ex < v) {  // this thread's sub-tiles hold t: find which
-            u128 before = ex;
-            int kk = -1;
-#pragma unroll
-            for (int k = 0; k < SPT; ++k) {
-                if (kk < 0) {
-                    if (t - before < sub[k]) kk = k;
-                    else before += sub[k];
-                }
-            }
-            s_flag = (unsigned)(tid * SPT + kk);
-            s_rem = t - before;
-        }
-        __syncthreads();
-        const int p = (int)s_flag;
-        const u128 rem = s_rem;
-        // sub-tile p: DU consecutive elements per thread; a block scan of the threads' sums; the element whose range holds
-        // rem (selections, no indexing)
-        static_assert(SUB == NT * DU, "a sub-tile is DU elements per thread");
-        const int e0 = p * SUB + tid * DU;
-        u128 we[DU], wsum = 0;
-#pragma unroll
-        for (int q = 0; q < DU; ++q) {
-            const int e = e0 + q;
-            const bool in = p < nsub && e < vocab;
-            const float te = in ? tr[e] : -INFINITY;
-            const float de = (in && si.mode == 1) ? dr[e] : -INFINITY;
-            we[q] = fast ? pair_weight<true>(si.mode, te, de, si.Mp, si.Mq, si.c2, si.zp, si.zq)
-                         : pair_weight(si.mode, te, de, si.Mp, si.Mq, si.c2, si.zp, si.zq);
-            wsum += we[q];
-        }
-        u128 sub_total;
-        const u128 before = block_scan_u128(wsum, sub_total, s_wt);
-        if (p < nsub && wsum != 0 && before <= rem && rem - before < wsum) {
-            u128 acc = before;
-            int qf = -1;
-#pragma unroll
-            for (int q = 0; q < DU; ++q) {
-                const bool hit = qf < 0 && rem - acc < we[q];
-                qf = hit ? q : qf;
-                acc += qf < 0 ? we[q] : (u128)0;
-            }
-            s_tok = e0 + qf;
-        }
-        __syncthreads();
-        token = s_tok;
+        token = pick_token(sub, nsub, vocab, u_resample[seq], si, tr, dr, fast, s_wt, &s_rem, &s_flag, &s_tok);
     }
     if (threadIdx.x == 0) {
         const int W1 = width + 1;
@@ -1136,8 +1349,8 @@ GBS_EXPORT int gbs_spec_verify(const float* target, const float* draft, int n_se
                            u_resample, w);
         rc = launch_status();
         if (rc) return rc;
-        hipLaunchKernelGGL(spec_exact_k, dim3(p.SZ, n_seq), dim3(XNT), 0, st, target, dr, width, vocab, ld, chunk_for(vocab, p.SZ), vec, draft_ids,
-                           temperatures, u_accept, w);
+        hipLaunchKernelGGL(spec_exact_k, dim3(p.SZ, n_seq), dim3(NT), 0, st, target, dr, width, vocab, ld, p.tpb, vec, draft_ids,
+                           temperatures, u_accept, u_resample, w);
         rc = launch_status();
         if (rc) return rc;
     } else {
