@@ -606,15 +606,6 @@ __device__ __forceinline__ float block_sum_f32(float v, float* s) {
     return r;
 }
 
-// one element of a thread's float sum of 2^((v - m) c2) against its running maximum m. m starts at -FLT_MAX, so that a
-// -inf value adds exp2(-inf) = 0 and no inf - inf arises; a larger value rescales the sum by 2^((m - v) c2).
-__device__ __forceinline__ void online_add(float v, float c2, float& m, float& s) {
-    const float d = v - m;
-    const float e = __builtin_amdgcn_exp2f(-fabsf(d) * c2);
-    s = d > 0.0f ? fmaf(s, e, 1.0f) : s + e;
-    m = fmaxf(m, v);
-}
-
 // The draft's test from float sums Fp, Fq of the rows (ACC_YES: floor(u Eq Zp) < Ep Zq for every Zp, Zq the bounds
 // allow; ACC_NO: for none; else ACC_OPEN). Ep = 0 always rejects and Eq = 0 (with Ep > 0) always accepts, since Zq >= 2^44.
 __device__ __forceinline__ unsigned accept_bounds(float u, u64 ep, u64 eq, float fp, float fq, int vocab) {
@@ -717,18 +708,95 @@ __device__ void decide_rows(int seq, int width, int vocab, long long stride, con
     st_agent(&ws.seqs[seq].pending, si.pending);
 }
 
+// Streams a whole target row (and the draft row when `two`) through g(t, d, i0) by 4-element groups t[q], d[q] of
+// elements i0 + q, each element once and each thread's groups in ascending index order; elements past the row arrive
+// as -inf. vec as for stream_rows; otherwise each element is a group of its own (the rest -inf).
+template <int NTH, class G>
+__device__ __forceinline__ void stream_groups(const float* tr, const float* dr, bool two, int vocab, bool vec, G&& g) {
+    constexpr int GSTEP = NTH * 4, ISTEP = GSTEP * U;
+    const int tid = (int)threadIdx.x;
+    if (!vec) {
+        for (int i = tid; i < vocab; i += NTH) {
+            const float t[4] = {tr[i], -INFINITY, -INFINITY, -INFINITY};
+            const float d[4] = {two ? dr[i] : -INFINITY, -INFINITY, -INFINITY, -INFINITY};
+            g(t, d, i);
+        }
+        return;
+    }
+    const __amdgpu_buffer_rsrc_t rt = rsrc(tr, (u32)vocab * 4u), rd = rsrc(two ? dr : tr, (u32)vocab * 4u);
+    const int nit = (vocab + ISTEP - 1) / ISTEP;
+    auto issue = [&](int base, u32x4 (&t)[U], u32x4 (&d)[U]) {
+#pragma unroll
+        for (int j = 0; j < U; ++j) {
+            const u32 off = (u32)(base + j * GSTEP) * 4u;
+            t[j] = __builtin_amdgcn_raw_buffer_load_b128(rt, off, 0, GBS_SPEC_AUX_FWD);
+            if (two) d[j] = __builtin_amdgcn_raw_buffer_load_b128(rd, off, 0, GBS_SPEC_AUX_FWD);
+        }
+    };
+    u32x4 tn[U], dn[U];
+    if (nit > 0) issue(tid * 4, tn, dn);
+    for (int k = 0; k < nit; ++k) {
+        const int base = k * ISTEP + tid * 4;
+        u32x4 t[U], d[U];
+#pragma unroll
+        for (int j = 0; j < U; ++j) {
+            t[j] = tn[j];
+            d[j] = dn[j];
+        }
+        if (k + 1 < nit) issue(base + ISTEP, tn, dn);
+#pragma unroll
+        for (int j = 0; j < U; ++j) {
+            const int e = base + j * GSTEP;
+            float tv[4], dv[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const bool in = e + q < vocab;
+                tv[q] = in ? __uint_as_float(t[j][q]) : -INFINITY;
+                dv[q] = (two && in) ? __uint_as_float(d[j][q]) : -INFINITY;
+            }
+            g(tv, dv, e);
+        }
+    }
+}
+
+// The row pass of one thread: the target's largest value and its first index (a strict > over ascending indices keeps
+// the first of equal values, -0 and +0 included; NaN and -inf never replace -inf), the draft's largest value, the NaN
+// flag and, when DRAW, the float sums of 2^((v - m) c2) against running maxima m (starting at -FLT_MAX, so that -inf
+// adds exp2(-inf) = 0). A group whose largest value exceeds a running maximum (rare past a row's first groups) takes a
+// wave-uniform branch that updates the maxima element by element and rescales the sums by 2^((m_old - m_new) c2);
+// then every term's exponent is <= 0.
 template <bool DRAW>
 __device__ __forceinline__ void rows_sweep(const float* tr, const float* dr, bool has_draft, int vocab, bool vec, float c2, float& tm, int& ti,
-                                           float& dm, int& di, bool& nanf, float& om_t, float& s_t, float& om_d, float& s_d) {
-    stream_rows<false, RNT>(tr, dr, has_draft, vocab, 0, vocab, vec, [&](float t, float d, int i) {
-        nanf |= __builtin_isunordered(t, d);
-        ti = t > tm ? i : ti;
-        tm = t > tm ? t : tm;
-        di = d > dm ? i : di;
-        dm = d > dm ? d : dm;
+                                           float& dm, bool& nanf, float& om_t, float& s_t, float& om_d, float& s_d) {
+    stream_groups<RNT>(tr, dr, has_draft, vocab, vec, [&](const float (&t)[4], const float (&d)[4], int i0) {
+        bool un = false;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) un |= __builtin_isunordered(t[q], d[q]);
+        nanf |= un;
+        const float gt = fmaxf(fmaxf(t[0], t[1]), fmaxf(t[2], t[3]));
+        const float gd = fmaxf(fmaxf(d[0], d[1]), fmaxf(d[2], d[3]));
+        dm = fmaxf(dm, gd);
+        const bool up = gt > tm || (DRAW && (gt > om_t || gd > om_d));
+        if (ballot(up) != 0ull) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                ti = t[q] > tm ? i0 + q : ti;
+                tm = t[q] > tm ? t[q] : tm;
+            }
+            if (DRAW) {
+                const float nt = fmaxf(om_t, gt), nd = fmaxf(om_d, gd);
+                s_t = nt > om_t ? s_t * __builtin_amdgcn_exp2f((om_t - nt) * c2) : s_t;
+                s_d = nd > om_d ? s_d * __builtin_amdgcn_exp2f((om_d - nd) * c2) : s_d;
+                om_t = nt;
+                om_d = nd;
+            }
+        }
         if (DRAW) {
-            online_add(t, c2, om_t, s_t);
-            online_add(d, c2, om_d, s_d);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                s_t += __builtin_amdgcn_exp2f((t[q] - om_t) * c2);
+                s_d += __builtin_amdgcn_exp2f((d[q] - om_d) * c2);
+            }
         }
     });
 }
@@ -752,12 +820,13 @@ __global__ void __launch_bounds__(RNT) spec_rows_k(const float* __restrict__ tar
     // strict > keeps the first of equal values, -0 and +0 included; NaN and -inf never replace -inf), and at T > 0 the
     // float sums against running maxima
     float tm = -INFINITY, dm = -INFINITY, om_t = -FLT_MAX, om_d = -FLT_MAX, s_t = 0.0f, s_d = 0.0f;
-    int ti = 0, di = 0;
+    int ti = 0;
     bool nanf = false;
-    if (draw) rows_sweep<true>(tr, dr, has_draft, vocab, vec, c2, tm, ti, dm, di, nanf, om_t, s_t, om_d, s_d);
-    else rows_sweep<false>(tr, dr, has_draft, vocab, vec, c2, tm, ti, dm, di, nanf, om_t, s_t, om_d, s_d);
+    if (draw) rows_sweep<true>(tr, dr, has_draft, vocab, vec, c2, tm, ti, dm, nanf, om_t, s_t, om_d, s_d);
+    else rows_sweep<false>(tr, dr, has_draft, vocab, vec, c2, tm, ti, dm, nanf, om_t, s_t, om_d, s_d);
+    // the draft's key carries no index (only its maximum's value is used)
     const u64 tkey = block_max_u64<RNT>(tm == -INFINITY ? 0ull : make_key(okey_f32(tm), (u32)ti), s_red);
-    const u64 dkey = block_max_u64<RNT>(dm == -INFINITY ? 0ull : make_key(okey_f32(dm), (u32)di), s_red);
+    const u64 dkey = block_max_u64<RNT>(dm == -INFINITY ? 0ull : make_key(okey_f32(dm), 0u), s_red);
     const bool nan = block_max_u64<RNT>(nanf ? 1ull : 0ull, s_red) != 0ull;
     float fp = 0.0f, fq = 0.0f;
     if (draw && tkey != 0ull && !nan) {
@@ -874,6 +943,22 @@ __device__ __forceinline__ void draw_tiles(const float* tr, const float* dr, int
             st_agent(o, (u64)part);
             st_agent(o + 1, (u64)(part >> 64));
         }
+    }
+}
+
+// a sequence's outputs: status, accepted count, the accepted drafts, then the drawn token and -1 after it
+__device__ void write_outputs(int seq, const SeqInfo& si, int token, int width, const int* __restrict__ draft_ids, int* __restrict__ out_accepted,
+                              int* __restrict__ out_tokens, int* __restrict__ out_status) {
+    const int W1 = width + 1;
+    if (out_status) out_status[seq] = si.status;
+    out_accepted[seq] = si.status == GBS_ROW_OK ? si.accepted : 0;
+    for (int j = 0; j < W1; ++j) {
+        int v = -1;
+        if (si.status == GBS_ROW_OK) {
+            if (j < si.accepted) v = draft_ids[(size_t)seq * width + j];
+            else if (j == si.accepted) v = token;
+        }
+        out_tokens[(size_t)seq * W1 + j] = v;
     }
 }
 
@@ -1041,7 +1126,8 @@ __device__ __forceinline__ void exact_tiles(const float* tr, const float* dr, in
 __global__ void __launch_bounds__(NT) spec_exact_k(const float* __restrict__ target, const float* __restrict__ draft, int width, int vocab,
                                                    long long stride, int tpb, bool vec, const int* __restrict__ draft_ids,
                                                    const float* __restrict__ temps, const float* __restrict__ u_accept,
-                                                   const float* __restrict__ u_resample, SpecWs ws) {
+                                                   const float* __restrict__ u_resample, SpecWs ws, int* __restrict__ out_accepted,
+                                                   int* __restrict__ out_tokens, int* __restrict__ out_status) {
     __shared__ u64 s_red[NT / WAVE];
     __shared__ u128 s_wt[NT / WAVE];
     __shared__ u128 s_rem;
@@ -1179,6 +1265,7 @@ __global__ void __launch_bounds__(NT) spec_exact_k(const float* __restrict__ tar
             sx.mode = 0;
             sx.token = token;
             store_seq(ws.seqs, seq, sx);
+            write_outputs(seq, sx, token, width, draft_ids, out_accepted, out_tokens, out_status);
         }
         return;
     }
@@ -1214,7 +1301,10 @@ __global__ void __launch_bounds__(NT) spec_exact_k(const float* __restrict__ tar
         }
     }
     if (!arrive_last(&ws.row_counters[seq], (unsigned)S, &s_flag)) return;
-    if (!work) return;
+    if (!work) {  // final since the row pass: an error status, or a greedy draw row
+        if (threadIdx.x == 0) write_outputs(seq, si, si.token, width, draft_ids, out_accepted, out_tokens, out_status);
+        return;
+    }
     if (threadIdx.x == 0) s_done = 0;
     __syncthreads();
     for (int j = j0; j <= j1; ++j) {
@@ -1259,6 +1349,7 @@ __global__ void __launch_bounds__(NT) spec_exact_k(const float* __restrict__ tar
                     si.zq = b;
                 }
                 store_seq(ws.seqs, seq, si);
+                if (si.mode == 0) write_outputs(seq, si, si.token, width, draft_ids, out_accepted, out_tokens, out_status);
                 s_done = 1;
             }
         }
@@ -1272,7 +1363,7 @@ __global__ void __launch_bounds__(NT) spec_exact_k(const float* __restrict__ tar
 __global__ void __launch_bounds__(NT) spec_draw_k(const float* __restrict__ target, const float* __restrict__ draft, int width, int vocab, long long stride,
                                                   int tpb, bool vec, const int* __restrict__ draft_ids, const float* __restrict__ u_resample,
                                                   SpecWs ws, int* __restrict__ out_accepted, int* __restrict__ out_tokens,
-                                                  int* __restrict__ out_status) {
+                                                  int* __restrict__ out_status, bool final_written) {
     __shared__ u128 s_rem;
     __shared__ u128 s_wt[NT / WAVE];
     __shared__ unsigned s_flag;
@@ -1282,6 +1373,7 @@ __global__ void __launch_bounds__(NT) spec_draw_k(const float* __restrict__ targ
     const int nsub = tiles * NWD;
     const SeqInfo si = load_seq(ws.seqs, seq);
     const bool drawing = si.status == GBS_ROW_OK && si.mode != 0;
+    if (final_written && !drawing) return;  // the one-read form's exact pass wrote this sequence's outputs
     const float* tr = target + (size_t)si.row * (size_t)stride;
     const float* dr = draft + (size_t)si.row * (size_t)stride;
     u128* wp = ws.wparts + (size_t)seq * nsub;
@@ -1305,19 +1397,7 @@ __global__ void __launch_bounds__(NT) spec_draw_k(const float* __restrict__ targ
         }
         token = pick_token(sub, nsub, vocab, u_resample[seq], si, tr, dr, fast, s_wt, &s_rem, &s_flag, &s_tok);
     }
-    if (threadIdx.x == 0) {
-        const int W1 = width + 1;
-        if (out_status) out_status[seq] = si.status;
-        out_accepted[seq] = si.status == GBS_ROW_OK ? si.accepted : 0;
-        for (int j = 0; j < W1; ++j) {
-            int v = -1;
-            if (si.status == GBS_ROW_OK) {
-                if (j < si.accepted) v = draft_ids[(size_t)seq * width + j];
-                else if (j == si.accepted) v = token;
-            }
-            out_tokens[(size_t)seq * W1 + j] = v;
-        }
-    }
+    if (threadIdx.x == 0) write_outputs(seq, si, token, width, draft_ids, out_accepted, out_tokens, out_status);
 }
 
 }  // namespace
@@ -1350,7 +1430,7 @@ GBS_EXPORT int gbs_spec_verify(const float* target, const float* draft, int n_se
         rc = launch_status();
         if (rc) return rc;
         hipLaunchKernelGGL(spec_exact_k, dim3(p.SZ, n_seq), dim3(NT), 0, st, target, dr, width, vocab, ld, p.tpb, vec, draft_ids,
-                           temperatures, u_accept, u_resample, w);
+                           temperatures, u_accept, u_resample, w, out_accepted, out_tokens, out_status);
         rc = launch_status();
         if (rc) return rc;
     } else {
@@ -1363,6 +1443,6 @@ GBS_EXPORT int gbs_spec_verify(const float* target, const float* draft, int n_se
         if (rc) return rc;
     }
     hipLaunchKernelGGL(spec_draw_k, dim3(p.S3, n_seq), dim3(NT), 0, st, target, dr, width, vocab, ld, p.tpb, vec, draft_ids, u_resample, w,
-                       out_accepted, out_tokens, out_status);
+                       out_accepted, out_tokens, out_status, p.R >= ROWS_KERNEL_MIN);
     return launch_status();
 }
