@@ -89,9 +89,10 @@ struct SeqInfo {
     int status, accepted, row, mode;  // mode 0: token fixed; 1: residual draw; 2: bonus draw
     int token, argmax;                // argmax: the draw row's target argmax (the draw of a zero total)
     float Mp, Mq, c2;                 // the draw row's maxima and 1/T scale
-    int pad;
+    float fp;                         // the one-read form: the draw row's float sums (fq below)
     u64 zp, zq;                       // the draw row's mass sums
-    int j0, j1, pending, pad2;        // the one-read form: rows j0..j1 of the sequence need exact sums (pending)
+    int j0, j1, pending;              // the one-read form: rows j0..j1 of the sequence need exact sums (pending)
+    float fq;
 };
 
 // the one-read form's exact pass, per sub-tile of a draw row: sums of the masses of the tokens whose residual weight is
@@ -104,7 +105,8 @@ struct AmbRec {
     u64 ep, eq;
     u32 p, pad;
 };
-constexpr int AMB_CAP = 128;  // undecided tokens a block of the exact pass keeps
+constexpr int AMB_CAP = 128;       // undecided tokens a block of the exact pass keeps
+constexpr int AMB_SEQ_CAP = 1024;  // and a sequence's list holds (beyond either, the draw kernel draws)
 
 struct SpecWs {
     unsigned* row_counters;  // [R]
@@ -118,8 +120,7 @@ struct SpecWs {
     u128* wparts;            // [n_seq][tiles][NWD]: the draw's sub-tile weights
     u64* zparts;             // [R][SZ][2]: the one-read form's exact sums, per block of the exact pass
     SubRec* subrecs;         // [n_seq][tiles][NWD]: the one-read form's sub-tile sums for the draw (many rows only)
-    AmbRec* ambs;            // [n_seq][S3][AMB_CAP]: its undecided tokens, per block
-    u32* ambcnt;             // [n_seq][S3]: their counts (above AMB_CAP: more than were kept)
+    AmbRec* ambs;            // [n_seq][AMB_SEQ_CAP]: its undecided tokens (counted in draw_counters, zero after)
 };
 
 // The counters that must be zero between launches sit at fixed offsets in the first SPEC_CTL_BYTES (room for 65535
@@ -147,7 +148,7 @@ Plan plan(int n_seq, int width, int vocab) {
               align256((size_t)p.R * sizeof(RowInfo)) + align256((size_t)n_seq * sizeof(SeqInfo)) +
               align256((size_t)n_seq * tiles * NWD * 16) + align256((size_t)p.R * p.SZ * 16) +
               (p.R >= ROWS_KERNEL_MIN ? align256((size_t)n_seq * tiles * NWD * sizeof(SubRec)) +
-                                            align256((size_t)n_seq * p.S3 * AMB_CAP * sizeof(AmbRec)) + align256((size_t)n_seq * p.S3 * 4)
+                                            align256((size_t)n_seq * AMB_SEQ_CAP * sizeof(AmbRec))
                                       : 0);
     return p;
 }
@@ -166,8 +167,7 @@ SpecWs carve(void* ws, int n_seq, int vocab, const Plan& p) {
     w.wparts = (u128*)c; c += align256((size_t)n_seq * ((vocab + TILE - 1) / TILE) * NWD * 16);
     w.zparts = (u64*)c; c += align256((size_t)p.R * p.SZ * 16);
     w.subrecs = (SubRec*)c; c += align256((size_t)n_seq * ((vocab + TILE - 1) / TILE) * NWD * sizeof(SubRec));
-    w.ambs = (AmbRec*)c; c += align256((size_t)n_seq * p.S3 * AMB_CAP * sizeof(AmbRec));
-    w.ambcnt = (u32*)c;
+    w.ambs = (AmbRec*)c;
     return w;
 }
 
@@ -312,6 +312,8 @@ __device__ __forceinline__ SeqInfo load_seq(const SeqInfo* seqs, int s) {
     v.Mp = __uint_as_float(uni(ld_agent((const u32*)&seqs[s].Mp)));
     v.Mq = __uint_as_float(uni(ld_agent((const u32*)&seqs[s].Mq)));
     v.c2 = __uint_as_float(uni(ld_agent((const u32*)&seqs[s].c2)));
+    v.fp = __uint_as_float(uni(ld_agent((const u32*)&seqs[s].fp)));
+    v.fq = __uint_as_float(uni(ld_agent((const u32*)&seqs[s].fq)));
     v.zp = uni(ld_agent(&seqs[s].zp));
     v.zq = uni(ld_agent(&seqs[s].zq));
     return v;
@@ -698,6 +700,8 @@ __device__ void decide_rows(int seq, int width, int vocab, long long stride, con
                 si.Mp = key_value(ri.tkey);
                 si.Mq = k < width ? key_value(ri.dkey) : si.Mp;
                 si.c2 = temp_scale(Tk);
+                si.fp = ld_agent((const float*)&ws.rows[r0 + k].fp);
+                si.fq = ld_agent((const float*)&ws.rows[r0 + k].fq);
             }
         }
         si.pending = (si.j0 != si.j1 || Tk != 0.0f) ? 1 : 0;
@@ -706,6 +710,8 @@ __device__ void decide_rows(int seq, int width, int vocab, long long stride, con
     st_agent(&ws.seqs[seq].j0, si.j0);
     st_agent(&ws.seqs[seq].j1, si.j1);
     st_agent(&ws.seqs[seq].pending, si.pending);
+    st_agent((u32*)&ws.seqs[seq].fp, __float_as_uint(si.fp));
+    st_agent((u32*)&ws.seqs[seq].fq, __float_as_uint(si.fq));
 }
 
 // Streams a whole target row (and the draft row when `two`) through g(t, d, i0) by 4-element groups t[q], d[q] of
@@ -1038,15 +1044,19 @@ __device__ int pick_token(const u128 (&sub)[SPT], int nsub, int vocab, float u, 
 // the draw's sub-tile weights, which need Zp and Zq: the bonus draw's weight is Ep alone (a sub-tile's sum A of Ep);
 // the residual's, max(Ep Zq - Eq Zp, 0), is Ep Zq - Eq Zp for a token with Ep / Eq >= Hp / Lq (A and B sum its Ep and Eq)
 // and 0 for one with Ep / Eq <= Lp / Hq, where [Lp, Hp] and [Lq, Hq] bound Zp and Zq (the row's float sums). The few
-// tokens in between keep their (Ep, Eq), up to KAMB per sub-tile; a sub-tile with more is summed again by the last
-// block. The sequence's last block adds the sums up, weights each sub-tile exactly as A Zq - B Zp plus its kept
-// tokens' weights, draws, and leaves the draw kernel only the outputs. Rows whose bounds are unusable, too many
-// re-summed sub-tiles, and sequences with open tests before the draw row (j0 < j1: exact sums for rows j0..j1, in
-// chunks of tpb tiles, then the tests in order) leave the draw to the draw kernel, with the draw row's exact sums.
+// tokens in between keep their (Ep, Eq, sub-tile) in the block's LDS list, flushed at the block's end to the
+// sequence's list (one atomic per block for its place). The sequence's last block adds the sums up, weights each
+// sub-tile exactly as A Zq - B Zp plus its listed tokens' weights, draws, writes the outputs and leaves the draw kernel
+// nothing to do. Rows whose bounds are unusable, lists that overflow, and sequences with open tests before the draw
+// row (j0 < j1: exact sums for rows j0..j1, in chunks of tpb tiles, then the tests in order) leave the draw to the
+// draw kernel, with the draw row's exact sums.
+
+// a mass (< 2^46) as a float, within 2^-23 of it: two exact conversions and one rounding fused multiply-add
+__device__ __forceinline__ float to_float(u64 v) { return fmaf((float)(u32)(v >> 32), 4294967296.0f, (float)(u32)v); }
 
 template <int MODE, bool FAST>
 __device__ __forceinline__ void exact_tiles(const float* tr, const float* dr, int vocab, int t0, int t1, bool vec, float Mp, float Mq, float c2,
-                                            float rho_hi, float rho_lo, SubRec* recs, AmbRec* ambs, unsigned* s_namb, u64& zp, u64& zq) {
+                                            float rho_hi, float rho_lo, SubRec* recs, AmbRec* s_amb, unsigned* s_namb, u64& zp, u64& zq) {
     const int tid = (int)threadIdx.x, w = tid / WAVE, l = lane_id();
     const __amdgpu_buffer_rsrc_t rt = rsrc(tr, (u32)vocab * 4u), rd = rsrc(MODE == 1 ? dr : tr, (u32)vocab * 4u);
     auto issue = [&](int tile, float (&t)[DU * 4], float (&d)[DU * 4]) {
@@ -1097,7 +1107,7 @@ __device__ __forceinline__ void exact_tiles(const float* tr, const float* dr, in
                 } else {
                     const u64 eq = row_mass<FAST>(in ? d[j * 4 + q] : -INFINITY, Mq, c2);
                     zq += eq;
-                    const float a = (float)ep, b = (float)eq;
+                    const float a = to_float(ep), b = to_float(eq);
                     const bool pos = a * LO >= b * rho_hi;
                     const bool neg = a * HI <= b * rho_lo;
                     A += pos ? ep : 0ull;
@@ -1105,11 +1115,7 @@ __device__ __forceinline__ void exact_tiles(const float* tr, const float* dr, in
                     const bool amb = !pos && !neg;
                     if (ballot(amb) != 0ull && amb) {
                         const unsigned slot = atomicAdd(s_namb, 1u);
-                        if (slot < (unsigned)AMB_CAP) {
-                            st_agent(&ambs[slot].ep, ep);
-                            st_agent(&ambs[slot].eq, eq);
-                            st_agent(&ambs[slot].p, (u32)p);
-                        }
+                        if (slot < (unsigned)AMB_CAP) s_amb[slot] = AmbRec{ep, eq, (u32)p, 0u};
                     }
                 }
             }
@@ -1133,8 +1139,8 @@ __global__ void __launch_bounds__(NT) spec_exact_k(const float* __restrict__ tar
     __shared__ u128 s_rem;
     __shared__ unsigned s_flag;
     __shared__ int s_done, s_tok;
-    __shared__ unsigned s_namb, s_ovf;
-    __shared__ unsigned s_acnt[(GBS_MAX_VOCAB + TILE - 1) / TILE + 1];  // per block: kept undecided tokens, then their prefix
+    __shared__ unsigned s_namb;
+    __shared__ AmbRec s_amb[AMB_CAP];
     __shared__ u64 s_wlo[(GBS_MAX_VOCAB + TILE - 1) / TILE * NWD], s_whi[(GBS_MAX_VOCAB + TILE - 1) / TILE * NWD];
     const int S = gridDim.x, sp = blockIdx.x, seq = blockIdx.y;
     const int W1 = width + 1, r0 = seq * W1;
@@ -1151,8 +1157,7 @@ __global__ void __launch_bounds__(NT) spec_exact_k(const float* __restrict__ tar
         const float Mp = si.Mp, Mq = si.Mq, c2 = si.c2;
         const bool fast = mass_fast_ok(Mp, c2) && mass_fast_ok(Mq, c2);
         // the ratio bounds from the row's float sums (as accept_bounds takes them)
-        const float fp = __uint_as_float(uni(ld_agent((const u32*)&ws.rows[si.row].fp)));
-        const float fq = __uint_as_float(uni(ld_agent((const u32*)&ws.rows[si.row].fq)));
+        const float fp = si.fp, fq = si.fq;
         const bool bounds = fast && isfinite(fp) && isfinite(fq) && fp >= 1.0f && fq >= 1.0f;
         const bool fused = mode == 2 || bounds;
         float rho_hi = 0.0f, rho_lo = 0.0f;
@@ -1164,16 +1169,15 @@ __global__ void __launch_bounds__(NT) spec_exact_k(const float* __restrict__ tar
             rho_lo = (float)(lp / hq);
         }
         SubRec* recs = ws.subrecs + (size_t)seq * nsub;
-        AmbRec* ambs = ws.ambs + (size_t)seq * S * AMB_CAP;
+        AmbRec* list = ws.ambs + (size_t)seq * AMB_SEQ_CAP;
         const int t0 = sp * tpb, t1 = min(tiles, t0 + tpb);
         u64 zp = 0, zq = 0;
         if (threadIdx.x == 0) s_namb = 0;
         __syncthreads();
         if (fused) {
-            AmbRec* mine = ambs + (size_t)sp * AMB_CAP;
-            if (mode == 1) exact_tiles<1, true>(tr, dr, vocab, t0, t1, vec, Mp, Mq, c2, rho_hi, rho_lo, recs, mine, &s_namb, zp, zq);
-            else if (fast) exact_tiles<2, true>(tr, dr, vocab, t0, t1, vec, Mp, Mq, c2, 0.0f, 0.0f, recs, mine, &s_namb, zp, zq);
-            else exact_tiles<2, false>(tr, dr, vocab, t0, t1, vec, Mp, Mq, c2, 0.0f, 0.0f, recs, mine, &s_namb, zp, zq);
+            if (mode == 1) exact_tiles<1, true>(tr, dr, vocab, t0, t1, vec, Mp, Mq, c2, rho_hi, rho_lo, recs, s_amb, &s_namb, zp, zq);
+            else if (fast) exact_tiles<2, true>(tr, dr, vocab, t0, t1, vec, Mp, Mq, c2, 0.0f, 0.0f, recs, s_amb, &s_namb, zp, zq);
+            else exact_tiles<2, false>(tr, dr, vocab, t0, t1, vec, Mp, Mq, c2, 0.0f, 0.0f, recs, s_amb, &s_namb, zp, zq);
         } else {
             const int lo = min(vocab, t0 * TILE), hi = min(vocab, t1 * TILE);
             stream_rows<false>(tr, dr, mode == 1, vocab, lo, hi, vec, [&](float t, float d, int) {
@@ -1181,76 +1185,94 @@ __global__ void __launch_bounds__(NT) spec_exact_k(const float* __restrict__ tar
                 zq += d > -INFINITY ? mass(d, Mq, c2) : 0ull;
             });
         }
-        zp = block_sum_u64<NT>(zp, s_red);
+        zp = block_sum_u64<NT>(zp, s_red);  // (its barriers also publish s_namb and s_amb)
         zq = block_sum_u64<NT>(zq, s_red);
+        // the block's undecided tokens go to the sequence's list, at a place taken by one atomic (the block's count is
+        // added even past the list's end, so that the last block sees the overflow)
+        const unsigned nb = s_namb < (unsigned)AMB_CAP ? s_namb : (unsigned)AMB_CAP;
         if (threadIdx.x == 0) {
             st_agent(&ws.zparts[((size_t)si.row * S + sp) * 2], zp);
             st_agent(&ws.zparts[((size_t)si.row * S + sp) * 2 + 1], zq);
-            st_agent(&ws.ambcnt[(size_t)seq * S + sp], s_namb);
+            s_flag = s_namb != 0u ? atomicAdd(&ws.draw_counters[seq], s_namb > (unsigned)AMB_CAP ? (unsigned)AMB_SEQ_CAP + 1u : s_namb) : 0u;
+        }
+        __syncthreads();
+        const unsigned base = s_flag;
+        for (unsigned i = threadIdx.x; i < nb; i += NT) {
+            if (base + i < (unsigned)AMB_SEQ_CAP) {
+                st_agent(&list[base + i].ep, s_amb[i].ep);
+                st_agent(&list[base + i].eq, s_amb[i].eq);
+                st_agent(&list[base + i].p, s_amb[i].p);
+            }
         }
         if (!arrive_last(&ws.row_counters[seq], (unsigned)S, &s_flag)) return;
+        // the last block: every load at once (the blocks' sums, the sub-tile sums, the list's length and its first
+        // 2 NT entries), then the exact sums, the sub-tile weights and the draw
         u64 a = 0, b = 0;
         for (int o = (int)threadIdx.x; o < S; o += NT) {
             a += ld_agent(&ws.zparts[((size_t)si.row * S + o) * 2]);
             b += ld_agent(&ws.zparts[((size_t)si.row * S + o) * 2 + 1]);
         }
+        constexpr int PPT = (GBS_MAX_VOCAB + TILE - 1) / TILE * NWD / NT;  // sub-tiles per thread at the largest vocabulary
+        u64 A[PPT], B[PPT];
+#pragma unroll
+        for (int k = 0; k < PPT; ++k) {
+            const int p = (int)threadIdx.x + k * NT;
+            A[k] = (fused && p < nsub) ? ld_agent(&recs[p].A) : 0ull;
+            B[k] = (fused && mode == 1 && p < nsub) ? ld_agent(&recs[p].B) : 0ull;
+        }
+        const unsigned total = uni(ld_agent(&ws.draw_counters[seq]));
+        AmbRec e[2];
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int g = (int)threadIdx.x + k * NT;
+            e[k].ep = ld_agent(&list[g].ep);
+            e[k].eq = ld_agent(&list[g].eq);
+            e[k].p = ld_agent(&list[g].p);
+        }
         a = block_sum_u64<NT>(a, s_red);
         b = block_sum_u64<NT>(b, s_red);
+        if (threadIdx.x == 0) st_agent(&ws.draw_counters[seq], 0u);  // the list's counter, zero again for the next launch
         SeqInfo sx = si;
         sx.zp = a;
         sx.zq = b;
-        if (!fused) {
+        if (!fused || total > (unsigned)AMB_SEQ_CAP) {  // the draw kernel draws, with the exact sums
             if (threadIdx.x == 0) {
                 st_agent(&ws.seqs[seq].zp, a);
                 st_agent(&ws.seqs[seq].zq, b);
             }
             return;
         }
-        // the sub-tile weights, in LDS: A Zq - B Zp (the bonus draw: A), then each kept undecided token's exact weight
+        // the sub-tile weights in LDS: A Zq - B Zp (the bonus draw: A), then each undecided token's exact weight
         // max(Ep Zq - Eq Zp, 0) added to its sub-tile's (64-bit LDS atomics, the carry into the high half)
-        if (threadIdx.x == 0) s_ovf = 0;
-        for (int p = (int)threadIdx.x; p < nsub; p += NT) {
-            const u64 A = ld_agent(&recs[p].A);
-            const u128 wgt = mode == 2 ? (u128)A : (u128)A * b - (u128)ld_agent(&recs[p].B) * a;
-            s_wlo[p] = (u64)wgt;
-            s_whi[p] = (u64)(wgt >> 64);
-        }
-        for (int o = (int)threadIdx.x; o < S; o += NT) s_acnt[o] = ld_agent(&ws.ambcnt[(size_t)seq * S + o]);
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            unsigned run = 0, ovf = 0;
-            for (int o = 0; o < S; ++o) {
-                const unsigned c = s_acnt[o];
-                ovf |= c > (unsigned)AMB_CAP ? 1u : 0u;
-                s_acnt[o] = run;
-                run += c;
+#pragma unroll
+        for (int k = 0; k < PPT; ++k) {
+            const int p = (int)threadIdx.x + k * NT;
+            if (p < nsub) {
+                const u128 wgt = mode == 2 ? (u128)A[k] : (u128)A[k] * b - (u128)B[k] * a;
+                s_wlo[p] = (u64)wgt;
+                s_whi[p] = (u64)(wgt >> 64);
             }
-            s_acnt[S] = run;
-            s_ovf = ovf;
         }
         __syncthreads();
-        if (s_ovf != 0u) {  // a block kept fewer undecided tokens than it met: the draw kernel draws, with the exact sums
-            if (threadIdx.x == 0) {
-                st_agent(&ws.seqs[seq].zp, a);
-                st_agent(&ws.seqs[seq].zq, b);
-            }
-            return;
-        }
-        const int total = (int)s_acnt[S];
-        for (int g = (int)threadIdx.x; g < total; g += NT) {
-            int o = 0;
-            while (o + 1 < S && s_acnt[o + 1] <= (unsigned)g) ++o;
-            const AmbRec* e = &ambs[(size_t)o * AMB_CAP + (g - (int)s_acnt[o])];
-            const u64 ep = ld_agent(&e->ep), eq = ld_agent(&e->eq);
-            const int p = (int)ld_agent(&e->p);
-            const u128 x = (u128)ep * b, y = (u128)eq * a;
+        auto add_token = [&](const AmbRec& r) {
+            const u128 x = (u128)r.ep * b, y = (u128)r.eq * a;
             if (x > y) {
                 const u128 d = x - y;
                 const u64 lo = (u64)d;
-                const u64 old = atomicAdd((unsigned long long*)&s_wlo[p], (unsigned long long)lo);
+                const u64 old = atomicAdd((unsigned long long*)&s_wlo[r.p], (unsigned long long)lo);
                 const u64 carry = old + lo < old ? 1ull : 0ull;
-                atomicAdd((unsigned long long*)&s_whi[p], (unsigned long long)((u64)(d >> 64) + carry));
+                atomicAdd((unsigned long long*)&s_whi[r.p], (unsigned long long)((u64)(d >> 64) + carry));
             }
+        };
+#pragma unroll
+        for (int k = 0; k < 2; ++k)
+            if ((unsigned)threadIdx.x + (unsigned)(k * NT) < total) add_token(e[k]);
+        for (unsigned g = threadIdx.x + 2u * NT; g < total; g += NT) {
+            AmbRec r;
+            r.ep = ld_agent(&list[g].ep);
+            r.eq = ld_agent(&list[g].eq);
+            r.p = ld_agent(&list[g].p);
+            add_token(r);
         }
         __syncthreads();
         constexpr int SPT = ((GBS_MAX_VOCAB + TILE - 1) / TILE * NWD + NT - 1) / NT;

@@ -173,6 +173,8 @@ def test_spec_one_read_acceptance_on_the_boundary(vocab):
             if q < 0.999:
                 cfg["u_accept"][s, j] = np.float32(q * (1.0 + rng.uniform(-2.0**-20, 2.0**-20)))
                 near += 1
+    cfg["target"][1 * W1, 5] = np.inf                    # sequence 1: an infinite logit (no float bounds for its row)
+    cfg["temperatures"][3 * W1:4 * W1] = 1e-30           # sequence 3: c2 near the float range's end
     log(f"spec boundary vocab={vocab} n_seq={n_seq}: {near} drafts with u at p(x)/q(x)")
     (a, t, s), (wa, wt, ws) = run(cfg)
     assert near >= n_seq
