@@ -270,7 +270,7 @@ def measure(wl, args, steps, cpu_seconds, dev, lib, stream):
         ms = time_launches(launch, steps, args.warmup)
         rows = R
         nbytes = 2 * R * vocab * 4
-        kernel = "spec_rows_k + spec_exact_k + spec_draw_k" if R >= 192 else "spec_max_k + spec_mass_k + spec_draw_k"
+        kernel = ("spec_rows_k" if R >= 192 else "spec_split_k") + " + spec_exact_k + spec_draw_k"
         dtype = "f32 (integer masses)"
         workload = "config 5: speculative verification, 32 sequences x (7 drafts + 1 bonus), rejection + residual resampling"
         if not args.no_cpu:

@@ -8,15 +8,12 @@
 // exceeds t; after `width` acceptances the bonus token is drawn from p of the last row the same way. Temperature 0:
 // p is the argmax (ties to the lowest id).
 //
-// Two forms. With fewer rows than fill the chip (two-read form), three launches, each (splits, rows) with a last-block
-// hand-off:
-//   1. row maxima (order keys, so the argmax ties to the lowest id) and NaN flags of target and draft rows;
-//   2. the rows' integer mass sums; the last row of a sequence to finish decides the sequence's acceptances;
-//   3. the residual (or bonus) weights of the one row per sequence that needs a draw, per chunk; the last block finds the
-//      chunk that holds the draw and scans it.
-// With many rows (one-read form): one block per row reads it once for the maxima and float bounds on the mass sums,
-// which decide nearly every draft; an exact pass sums the masses of the rows that still need them (each drawing
-// sequence's draw row, and any row whose test the bounds left open); then launch 3.
+// Every row is read once. The row pass takes the maxima (order keys, so the argmax ties to the lowest id), the NaN
+// flags and float bounds on the mass sums, which decide nearly every draft: spec_rows_k with one block per row when the
+// rows fill the chip, else spec_split_k over (chunks, rows). The block that completes a sequence decides what the
+// bounds allow. spec_exact_k then sums the exact masses of the rows that still need them (each drawing sequence's
+// draw row, and any row whose test the bounds left open), prepares the draw's weights in the same sweep and draws;
+// spec_draw_k draws only what that pass leaves (its fallbacks) and otherwise returns at once.
 #include <cfloat>
 
 #include "gbs_modeu.hpp"
@@ -74,28 +71,27 @@ int chunk_for(int vocab, int S) {
 }
 
 struct RowInfo {
-    u64 tkey, dkey;  // row maxima as order keys (0 = no finite-or-inf element)
-    u64 zp, zq;      // integer mass sums (the one-read form: not written)
+    u64 tkey, dkey;  // row maxima as order keys (0 = no finite-or-inf element; the draft's carries no index)
     unsigned nan;
-    unsigned state;  // the one-read form: the draft's test by the float sums, ACC_YES / ACC_NO / ACC_OPEN
-    float fp, fq;    // the one-read form: float sums of 2^((l - M) c2) over the target and the draft row
-    u64 ep, eq;      // the one-read form: the draft token's masses (a draft row at T > 0 whose test ran)
+    unsigned state;  // the draft's test by the float sums, ACC_YES / ACC_NO / ACC_OPEN
+    float fp, fq;    // float sums of 2^((l - M) c2) over the target and the draft row
+    u64 ep, eq;      // the draft token's masses (a draft row at T > 0 whose test ran)
 };
 
-// the one-read form's test of a draft from float bounds on the mass sums
+// the test of a draft from float bounds on the mass sums
 constexpr unsigned ACC_YES = 0, ACC_NO = 1, ACC_OPEN = 2;
 
 struct SeqInfo {
     int status, accepted, row, mode;  // mode 0: token fixed; 1: residual draw; 2: bonus draw
     int token, argmax;                // argmax: the draw row's target argmax (the draw of a zero total)
     float Mp, Mq, c2;                 // the draw row's maxima and 1/T scale
-    float fp;                         // the one-read form: the draw row's float sums (fq below)
+    float fp;                         // the draw row's float sums (fq below)
     u64 zp, zq;                       // the draw row's mass sums
-    int j0, j1, pending;              // the one-read form: rows j0..j1 of the sequence need exact sums (pending)
+    int j0, j1, pending;              // rows j0..j1 of the sequence need exact sums (pending)
     float fq;
 };
 
-// the one-read form's exact pass, per sub-tile of a draw row: sums of the masses of the tokens whose residual weight is
+// the exact pass, per sub-tile of a draw row: sums of the masses of the tokens whose residual weight is
 // certainly Ep Zq - Eq Zp (A: Ep, B: Eq; the bonus draw: A alone)
 struct SubRec {
     u64 A, B;
@@ -118,8 +114,8 @@ struct SpecWs {
     RowInfo* rows;           // [R]
     SeqInfo* seqs;           // [n_seq]
     u128* wparts;            // [n_seq][tiles][NWD]: the draw's sub-tile weights
-    u64* zparts;             // [R][SZ][2]: the one-read form's exact sums, per block of the exact pass
-    SubRec* subrecs;         // [n_seq][tiles][NWD]: the one-read form's sub-tile sums for the draw (many rows only)
+    u64* zparts;             // [R][SZ][2]: the exact sums, per block of the exact pass
+    SubRec* subrecs;         // [n_seq][tiles][NWD]: the exact pass's sub-tile sums for the draw
     AmbRec* ambs;            // [n_seq][AMB_SEQ_CAP]: its undecided tokens (counted in draw_counters, zero after)
 };
 
@@ -143,13 +139,11 @@ Plan plan(int n_seq, int width, int vocab) {
     want = want < 1 ? 1 : (want > tiles ? tiles : want);
     p.tpb = (tiles + want - 1) / want;
     p.S3 = (tiles + p.tpb - 1) / p.tpb;
-    p.SZ = p.S3;  // the one-read form's exact pass runs on the draw's grid
+    p.SZ = p.S3;  // the exact pass runs on the draw's grid
     p.bytes = SPEC_CTL_BYTES + align256((size_t)p.R * p.S * 16) + align256((size_t)p.R * p.S * 4) + align256((size_t)p.R * p.S * 16) +
               align256((size_t)p.R * sizeof(RowInfo)) + align256((size_t)n_seq * sizeof(SeqInfo)) +
               align256((size_t)n_seq * tiles * NWD * 16) + align256((size_t)p.R * p.SZ * 16) +
-              (p.R >= ROWS_KERNEL_MIN ? align256((size_t)n_seq * tiles * NWD * sizeof(SubRec)) +
-                                            align256((size_t)n_seq * AMB_SEQ_CAP * sizeof(AmbRec))
-                                      : 0);
+              align256((size_t)n_seq * tiles * NWD * sizeof(SubRec)) + align256((size_t)n_seq * AMB_SEQ_CAP * sizeof(AmbRec));
     return p;
 }
 
@@ -234,38 +228,10 @@ __device__ __forceinline__ void stream_rows(const float* tr, const float* dr, bo
 
 __device__ __forceinline__ u64 max_key(float v, int i) { return (v != v || v == -INFINITY) ? 0ull : make_key(okey_f32(v), (u32)i); }
 
-template <typename T>
-__device__ __forceinline__ T block_reduce_max(T v, T* s) {
-    s[threadIdx.x] = v;
-    __syncthreads();
-    for (int h = NT / 2; h > 0; h >>= 1) {
-        if ((int)threadIdx.x < h) s[threadIdx.x] = s[threadIdx.x] > s[threadIdx.x + h] ? s[threadIdx.x] : s[threadIdx.x + h];
-        __syncthreads();
-    }
-    const T r = s[0];
-    __syncthreads();
-    return r;
-}
-
-template <typename T>
-__device__ __forceinline__ T block_reduce_sum(T v, T* s) {
-    s[threadIdx.x] = v;
-    __syncthreads();
-    for (int h = NT / 2; h > 0; h >>= 1) {
-        if ((int)threadIdx.x < h) s[threadIdx.x] = s[threadIdx.x] + s[threadIdx.x + h];
-        __syncthreads();
-    }
-    const T r = s[0];
-    __syncthreads();
-    return r;
-}
-
 __device__ __forceinline__ RowInfo load_row(const RowInfo* rows, int r) {
     RowInfo ri;
     ri.tkey = ld_agent(&rows[r].tkey);
     ri.dkey = ld_agent(&rows[r].dkey);
-    ri.zp = ld_agent(&rows[r].zp);
-    ri.zq = ld_agent(&rows[r].zq);
     ri.nan = ld_agent(&rows[r].nan);
     return ri;
 }
@@ -295,8 +261,6 @@ __device__ __forceinline__ RowInfo load_row_uniform(const RowInfo* rows, int r) 
     RowInfo ri = load_row(rows, r);
     ri.tkey = uni(ri.tkey);
     ri.dkey = uni(ri.dkey);
-    ri.zp = uni(ri.zp);
-    ri.zq = uni(ri.zq);
     ri.nan = uni(ri.nan);
     return ri;
 }
@@ -324,195 +288,12 @@ __device__ __forceinline__ u128 load_u128(const u128* p) {
     return ((u128)hi << 64) | lo;
 }
 
-// ---- launch 1: maxima ----
-__global__ void __launch_bounds__(NT) spec_max_k(const float* __restrict__ target, const float* __restrict__ draft, int width, int vocab, long long stride,
-                                                 int chunk, bool vec, SpecWs ws) {
-    __shared__ u64 s_red[NT];
-    __shared__ unsigned s_flag;
-    const int S = gridDim.x, sp = blockIdx.x, r = blockIdx.y;
-    const bool has_draft = (r % (width + 1)) < width;
-    const float* tr = target + (size_t)r * (size_t)stride;
-    const float* dr = draft + (size_t)r * (size_t)stride;
-    const int lo = sp * chunk, hi = min(vocab, lo + chunk);
-    // per thread: the largest value and its first index (elements arrive in ascending index order, and a strict > keeps
-    // the first of equal values, -0 and +0 included); NaN and -inf never replace -inf
-    float tm = -INFINITY, dm = -INFINITY;
-    int ti = 0, di = 0;
-    bool nan = false;
-    stream_rows<false>(tr, dr, has_draft, vocab, lo, hi, vec, [&](float t, float d, int i) {
-        nan |= __builtin_isunordered(t, d);
-        ti = t > tm ? i : ti;
-        tm = t > tm ? t : tm;
-        di = d > dm ? i : di;
-        dm = d > dm ? d : dm;
-    });
-    u64 tk = tm == -INFINITY ? 0ull : make_key(okey_f32(tm), (u32)ti);
-    u64 dk = dm == -INFINITY ? 0ull : make_key(okey_f32(dm), (u32)di);
-    tk = block_reduce_max(tk, s_red);
-    dk = block_reduce_max(dk, s_red);
-    const unsigned bn = block_reduce_max((u64)(nan ? 1 : 0), s_red) != 0ull;
-    if (threadIdx.x == 0) {
-        st_agent(&ws.maxparts[((size_t)r * S + sp) * 2], tk);
-        st_agent(&ws.maxparts[((size_t)r * S + sp) * 2 + 1], dk);
-        st_agent(&ws.nanparts[(size_t)r * S + sp], bn);
-    }
-    if (!arrive_last(&ws.row_counters[r], (unsigned)S, &s_flag)) return;
-    // the row's partials, loaded in parallel (one per thread) and reduced
-    u64 a = 0, b = 0, n = 0;
-    for (int o = (int)threadIdx.x; o < S; o += NT) {
-        const u64 x = ld_agent(&ws.maxparts[((size_t)r * S + o) * 2]), y = ld_agent(&ws.maxparts[((size_t)r * S + o) * 2 + 1]);
-        a = x > a ? x : a;
-        b = y > b ? y : b;
-        n |= ld_agent(&ws.nanparts[(size_t)r * S + o]);
-    }
-    a = block_reduce_max(a, s_red);
-    b = block_reduce_max(b, s_red);
-    n = block_reduce_max(n, s_red);
-    if (threadIdx.x == 0) {
-        st_agent(&ws.rows[r].tkey, a);
-        st_agent(&ws.rows[r].dkey, b);
-        st_agent(&ws.rows[r].nan, (unsigned)n);
-    }
-}
-
 __device__ __forceinline__ bool temp_ok(float t) { return isfinite(t) && t >= 0.0f; }
 
 // floor(u * a) < b, exactly
 __device__ __forceinline__ bool accept_test(float u, u128 a, u128 b) { return mul_floor(u, a, nullptr) < b; }
 
 __device__ __forceinline__ float key_value(u64 k) { return okey_to_f32(key_ok(k)); }
-
-// The sequence's decisions, by the block that completes the sequence's last row (all its rows' records are written).
-__device__ void decide_sequence(int seq, int width, int vocab, long long stride, const float* __restrict__ target, const float* __restrict__ draft,
-                                const int* __restrict__ draft_ids, const float* __restrict__ temps, const float* __restrict__ u_accept,
-                                const float* __restrict__ u_resample, SpecWs ws) {
-    const int W1 = width + 1;
-    // Each thread checks rows j = tid, tid + blockDim.x, ... <= width (their parameters, flags and, for
-    // a draft row, the acceptance test), all rows at once: the status flags are or-ed and the first rejection is the
-    // minimum rejecting j.
-    __shared__ int s_all, s_first;
-    if (threadIdx.x == 0) {
-        s_all = 0;
-        s_first = width;
-    }
-    __syncthreads();
-    const int r0 = seq * W1;
-    for (int j = (int)threadIdx.x; j <= width; j += (int)blockDim.x) {
-        const RowInfo ri = load_row(ws.rows, r0 + j);
-        const float Tj = temps[r0 + j];
-        bool bad = !temp_ok(Tj);
-        if (j == 0) bad |= !(u_resample[seq] >= 0.0f && u_resample[seq] < 1.0f);
-        bool acc = false;
-        if (j < width) {
-            const float u = u_accept[(size_t)seq * width + j];
-            const int x = draft_ids[(size_t)seq * width + j];
-            bad |= !(u >= 0.0f && u < 1.0f) || x < 0 || x >= vocab;
-            if (!bad && !ri.nan && ri.tkey != 0ull && ri.dkey != 0ull) {
-                if (Tj == 0.0f) acc = x == (int)key_id(ri.tkey);
-                else {
-                    const float cj = temp_scale(Tj);
-                    const float tx = target[(size_t)(r0 + j) * (size_t)stride + x], dx = draft[(size_t)(r0 + j) * (size_t)stride + x];
-                    const u64 ep = tx > -INFINITY ? mass(tx, key_value(ri.tkey), cj) : 0ull;
-                    const u64 eq = dx > -INFINITY ? mass(dx, key_value(ri.dkey), cj) : 0ull;
-                    acc = accept_test(u, (u128)eq * ri.zp, (u128)ep * ri.zq);
-                }
-            }
-            if (!acc) atomicMin(&s_first, j);
-        }
-        int f = bad ? 1 : 0;
-        f |= ri.nan != 0u ? 2 : 0;
-        f |= (ri.tkey == 0ull || (j < width && ri.dkey == 0ull)) ? 4 : 0;
-        if (f) atomicOr(&s_all, f);
-    }
-    __syncthreads();
-    if (threadIdx.x != 0) return;
-    SeqInfo si{};
-    si.status = GBS_ROW_OK;
-    const int all = s_all;
-    if (all & 1) si.status = GBS_ROW_INVALID_PARAMS;
-    else if (all & 2) si.status = GBS_ROW_NAN_LOGIT;
-    else if (all & 4) si.status = GBS_ROW_NO_CANDIDATES;
-    if (si.status == GBS_ROW_OK) {
-        const int k = s_first;
-        si.accepted = k;
-        si.row = r0 + k;
-        const float Tk = temps[r0 + k];
-        const RowInfo ri = load_row(ws.rows, r0 + k);
-        si.argmax = (int)key_id(ri.tkey);
-        if (Tk == 0.0f) {
-            si.mode = 0;
-            si.token = si.argmax;
-        } else {
-            si.mode = k < width ? 1 : 2;
-            si.token = -1;
-            si.Mp = key_value(ri.tkey);
-            si.Mq = key_value(ri.dkey);
-            si.c2 = temp_scale(Tk);
-            si.zp = ri.zp;
-            si.zq = ri.zq;
-        }
-    }
-    store_seq(ws.seqs, seq, si);
-}
-
-// ---- launch 2: mass sums, then the sequence's acceptances ----
-__global__ void __launch_bounds__(NT) spec_mass_k(const float* __restrict__ target, const float* __restrict__ draft, int width, int vocab, long long stride,
-                                                  int chunk, bool vec, const int* __restrict__ draft_ids, const float* __restrict__ temps,
-                                                  const float* __restrict__ u_accept, const float* __restrict__ u_resample, SpecWs ws) {
-    __shared__ u64 s_red[NT];
-    __shared__ unsigned s_flag;
-    const int S = gridDim.x, sp = blockIdx.x, r = blockIdx.y;
-    const int W1 = width + 1;
-    const int seq = r / W1;
-    const bool has_draft = (r % W1) < width;
-    const float T = temps[r];
-    const bool draw = temp_ok(T) && T > 0.0f;
-    const RowInfo info = load_row_uniform(ws.rows, r);
-    const float Mp = key_value(info.tkey), Mq = key_value(info.dkey);
-    const float c2 = draw ? temp_scale(T) : 0.0f;
-    const float* tr = target + (size_t)r * (size_t)stride;
-    const float* dr = draft + (size_t)r * (size_t)stride;
-    const int lo = sp * chunk, hi = min(vocab, lo + chunk);
-    u64 zp = 0, zq = 0;
-    if (draw && info.tkey != 0ull && !info.nan) {
-        // the reverse of the maxima pass's order: the bytes that pass read last are the likeliest still in cache
-        const bool two = has_draft && info.dkey != 0ull;
-        const float Mq2 = two ? Mq : Mp;  // a missing draft row streams -inf, of mass 0 under either maximum
-        if (mass_fast_ok(Mp, c2) && mass_fast_ok(Mq2, c2))
-            stream_rows<true>(tr, dr, two, vocab, lo, hi, vec, [&](float t, float d, int) {
-                zp += mass_fast(t, Mp, c2);
-                zq += mass_fast(d, Mq2, c2);
-            });
-        else
-            stream_rows<true>(tr, dr, two, vocab, lo, hi, vec, [&](float t, float d, int) {
-                zp += t > -INFINITY ? mass(t, Mp, c2) : 0ull;
-                zq += d > -INFINITY ? mass(d, Mq2, c2) : 0ull;
-            });
-    }
-    zp = block_reduce_sum(zp, s_red);
-    zq = block_reduce_sum(zq, s_red);
-    if (threadIdx.x == 0) {
-        st_agent(&ws.sumparts[((size_t)r * S + sp) * 2], zp);
-        st_agent(&ws.sumparts[((size_t)r * S + sp) * 2 + 1], zq);
-    }
-    if (!arrive_last(&ws.row_counters[r], (unsigned)S, &s_flag)) return;
-    {
-        // the row's partial sums, loaded in parallel (one per thread) and reduced
-        u64 a = 0, b = 0;
-        for (int o = (int)threadIdx.x; o < S; o += NT) {
-            a += ld_agent(&ws.sumparts[((size_t)r * S + o) * 2]);
-            b += ld_agent(&ws.sumparts[((size_t)r * S + o) * 2 + 1]);
-        }
-        a = block_reduce_sum(a, s_red);
-        b = block_reduce_sum(b, s_red);
-        if (threadIdx.x == 0) {
-            st_agent(&ws.rows[r].zp, a);
-            st_agent(&ws.rows[r].zq, b);
-        }
-    }
-    if (!arrive_last(&ws.seq_counters[seq], (unsigned)W1, &s_flag)) return;
-    decide_sequence(seq, width, vocab, stride, target, draft, draft_ids, temps, u_accept, u_resample, ws);
-}
 
 // the mass of a token of logit l in a row of maximum M; FAST: mass_fast's preconditions hold for the row
 template <bool FAST>
@@ -531,10 +312,6 @@ __device__ __forceinline__ u128 pair_weight(int mode, float t, float d, float Mp
     return a > b ? a - b : (u128)0;
 }
 
-// the same, of element i of the sequence's draw row
-__device__ __forceinline__ u128 draw_weight(int mode, const float* tr, const float* dr, int i, float Mp, float Mq, float c2, u64 zp, u64 zq) {
-    return pair_weight(mode, tr[i], mode == 2 ? -INFINITY : dr[i], Mp, Mq, c2, zp, zq);
-}
 
 // sum of a u128 over the wave, in every lane (cross-lane moves by DPP and permlane swaps)
 __device__ __forceinline__ u128 wave_sum_u128(u128 v) {
@@ -549,7 +326,7 @@ __device__ __forceinline__ u128 wave_sum_u128(u128 v) {
     return ((u128)hi << 64) | lo;
 }
 
-// ---- the one-read form, for many rows: one block per row ----
+// ---- the row pass, for many rows: one block per row ----
 // The block reads its target and draft row once. Besides the maxima and the NaN flag it sums 2^((l - M) c2) in float
 // (per thread against a running maximum, rescaled to the row's maximum at the end). That float sum F bounds the exact
 // mass sum: Z = sum of mass(l) with mass(l) = floor(2^44 2^y) for y the float (l - M) c2 (n <= -52 or y < -64 give 0),
@@ -627,7 +404,7 @@ __device__ __forceinline__ unsigned accept_bounds(float u, u64 ep, u64 eq, float
     return ACC_OPEN;
 }
 
-// The sequence's decisions in the one-read form, by the block that completes the sequence's last row. Thread j checks
+// The sequence's decisions, by the block that completes the sequence's last row. Thread j checks
 // row j (its parameters, flags and the draft's bounded test); the first row whose test is not ACC_YES is j0, the first
 // ACC_NO (or the bonus row) j1. With j0 == j1 the accepted count is final; the draw then needs row j1's exact sums
 // (pending), unless its temperature is 0. With j0 < j1 the tests from j0 on wait for exact sums (pending).
@@ -714,15 +491,15 @@ __device__ void decide_rows(int seq, int width, int vocab, long long stride, con
     st_agent((u32*)&ws.seqs[seq].fq, __float_as_uint(si.fq));
 }
 
-// Streams a whole target row (and the draft row when `two`) through g(t, d, i0) by 4-element groups t[q], d[q] of
-// elements i0 + q, each element once and each thread's groups in ascending index order; elements past the row arrive
-// as -inf. vec as for stream_rows; otherwise each element is a group of its own (the rest -inf).
+// Streams elements [lo, hi) of a target row (and of the draft row when `two`) through g(t, d, i0) by 4-element groups
+// t[q], d[q] of elements i0 + q, each element once and each thread's groups in ascending index order; elements past
+// `hi` arrive as -inf. vec as for stream_rows; otherwise each element is a group of its own (the rest -inf).
 template <int NTH, class G>
-__device__ __forceinline__ void stream_groups(const float* tr, const float* dr, bool two, int vocab, bool vec, G&& g) {
+__device__ __forceinline__ void stream_groups(const float* tr, const float* dr, bool two, int vocab, int lo, int hi, bool vec, G&& g) {
     constexpr int GSTEP = NTH * 4, ISTEP = GSTEP * U;
     const int tid = (int)threadIdx.x;
     if (!vec) {
-        for (int i = tid; i < vocab; i += NTH) {
+        for (int i = lo + tid; i < hi; i += NTH) {
             const float t[4] = {tr[i], -INFINITY, -INFINITY, -INFINITY};
             const float d[4] = {two ? dr[i] : -INFINITY, -INFINITY, -INFINITY, -INFINITY};
             g(t, d, i);
@@ -730,7 +507,7 @@ __device__ __forceinline__ void stream_groups(const float* tr, const float* dr, 
         return;
     }
     const __amdgpu_buffer_rsrc_t rt = rsrc(tr, (u32)vocab * 4u), rd = rsrc(two ? dr : tr, (u32)vocab * 4u);
-    const int nit = (vocab + ISTEP - 1) / ISTEP;
+    const int nit = (hi - lo + ISTEP - 1) / ISTEP;
     auto issue = [&](int base, u32x4 (&t)[U], u32x4 (&d)[U]) {
 #pragma unroll
         for (int j = 0; j < U; ++j) {
@@ -740,9 +517,9 @@ __device__ __forceinline__ void stream_groups(const float* tr, const float* dr, 
         }
     };
     u32x4 tn[U], dn[U];
-    if (nit > 0) issue(tid * 4, tn, dn);
+    if (nit > 0) issue(lo + tid * 4, tn, dn);
     for (int k = 0; k < nit; ++k) {
-        const int base = k * ISTEP + tid * 4;
+        const int base = lo + k * ISTEP + tid * 4;
         u32x4 t[U], d[U];
 #pragma unroll
         for (int j = 0; j < U; ++j) {
@@ -756,7 +533,7 @@ __device__ __forceinline__ void stream_groups(const float* tr, const float* dr, 
             float tv[4], dv[4];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                const bool in = e + q < vocab;
+                const bool in = e + q < hi;
                 tv[q] = in ? __uint_as_float(t[j][q]) : -INFINITY;
                 dv[q] = (two && in) ? __uint_as_float(d[j][q]) : -INFINITY;
             }
@@ -771,10 +548,10 @@ __device__ __forceinline__ void stream_groups(const float* tr, const float* dr, 
 // adds exp2(-inf) = 0). A group whose largest value exceeds a running maximum (rare past a row's first groups) takes a
 // wave-uniform branch that updates the maxima element by element and rescales the sums by 2^((m_old - m_new) c2);
 // then every term's exponent is <= 0.
-template <bool DRAW>
-__device__ __forceinline__ void rows_sweep(const float* tr, const float* dr, bool has_draft, int vocab, bool vec, float c2, float& tm, int& ti,
-                                           float& dm, bool& nanf, float& om_t, float& s_t, float& om_d, float& s_d) {
-    stream_groups<RNT>(tr, dr, has_draft, vocab, vec, [&](const float (&t)[4], const float (&d)[4], int i0) {
+template <bool DRAW, int NTH>
+__device__ __forceinline__ void rows_sweep(const float* tr, const float* dr, bool has_draft, int vocab, int lo, int hi, bool vec, float c2,
+                                           float& tm, int& ti, float& dm, bool& nanf, float& om_t, float& s_t, float& om_d, float& s_d) {
+    stream_groups<NTH>(tr, dr, has_draft, vocab, lo, hi, vec, [&](const float (&t)[4], const float (&d)[4], int i0) {
         bool un = false;
 #pragma unroll
         for (int q = 0; q < 4; ++q) un |= __builtin_isunordered(t[q], d[q]);
@@ -828,8 +605,8 @@ __global__ void __launch_bounds__(RNT) spec_rows_k(const float* __restrict__ tar
     float tm = -INFINITY, dm = -INFINITY, om_t = -FLT_MAX, om_d = -FLT_MAX, s_t = 0.0f, s_d = 0.0f;
     int ti = 0;
     bool nanf = false;
-    if (draw) rows_sweep<true>(tr, dr, has_draft, vocab, vec, c2, tm, ti, dm, nanf, om_t, s_t, om_d, s_d);
-    else rows_sweep<false>(tr, dr, has_draft, vocab, vec, c2, tm, ti, dm, nanf, om_t, s_t, om_d, s_d);
+    if (draw) rows_sweep<true, RNT>(tr, dr, has_draft, vocab, 0, vocab, vec, c2, tm, ti, dm, nanf, om_t, s_t, om_d, s_d);
+    else rows_sweep<false, RNT>(tr, dr, has_draft, vocab, 0, vocab, vec, c2, tm, ti, dm, nanf, om_t, s_t, om_d, s_d);
     // the draft's key carries no index (only its maximum's value is used)
     const u64 tkey = block_max_u64<RNT>(tm == -INFINITY ? 0ull : make_key(okey_f32(tm), (u32)ti), s_red);
     const u64 dkey = block_max_u64<RNT>(dm == -INFINITY ? 0ull : make_key(okey_f32(dm), 0u), s_red);
@@ -1037,7 +814,86 @@ __device__ int pick_token(const u128 (&sub)[SPT], int nsub, int vocab, float u, 
     return s_tok;
 }
 
-// ---- the one-read form's exact pass ----
+// ---- the row pass for fewer rows: (splits, rows) ----
+// Block sp takes chunk sp of row r: its part of the row pass (maxima, NaN flag and, at T > 0, float sums rescaled to
+// the chunk's maximum). The row's last block rescales the chunks' sums to the row's maximum (one more rescaling of
+// each term, inside the bound's margin) and writes the row's record; the block that completes a sequence's last row
+// decides it as spec_rows_k's does.
+__global__ void __launch_bounds__(NT) spec_split_k(const float* __restrict__ target, const float* __restrict__ draft, int width, int vocab,
+                                                   long long stride, int chunk, bool vec, const int* __restrict__ draft_ids,
+                                                   const float* __restrict__ temps, const float* __restrict__ u_accept,
+                                                   const float* __restrict__ u_resample, SpecWs ws) {
+    __shared__ u64 s_red[NT / WAVE];
+    __shared__ float s_redf[NT / WAVE];
+    __shared__ unsigned s_flag;
+    const int S = gridDim.x, sp = blockIdx.x, r = blockIdx.y;
+    const int W1 = width + 1;
+    const int seq = r / W1;
+    const bool has_draft = (r % W1) < width;
+    const float* tr = target + (size_t)r * (size_t)stride;
+    const float* dr = draft + (size_t)r * (size_t)stride;
+    const int lo = min(vocab, sp * chunk), hi = min(vocab, lo + chunk);
+    const float T = temps[r];
+    const bool draw = temp_ok(T) && T > 0.0f;
+    const float c2 = draw ? temp_scale(T) : 0.0f;
+    float tm = -INFINITY, dm = -INFINITY, om_t = -FLT_MAX, om_d = -FLT_MAX, s_t = 0.0f, s_d = 0.0f;
+    int ti = 0;
+    bool nanf = false;
+    if (draw) rows_sweep<true, NT>(tr, dr, has_draft, vocab, lo, hi, vec, c2, tm, ti, dm, nanf, om_t, s_t, om_d, s_d);
+    else rows_sweep<false, NT>(tr, dr, has_draft, vocab, lo, hi, vec, c2, tm, ti, dm, nanf, om_t, s_t, om_d, s_d);
+    const u64 tk = block_max_u64<NT>(tm == -INFINITY ? 0ull : make_key(okey_f32(tm), (u32)ti), s_red);
+    const u64 dk = block_max_u64<NT>(dm == -INFINITY ? 0ull : make_key(okey_f32(dm), 0u), s_red);
+    const bool bn = block_max_u64<NT>(nanf ? 1ull : 0ull, s_red) != 0ull;
+    float fp = 0.0f, fq = 0.0f;
+    if (draw) {  // the chunk's sums against its own maxima (an empty side sums to 0)
+        const float Mp = tk != 0ull ? key_value(tk) : 0.0f, Mq = dk != 0ull ? key_value(dk) : 0.0f;
+        fp = block_sum_f32<NT>((tk != 0ull && s_t > 0.0f) ? s_t * __builtin_amdgcn_exp2f((om_t - Mp) * c2) : 0.0f, s_redf);
+        fq = block_sum_f32<NT>((dk != 0ull && s_d > 0.0f) ? s_d * __builtin_amdgcn_exp2f((om_d - Mq) * c2) : 0.0f, s_redf);
+    }
+    if (threadIdx.x == 0) {
+        st_agent(&ws.maxparts[((size_t)r * S + sp) * 2], tk);
+        st_agent(&ws.maxparts[((size_t)r * S + sp) * 2 + 1], dk);
+        st_agent(&ws.nanparts[(size_t)r * S + sp], bn ? 1u : 0u);
+        st_agent(&ws.sumparts[((size_t)r * S + sp) * 2], (u64)__float_as_uint(fp));
+        st_agent(&ws.sumparts[((size_t)r * S + sp) * 2 + 1], (u64)__float_as_uint(fq));
+    }
+    if (!arrive_last(&ws.row_counters[r], (unsigned)S, &s_flag)) return;
+    // the row: maxima over the chunks, then each chunk's sums rescaled to them (thread o takes chunks o, o + NT, ...)
+    u64 a = 0, b = 0, n = 0;
+    for (int o = (int)threadIdx.x; o < S; o += NT) {
+        const u64 x = ld_agent(&ws.maxparts[((size_t)r * S + o) * 2]), y = ld_agent(&ws.maxparts[((size_t)r * S + o) * 2 + 1]);
+        a = x > a ? x : a;
+        b = y > b ? y : b;
+        n |= ld_agent(&ws.nanparts[(size_t)r * S + o]);
+    }
+    a = block_max_u64<NT>(a, s_red);
+    b = block_max_u64<NT>(b, s_red);
+    n = block_max_u64<NT>(n, s_red);
+    if (draw && a != 0ull && n == 0ull) {
+        const float Mp = key_value(a), Mq = b != 0ull ? key_value(b) : Mp;
+        float xp = 0.0f, xq = 0.0f;
+        for (int o = (int)threadIdx.x; o < S; o += NT) {
+            const u64 x = ld_agent(&ws.maxparts[((size_t)r * S + o) * 2]), y = ld_agent(&ws.maxparts[((size_t)r * S + o) * 2 + 1]);
+            const float gp = __uint_as_float((u32)ld_agent(&ws.sumparts[((size_t)r * S + o) * 2]));
+            const float gq = __uint_as_float((u32)ld_agent(&ws.sumparts[((size_t)r * S + o) * 2 + 1]));
+            xp += (x != 0ull && gp > 0.0f) ? gp * __builtin_amdgcn_exp2f((key_value(x) - Mp) * c2) : 0.0f;
+            xq += (y != 0ull && gq > 0.0f) ? gq * __builtin_amdgcn_exp2f((key_value(y) - Mq) * c2) : 0.0f;
+        }
+        fp = block_sum_f32<NT>(xp, s_redf);
+        fq = block_sum_f32<NT>(xq, s_redf);
+    }
+    if (threadIdx.x == 0) {
+        st_agent(&ws.rows[r].tkey, a);
+        st_agent(&ws.rows[r].dkey, b);
+        st_agent(&ws.rows[r].nan, (unsigned)n);
+        st_agent((u32*)&ws.rows[r].fp, __float_as_uint(fp));
+        st_agent((u32*)&ws.rows[r].fq, __float_as_uint(fq));
+    }
+    if (!arrive_last(&ws.seq_counters[seq], (unsigned)W1, &s_flag)) return;
+    decide_rows(seq, width, vocab, stride, target, draft, draft_ids, temps, u_accept, u_resample, ws);
+}
+
+// ---- the exact pass ----
 // Grid (S3, n_seq), the draw's grid. A pending sequence whose accepted count is final (j0 == j1) has one row left,
 // the row it draws from; block b takes that row's tiles [b tpb, (b + 1) tpb) in the draw's layout (sub-tile p = tile
 // NWD + wave holds elements [SUB p, SUB (p + 1))) and sums its exact masses, Zp and Zq. In the same sweep it prepares
@@ -1395,7 +1251,7 @@ __global__ void __launch_bounds__(NT) spec_draw_k(const float* __restrict__ targ
     const int nsub = tiles * NWD;
     const SeqInfo si = load_seq(ws.seqs, seq);
     const bool drawing = si.status == GBS_ROW_OK && si.mode != 0;
-    if (final_written && !drawing) return;  // the one-read form's exact pass wrote this sequence's outputs
+    if (final_written && !drawing) return;  // the exact pass wrote this sequence's outputs
     const float* tr = target + (size_t)si.row * (size_t)stride;
     const float* dr = draft + (size_t)si.row * (size_t)stride;
     u128* wp = ws.wparts + (size_t)seq * nsub;
@@ -1451,20 +1307,17 @@ GBS_EXPORT int gbs_spec_verify(const float* target, const float* draft, int n_se
                            u_resample, w);
         rc = launch_status();
         if (rc) return rc;
-        hipLaunchKernelGGL(spec_exact_k, dim3(p.SZ, n_seq), dim3(NT), 0, st, target, dr, width, vocab, ld, p.tpb, vec, draft_ids,
-                           temperatures, u_accept, u_resample, w, out_accepted, out_tokens, out_status);
-        rc = launch_status();
-        if (rc) return rc;
     } else {
-        hipLaunchKernelGGL(spec_max_k, dim3(p.S, p.R), dim3(NT), 0, st, target, dr, width, vocab, ld, chunk, vec, w);
-        rc = launch_status();
-        if (rc) return rc;
-        hipLaunchKernelGGL(spec_mass_k, dim3(p.S, p.R), dim3(NT), 0, st, target, dr, width, vocab, ld, chunk, vec, draft_ids, temperatures,
+        hipLaunchKernelGGL(spec_split_k, dim3(p.S, p.R), dim3(NT), 0, st, target, dr, width, vocab, ld, chunk, vec, draft_ids, temperatures,
                            u_accept, u_resample, w);
         rc = launch_status();
         if (rc) return rc;
     }
+    hipLaunchKernelGGL(spec_exact_k, dim3(p.SZ, n_seq), dim3(NT), 0, st, target, dr, width, vocab, ld, p.tpb, vec, draft_ids, temperatures,
+                       u_accept, u_resample, w, out_accepted, out_tokens, out_status);
+    rc = launch_status();
+    if (rc) return rc;
     hipLaunchKernelGGL(spec_draw_k, dim3(p.S3, n_seq), dim3(NT), 0, st, target, dr, width, vocab, ld, p.tpb, vec, draft_ids, u_resample, w,
-                       out_accepted, out_tokens, out_status, p.R >= ROWS_KERNEL_MIN);
+                       out_accepted, out_tokens, out_status, true);
     return launch_status();
 }
