@@ -114,15 +114,23 @@ struct SpecWs {
     RowInfo* rows;           // [R]
     SeqInfo* seqs;           // [n_seq]
     u128* wparts;            // [n_seq][tiles][NWD]: the draw's sub-tile weights
-    u64* zparts;             // [R][SZ][2]: the exact sums, per block of the exact pass
+    u64* zparts;             // [R][SZ][2]: the exact sums, per block of the exact pass (or per row block)
     SubRec* subrecs;         // [n_seq][tiles][NWD]: the exact pass's sub-tile sums for the draw
     AmbRec* ambs;            // [n_seq][AMB_SEQ_CAP]: its undecided tokens (counted in draw_counters, zero after)
+    unsigned* fstate;        // [n_seq]: whether the row blocks swept the draw row themselves (FS_*; zero after)
 };
+
+// The row kernel's blocks of a sequence sweep its draw row themselves once the sequence is decided, instead of the exact
+// pass's grid: the deciding block publishes FS_GO or FS_NO, and a block that waits past its time limit claims
+// FS_GIVEN_UP, after which the exact pass does the sweep. Whoever moves the word from FS_OPEN first decides, so the
+// sequence's blocks all sweep or none do.
+constexpr unsigned FS_OPEN = 0, FS_GO = 1, FS_NO = 2, FS_GIVEN_UP = 3;
+constexpr int FAMB_CAP = 256;  // undecided tokens a row block keeps while it sweeps
 
 // The counters that must be zero between launches sit at fixed offsets in the first SPEC_CTL_BYTES (room for 65535
 // rows and sequences, whatever this launch's shape); every launch leaves them zero. The rest is written before it is
 // read, so a workspace cleared once serves launches of any shape.
-constexpr size_t SPEC_CTL_BYTES = 3 * (size_t)65536 * 4;
+constexpr size_t SPEC_CTL_BYTES = 4 * (size_t)65536 * 4;
 
 struct Plan {
     int R, S, S3, tpb, SZ;
@@ -139,7 +147,8 @@ Plan plan(int n_seq, int width, int vocab) {
     want = want < 1 ? 1 : (want > tiles ? tiles : want);
     p.tpb = (tiles + want - 1) / want;
     p.S3 = (tiles + p.tpb - 1) / p.tpb;
-    p.SZ = p.S3;  // the exact pass runs on the draw's grid
+    // per-block exact sums per row: one per block of the exact pass's grid, or per row of a sequence (the row blocks')
+    p.SZ = p.S3 > width + 1 ? p.S3 : width + 1;
     p.bytes = SPEC_CTL_BYTES + align256((size_t)p.R * p.S * 16) + align256((size_t)p.R * p.S * 4) + align256((size_t)p.R * p.S * 16) +
               align256((size_t)p.R * sizeof(RowInfo)) + align256((size_t)n_seq * sizeof(SeqInfo)) +
               align256((size_t)n_seq * tiles * NWD * 16) + align256((size_t)p.R * p.SZ * 16) +
@@ -153,6 +162,7 @@ SpecWs carve(void* ws, int n_seq, int vocab, const Plan& p) {
     w.row_counters = (unsigned*)c; c += (size_t)65536 * 4;
     w.seq_counters = (unsigned*)c; c += (size_t)65536 * 4;
     w.draw_counters = (unsigned*)c; c += (size_t)65536 * 4;
+    w.fstate = (unsigned*)c; c += (size_t)65536 * 4;
     w.maxparts = (u64*)c; c += align256((size_t)p.R * p.S * 16);
     w.nanparts = (unsigned*)c; c += align256((size_t)p.R * p.S * 4);
     w.sumparts = (u64*)c; c += align256((size_t)p.R * p.S * 16);
@@ -404,11 +414,26 @@ __device__ __forceinline__ unsigned accept_bounds(float u, u64 ep, u64 eq, float
     return ACC_OPEN;
 }
 
+// The draw row's float sums bound its exact mass sums (as accept_bounds takes them) when both are finite and >= 1
+__device__ __forceinline__ bool ratio_bounds_ok(float fp, float fq) { return isfinite(fp) && isfinite(fq) && fp >= 1.0f && fq >= 1.0f; }
+
+// Bounds on Zp / Zq from those sums: a token with Ep / Eq >= hi has the residual weight Ep Zq - Eq Zp, one with
+// Ep / Eq <= lo has none
+__device__ __forceinline__ void ratio_bounds(float fp, float fq, int vocab, float& hi, float& lo) {
+    const double one = 17592186044416.0, V = (double)vocab;
+    const double hp = (double)fp * one * (1.0 + ACC_REL) + V, hq = (double)fq * one * (1.0 + ACC_REL) + V;
+    const double lp = fmax((double)fp * one * (1.0 - ACC_REL) - V, one), lq = fmax((double)fq * one * (1.0 - ACC_REL) - V, one);
+    hi = (float)(hp / lq);
+    lo = (float)(lp / hq);
+}
+
 // The sequence's decisions, by the block that completes the sequence's last row. Thread j checks
 // row j (its parameters, flags and the draft's bounded test); the first row whose test is not ACC_YES is j0, the first
 // ACC_NO (or the bonus row) j1. With j0 == j1 the accepted count is final; the draw then needs row j1's exact sums
 // (pending), unless its temperature is 0. With j0 < j1 the tests from j0 on wait for exact sums (pending).
-__device__ void decide_rows(int seq, int width, int vocab, long long stride, const float* __restrict__ target, const float* __restrict__ draft,
+// Returns, on thread 0, whether the draw row's sweep can run in the exact pass's one-read form with the fast masses
+// (the row blocks may then sweep it themselves).
+__device__ bool decide_rows(int seq, int width, int vocab, long long stride, const float* __restrict__ target, const float* __restrict__ draft,
                             const int* __restrict__ draft_ids, const float* __restrict__ temps, const float* __restrict__ u_accept,
                             const float* __restrict__ u_resample, SpecWs ws) {
     const int W1 = width + 1;
@@ -454,7 +479,7 @@ __device__ void decide_rows(int seq, int width, int vocab, long long stride, con
         if (f) atomicOr(&s_all, f);
     }
     __syncthreads();
-    if (threadIdx.x != 0) return;
+    if (threadIdx.x != 0) return false;
     SeqInfo si{};
     si.status = GBS_ROW_OK;
     const int all = s_all;
@@ -489,6 +514,9 @@ __device__ void decide_rows(int seq, int width, int vocab, long long stride, con
     st_agent(&ws.seqs[seq].pending, si.pending);
     st_agent((u32*)&ws.seqs[seq].fp, __float_as_uint(si.fp));
     st_agent((u32*)&ws.seqs[seq].fq, __float_as_uint(si.fq));
+    if (si.status != GBS_ROW_OK || si.pending == 0 || si.j0 != si.j1 || si.mode == 0) return false;
+    const bool fast = mass_fast_ok(si.Mp, si.c2) && mass_fast_ok(si.Mq, si.c2);
+    return fast && (si.mode == 2 || ratio_bounds_ok(si.fp, si.fq));
 }
 
 // Streams elements [lo, hi) of a target row (and of the draft row when `two`) through g(t, d, i0) by 4-element groups
@@ -584,12 +612,23 @@ __device__ __forceinline__ void rows_sweep(const float* tr, const float* dr, boo
     });
 }
 
+template <int MODE, bool FAST, int CAP>
+__device__ __forceinline__ void exact_subtiles(const float* tr, const float* dr, int vocab, int p0, int step, int p1, bool vec, float Mp, float Mq,
+                                               float c2, float rho_hi, float rho_lo, SubRec* recs, AmbRec* s_amb, unsigned* s_namb, u64& zp,
+                                               u64& zq);
+
+constexpr long long FUSE_WAIT_TICKS = 10000;  // a row block's wait for its sequence's decision: 100 us of the 100 MHz clock
+
+// fuse: the row blocks sweep their sequence's draw row once it is decided (every block of the launch resident at once),
+// writing the exact pass's per-block sums at [row][sz] of zparts, its sub-tile sums and its list of undecided tokens
 __global__ void __launch_bounds__(RNT) spec_rows_k(const float* __restrict__ target, const float* __restrict__ draft, int width, int vocab, long long stride,
                                                    bool vec, const int* __restrict__ draft_ids, const float* __restrict__ temps,
-                                                   const float* __restrict__ u_accept, const float* __restrict__ u_resample, SpecWs ws) {
+                                                   const float* __restrict__ u_accept, const float* __restrict__ u_resample, SpecWs ws,
+                                                   bool fuse, int sz) {
     __shared__ u64 s_red[RNT / WAVE];
     __shared__ float s_redf[RNT / WAVE];
-    __shared__ unsigned s_flag;
+    __shared__ unsigned s_flag, s_go, s_namb;
+    __shared__ AmbRec s_amb[FAMB_CAP];
     const int r = blockIdx.x;
     const int W1 = width + 1;
     const int seq = r / W1;
@@ -625,8 +664,72 @@ __global__ void __launch_bounds__(RNT) spec_rows_k(const float* __restrict__ tar
         st_agent((u32*)&ws.rows[r].fp, __float_as_uint(fp));
         st_agent((u32*)&ws.rows[r].fq, __float_as_uint(fq));
     }
-    if (!arrive_last(&ws.seq_counters[seq], (unsigned)W1, &s_flag)) return;
-    decide_rows(seq, width, vocab, stride, target, draft, draft_ids, temps, u_accept, u_resample, ws);
+    const bool last = arrive_last(&ws.seq_counters[seq], (unsigned)W1, &s_flag);
+    const bool go = last && decide_rows(seq, width, vocab, stride, target, draft, draft_ids, temps, u_accept, u_resample, ws);
+    if (!fuse) return;
+    if (threadIdx.x == 0) {
+        unsigned* word = &ws.fstate[seq];
+        unsigned v;
+        if (last) {
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            __builtin_amdgcn_s_waitcnt(0);  // the sequence's record has been stored
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            unsigned expect = FS_OPEN;
+            const bool set = __hip_atomic_compare_exchange_strong(word, &expect, go ? FS_GO : FS_NO, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                                  __HIP_MEMORY_SCOPE_AGENT);
+            v = set ? (go ? FS_GO : FS_NO) : expect;
+        } else {
+            const long long t_end = (long long)wall_clock64() + FUSE_WAIT_TICKS;
+            while ((v = __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) == FS_OPEN) {
+                if ((long long)wall_clock64() > t_end) {
+                    unsigned expect = FS_OPEN;
+                    const bool set = __hip_atomic_compare_exchange_strong(word, &expect, FS_GIVEN_UP, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                                          __HIP_MEMORY_SCOPE_AGENT);
+                    v = set ? FS_GIVEN_UP : expect;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(8);
+            }
+        }
+        s_go = v == FS_GO ? 1u : 0u;
+        s_namb = 0u;
+    }
+    __syncthreads();
+    if (!s_go) return;
+    // this block's share of the draw row's sub-tiles, one per wave at a time
+    const SeqInfo si = load_seq(ws.seqs, seq);
+    const int nsub = (vocab + TILE - 1) / TILE * NWD;
+    const int sp = r - seq * W1, per = (nsub + W1 - 1) / W1;
+    const int pb = min(nsub, sp * per), pe = min(nsub, pb + per);
+    const int p0 = pb + (int)threadIdx.x / WAVE;
+    const float* tq = target + (size_t)si.row * (size_t)stride;
+    const float* dq = draft + (size_t)si.row * (size_t)stride;
+    SubRec* recs = ws.subrecs + (size_t)seq * nsub;
+    u64 zp = 0, zq = 0;
+    if (si.mode == 1) {
+        float hi, lo;
+        ratio_bounds(si.fp, si.fq, vocab, hi, lo);
+        exact_subtiles<1, true, FAMB_CAP>(tq, dq, vocab, p0, RNT / WAVE, pe, vec, si.Mp, si.Mq, si.c2, hi, lo, recs, s_amb, &s_namb, zp, zq);
+    } else {
+        exact_subtiles<2, true, FAMB_CAP>(tq, dq, vocab, p0, RNT / WAVE, pe, vec, si.Mp, si.Mq, si.c2, 0.0f, 0.0f, recs, s_amb, &s_namb, zp, zq);
+    }
+    zp = block_sum_u64<RNT>(zp, s_red);  // (its barriers also publish s_namb and s_amb)
+    zq = block_sum_u64<RNT>(zq, s_red);
+    const unsigned nb = s_namb < (unsigned)FAMB_CAP ? s_namb : (unsigned)FAMB_CAP;
+    if (threadIdx.x == 0) {
+        st_agent(&ws.zparts[((size_t)si.row * sz + sp) * 2], zp);
+        st_agent(&ws.zparts[((size_t)si.row * sz + sp) * 2 + 1], zq);
+        s_flag = s_namb != 0u ? atomicAdd(&ws.draw_counters[seq], s_namb > (unsigned)FAMB_CAP ? (unsigned)AMB_SEQ_CAP + 1u : s_namb) : 0u;
+    }
+    __syncthreads();
+    AmbRec* list = ws.ambs + (size_t)seq * AMB_SEQ_CAP;
+    for (unsigned i = threadIdx.x; i < nb; i += RNT) {
+        if (s_flag + i < (unsigned)AMB_SEQ_CAP) {
+            st_agent(&list[s_flag + i].ep, s_amb[i].ep);
+            st_agent(&list[s_flag + i].eq, s_amb[i].eq);
+            st_agent(&list[s_flag + i].p, s_amb[i].p);
+        }
+    }
 }
 
 // inclusive prefix sum of a u128 over the wave
@@ -910,15 +1013,18 @@ __global__ void __launch_bounds__(NT) spec_split_k(const float* __restrict__ tar
 // a mass (< 2^46) as a float, within 2^-23 of it: two exact conversions and one rounding fused multiply-add
 __device__ __forceinline__ float to_float(u64 v) { return fmaf((float)(u32)(v >> 32), 4294967296.0f, (float)(u32)v); }
 
-template <int MODE, bool FAST>
-__device__ __forceinline__ void exact_tiles(const float* tr, const float* dr, int vocab, int t0, int t1, bool vec, float Mp, float Mq, float c2,
-                                            float rho_hi, float rho_lo, SubRec* recs, AmbRec* s_amb, unsigned* s_namb, u64& zp, u64& zq) {
-    const int tid = (int)threadIdx.x, w = tid / WAVE, l = lane_id();
+// Sub-tiles p0, p0 + step, ... below p1 (a sub-tile is one wave's SUB elements; sub-tile p starts at element p SUB),
+// each summed by the calling wave; undecided tokens go to s_amb (CAP entries, *s_namb counts them all).
+template <int MODE, bool FAST, int CAP>
+__device__ __forceinline__ void exact_subtiles(const float* tr, const float* dr, int vocab, int p0, int step, int p1, bool vec, float Mp, float Mq,
+                                               float c2, float rho_hi, float rho_lo, SubRec* recs, AmbRec* s_amb, unsigned* s_namb, u64& zp,
+                                               u64& zq) {
+    const int l = lane_id();
     const __amdgpu_buffer_rsrc_t rt = rsrc(tr, (u32)vocab * 4u), rd = rsrc(MODE == 1 ? dr : tr, (u32)vocab * 4u);
-    auto issue = [&](int tile, float (&t)[DU * 4], float (&d)[DU * 4]) {
+    auto issue = [&](int p, float (&t)[DU * 4], float (&d)[DU * 4]) {
 #pragma unroll
         for (int j = 0; j < DU; ++j) {
-            const int e = tile * TILE + w * SUB + j * (WAVE * 4) + l * 4;
+            const int e = p * SUB + j * (WAVE * 4) + l * 4;
             if (vec) {
                 const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(rt, (u32)e * 4u, 0, 2);
                 u32x4 b = {0u, 0u, 0u, 0u};
@@ -939,20 +1045,19 @@ __device__ __forceinline__ void exact_tiles(const float* tr, const float* dr, in
     };
     constexpr float LO = 1.0f - 1.0f / 524288.0f, HI = 1.0f + 1.0f / 524288.0f;  // 1 -+ 2^-19, over the float roundings
     float tn[DU * 4], dn[DU * 4];
-    if (t0 < t1) issue(t0, tn, dn);
-    for (int tile = t0; tile < t1; ++tile) {
+    if (p0 < p1) issue(p0, tn, dn);
+    for (int p = p0; p < p1; p += step) {
         float t[DU * 4], d[DU * 4];
 #pragma unroll
         for (int i = 0; i < DU * 4; ++i) {
             t[i] = tn[i];
             d[i] = dn[i];
         }
-        if (tile + 1 < t1) issue(tile + 1, tn, dn);
-        const int p = tile * NWD + w;
+        if (p + step < p1) issue(p + step, tn, dn);
         u64 A = 0, B = 0;
 #pragma unroll
         for (int j = 0; j < DU; ++j) {
-            const int e = tile * TILE + w * SUB + j * (WAVE * 4) + l * 4;
+            const int e = p * SUB + j * (WAVE * 4) + l * 4;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const bool in = e + q < vocab;  // buffer loads past the row's end return 0, not -inf
@@ -971,7 +1076,7 @@ __device__ __forceinline__ void exact_tiles(const float* tr, const float* dr, in
                     const bool amb = !pos && !neg;
                     if (ballot(amb) != 0ull && amb) {
                         const unsigned slot = atomicAdd(s_namb, 1u);
-                        if (slot < (unsigned)AMB_CAP) s_amb[slot] = AmbRec{ep, eq, (u32)p, 0u};
+                        if (slot < (unsigned)CAP) s_amb[slot] = AmbRec{ep, eq, (u32)p, 0u};
                     }
                 }
             }
@@ -986,7 +1091,7 @@ __device__ __forceinline__ void exact_tiles(const float* tr, const float* dr, in
 }
 
 __global__ void __launch_bounds__(NT) spec_exact_k(const float* __restrict__ target, const float* __restrict__ draft, int width, int vocab,
-                                                   long long stride, int tpb, bool vec, const int* __restrict__ draft_ids,
+                                                   long long stride, int tpb, int zs, bool vec, const int* __restrict__ draft_ids,
                                                    const float* __restrict__ temps, const float* __restrict__ u_accept,
                                                    const float* __restrict__ u_resample, SpecWs ws, int* __restrict__ out_accepted,
                                                    int* __restrict__ out_tokens, int* __restrict__ out_status) {
@@ -1006,6 +1111,9 @@ __global__ void __launch_bounds__(NT) spec_exact_k(const float* __restrict__ tar
     const int pending = uni(ld_agent(&ws.seqs[seq].pending));
     const int j0 = uni(ld_agent(&ws.seqs[seq].j0)), j1 = uni(ld_agent(&ws.seqs[seq].j1));
     const bool work = si.status == GBS_ROW_OK && pending != 0;
+    // swept: the row blocks summed the draw row (its blocks' sums are parts 0..width of zparts); block 0 finishes
+    const bool swept = uni(ld_agent(&ws.fstate[seq])) == FS_GO;
+    if (swept && sp != 0) return;
     if (work && j0 == j1) {
         const int mode = si.mode;
         const float* tr = target + (size_t)si.row * (size_t)stride;
@@ -1014,59 +1122,61 @@ __global__ void __launch_bounds__(NT) spec_exact_k(const float* __restrict__ tar
         const bool fast = mass_fast_ok(Mp, c2) && mass_fast_ok(Mq, c2);
         // the ratio bounds from the row's float sums (as accept_bounds takes them)
         const float fp = si.fp, fq = si.fq;
-        const bool bounds = fast && isfinite(fp) && isfinite(fq) && fp >= 1.0f && fq >= 1.0f;
+        const bool bounds = fast && ratio_bounds_ok(fp, fq);
         const bool fused = mode == 2 || bounds;
         float rho_hi = 0.0f, rho_lo = 0.0f;
-        if (mode == 1 && bounds) {
-            const double one = 17592186044416.0, V = (double)vocab;
-            const double hp = (double)fp * one * (1.0 + ACC_REL) + V, hq = (double)fq * one * (1.0 + ACC_REL) + V;
-            const double lp = fmax((double)fp * one * (1.0 - ACC_REL) - V, one), lq = fmax((double)fq * one * (1.0 - ACC_REL) - V, one);
-            rho_hi = (float)(hp / lq);
-            rho_lo = (float)(lp / hq);
-        }
+        if (mode == 1 && bounds) ratio_bounds(fp, fq, vocab, rho_hi, rho_lo);
         SubRec* recs = ws.subrecs + (size_t)seq * nsub;
         AmbRec* list = ws.ambs + (size_t)seq * AMB_SEQ_CAP;
-        const int t0 = sp * tpb, t1 = min(tiles, t0 + tpb);
-        u64 zp = 0, zq = 0;
-        if (threadIdx.x == 0) s_namb = 0;
-        __syncthreads();
-        if (fused) {
-            if (mode == 1) exact_tiles<1, true>(tr, dr, vocab, t0, t1, vec, Mp, Mq, c2, rho_hi, rho_lo, recs, s_amb, &s_namb, zp, zq);
-            else if (fast) exact_tiles<2, true>(tr, dr, vocab, t0, t1, vec, Mp, Mq, c2, 0.0f, 0.0f, recs, s_amb, &s_namb, zp, zq);
-            else exact_tiles<2, false>(tr, dr, vocab, t0, t1, vec, Mp, Mq, c2, 0.0f, 0.0f, recs, s_amb, &s_namb, zp, zq);
-        } else {
-            const int lo = min(vocab, t0 * TILE), hi = min(vocab, t1 * TILE);
-            stream_rows<false>(tr, dr, mode == 1, vocab, lo, hi, vec, [&](float t, float d, int) {
-                zp += t > -INFINITY ? mass(t, Mp, c2) : 0ull;
-                zq += d > -INFINITY ? mass(d, Mq, c2) : 0ull;
-            });
-        }
-        zp = block_sum_u64<NT>(zp, s_red);  // (its barriers also publish s_namb and s_amb)
-        zq = block_sum_u64<NT>(zq, s_red);
-        // the block's undecided tokens go to the sequence's list, at a place taken by one atomic (the block's count is
-        // added even past the list's end, so that the last block sees the overflow)
-        const unsigned nb = s_namb < (unsigned)AMB_CAP ? s_namb : (unsigned)AMB_CAP;
-        if (threadIdx.x == 0) {
-            st_agent(&ws.zparts[((size_t)si.row * S + sp) * 2], zp);
-            st_agent(&ws.zparts[((size_t)si.row * S + sp) * 2 + 1], zq);
-            s_flag = s_namb != 0u ? atomicAdd(&ws.draw_counters[seq], s_namb > (unsigned)AMB_CAP ? (unsigned)AMB_SEQ_CAP + 1u : s_namb) : 0u;
-        }
-        __syncthreads();
-        const unsigned base = s_flag;
-        for (unsigned i = threadIdx.x; i < nb; i += NT) {
-            if (base + i < (unsigned)AMB_SEQ_CAP) {
-                st_agent(&list[base + i].ep, s_amb[i].ep);
-                st_agent(&list[base + i].eq, s_amb[i].eq);
-                st_agent(&list[base + i].p, s_amb[i].p);
+        if (!swept) {
+            const int t0 = sp * tpb, t1 = min(tiles, t0 + tpb);
+            u64 zp = 0, zq = 0;
+            if (threadIdx.x == 0) s_namb = 0;
+            __syncthreads();
+            if (fused) {
+                // the block's tiles, sub-tile w of each to wave w
+                const int w = (int)threadIdx.x / WAVE, p0 = t0 * NWD + w, p1 = t1 * NWD;
+                if (mode == 1)
+                    exact_subtiles<1, true, AMB_CAP>(tr, dr, vocab, p0, NWD, p1, vec, Mp, Mq, c2, rho_hi, rho_lo, recs, s_amb, &s_namb, zp, zq);
+                else if (fast)
+                    exact_subtiles<2, true, AMB_CAP>(tr, dr, vocab, p0, NWD, p1, vec, Mp, Mq, c2, 0.0f, 0.0f, recs, s_amb, &s_namb, zp, zq);
+                else
+                    exact_subtiles<2, false, AMB_CAP>(tr, dr, vocab, p0, NWD, p1, vec, Mp, Mq, c2, 0.0f, 0.0f, recs, s_amb, &s_namb, zp, zq);
+            } else {
+                const int lo = min(vocab, t0 * TILE), hi = min(vocab, t1 * TILE);
+                stream_rows<false>(tr, dr, mode == 1, vocab, lo, hi, vec, [&](float t, float d, int) {
+                    zp += t > -INFINITY ? mass(t, Mp, c2) : 0ull;
+                    zq += d > -INFINITY ? mass(d, Mq, c2) : 0ull;
+                });
             }
+            zp = block_sum_u64<NT>(zp, s_red);  // (its barriers also publish s_namb and s_amb)
+            zq = block_sum_u64<NT>(zq, s_red);
+            // the block's undecided tokens go to the sequence's list, at a place taken by one atomic (the block's count is
+            // added even past the list's end, so that the last block sees the overflow)
+            const unsigned nb = s_namb < (unsigned)AMB_CAP ? s_namb : (unsigned)AMB_CAP;
+            if (threadIdx.x == 0) {
+                st_agent(&ws.zparts[((size_t)si.row * zs + sp) * 2], zp);
+                st_agent(&ws.zparts[((size_t)si.row * zs + sp) * 2 + 1], zq);
+                s_flag = s_namb != 0u ? atomicAdd(&ws.draw_counters[seq], s_namb > (unsigned)AMB_CAP ? (unsigned)AMB_SEQ_CAP + 1u : s_namb) : 0u;
+            }
+            __syncthreads();
+            const unsigned base = s_flag;
+            for (unsigned i = threadIdx.x; i < nb; i += NT) {
+                if (base + i < (unsigned)AMB_SEQ_CAP) {
+                    st_agent(&list[base + i].ep, s_amb[i].ep);
+                    st_agent(&list[base + i].eq, s_amb[i].eq);
+                    st_agent(&list[base + i].p, s_amb[i].p);
+                }
+            }
+            if (!arrive_last(&ws.row_counters[seq], (unsigned)S, &s_flag)) return;
         }
-        if (!arrive_last(&ws.row_counters[seq], (unsigned)S, &s_flag)) return;
         // the last block: every load at once (the blocks' sums, the sub-tile sums, the list's length and its first
         // 2 NT entries), then the exact sums, the sub-tile weights and the draw
         u64 a = 0, b = 0;
-        for (int o = (int)threadIdx.x; o < S; o += NT) {
-            a += ld_agent(&ws.zparts[((size_t)si.row * S + o) * 2]);
-            b += ld_agent(&ws.zparts[((size_t)si.row * S + o) * 2 + 1]);
+        const int parts = swept ? W1 : S;
+        for (int o = (int)threadIdx.x; o < parts; o += NT) {
+            a += ld_agent(&ws.zparts[((size_t)si.row * zs + o) * 2]);
+            b += ld_agent(&ws.zparts[((size_t)si.row * zs + o) * 2 + 1]);
         }
         constexpr int PPT = (GBS_MAX_VOCAB + TILE - 1) / TILE * NWD / NT;  // sub-tiles per thread at the largest vocabulary
         u64 A[PPT], B[PPT];
@@ -1173,8 +1283,8 @@ __global__ void __launch_bounds__(NT) spec_exact_k(const float* __restrict__ tar
             zp = block_sum_u64<NT>(zp, s_red);
             zq = block_sum_u64<NT>(zq, s_red);
             if (threadIdx.x == 0) {
-                st_agent(&ws.zparts[((size_t)r * S + sp) * 2], zp);
-                st_agent(&ws.zparts[((size_t)r * S + sp) * 2 + 1], zq);
+                st_agent(&ws.zparts[((size_t)r * zs + sp) * 2], zp);
+                st_agent(&ws.zparts[((size_t)r * zs + sp) * 2 + 1], zq);
             }
         }
     }
@@ -1191,8 +1301,8 @@ __global__ void __launch_bounds__(NT) spec_exact_k(const float* __restrict__ tar
         u64 a = 0, b = 0;
         if (T != 0.0f) {
             for (int o = (int)threadIdx.x; o < S; o += NT) {
-                a += ld_agent(&ws.zparts[((size_t)r * S + o) * 2]);
-                b += ld_agent(&ws.zparts[((size_t)r * S + o) * 2 + 1]);
+                a += ld_agent(&ws.zparts[((size_t)r * zs + o) * 2]);
+                b += ld_agent(&ws.zparts[((size_t)r * zs + o) * 2 + 1]);
             }
             a = block_sum_u64<NT>(a, s_red);
             b = block_sum_u64<NT>(b, s_red);
@@ -1251,6 +1361,7 @@ __global__ void __launch_bounds__(NT) spec_draw_k(const float* __restrict__ targ
     const int nsub = tiles * NWD;
     const SeqInfo si = load_seq(ws.seqs, seq);
     const bool drawing = si.status == GBS_ROW_OK && si.mode != 0;
+    if (sp == 0 && threadIdx.x == 0) st_agent(&ws.fstate[seq], FS_OPEN);  // read for the last time by the exact pass
     if (final_written && !drawing) return;  // the exact pass wrote this sequence's outputs
     const float* tr = target + (size_t)si.row * (size_t)stride;
     const float* dr = draft + (size_t)si.row * (size_t)stride;
@@ -1278,8 +1389,20 @@ __global__ void __launch_bounds__(NT) spec_draw_k(const float* __restrict__ targ
     if (threadIdx.x == 0) write_outputs(seq, si, token, width, draft_ids, out_accepted, out_tokens, out_status);
 }
 
-}  // namespace
+// compute units of the current device (0 when the query fails: the row blocks then never sweep the draw rows)
+int cu_count() {
+    static int counts[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    if (counts[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+        counts[dev] = n;
+    }
+    return counts[dev];
+}
 
+}  // namespace
 
 GBS_EXPORT size_t gbs_spec_verify_workspace_bytes(int n_seq, int width, int vocab) {
     if (n_seq <= 0 || width < 0 || vocab <= 0 || vocab > GBS_MAX_VOCAB) return 0;
@@ -1303,8 +1426,11 @@ GBS_EXPORT int gbs_spec_verify(const float* target, const float* draft, int n_se
     const long long ld = stride;
     int rc;
     if (p.R >= ROWS_KERNEL_MIN) {
+        // the row blocks sweep the draw rows only when all of them are resident at once (one per CU) and the exact
+        // pass's per-block sums have room for one per row of a sequence
+        const bool fuse = p.R <= cu_count() && !getenv("GBS_SPEC_FUSE_OFF");
         hipLaunchKernelGGL(spec_rows_k, dim3(p.R), dim3(RNT), 0, st, target, dr, width, vocab, ld, vec, draft_ids, temperatures, u_accept,
-                           u_resample, w);
+                           u_resample, w, fuse, p.SZ);
         rc = launch_status();
         if (rc) return rc;
     } else {
@@ -1313,7 +1439,7 @@ GBS_EXPORT int gbs_spec_verify(const float* target, const float* draft, int n_se
         rc = launch_status();
         if (rc) return rc;
     }
-    hipLaunchKernelGGL(spec_exact_k, dim3(p.SZ, n_seq), dim3(NT), 0, st, target, dr, width, vocab, ld, p.tpb, vec, draft_ids, temperatures,
+    hipLaunchKernelGGL(spec_exact_k, dim3(p.S3, n_seq), dim3(NT), 0, st, target, dr, width, vocab, ld, p.tpb, p.SZ, vec, draft_ids, temperatures,
                        u_accept, u_resample, w, out_accepted, out_tokens, out_status);
     rc = launch_status();
     if (rc) return rc;
