@@ -76,6 +76,7 @@ struct RowInfo {
     unsigned state;  // the draft's test by the float sums, ACC_YES / ACC_NO / ACC_OPEN
     float fp, fq;    // float sums of 2^((l - M) c2) over the target and the draft row
     u64 ep, eq;      // the draft token's masses (a draft row at T > 0 whose test ran)
+    unsigned check;  // the row block's own check (row_check), when the row kernel made it
 };
 
 // the test of a draft from float bounds on the mass sums
@@ -427,15 +428,79 @@ __device__ __forceinline__ void ratio_bounds(float fp, float fq, int vocab, floa
     lo = (float)(lp / hq);
 }
 
+// A row's inputs to its check: its temperature, and for a draft row its uniform, token and the two logits of the token
+struct RowArgs {
+    float T, u, tx, dx;
+    int x;
+    bool ures_ok;  // the sequence's resampling uniform is in [0, 1) (checked with row 0)
+};
+
+__device__ __forceinline__ RowArgs row_args(int seq, int j, int width, int vocab, long long stride, const float* __restrict__ target,
+                                            const float* __restrict__ draft, const int* __restrict__ draft_ids, const float* __restrict__ temps,
+                                            const float* __restrict__ u_accept, const float* __restrict__ u_resample) {
+    const int r = seq * (width + 1) + j;
+    RowArgs a;
+    a.T = temps[r];
+    a.ures_ok = true;
+    if (j == 0) {
+        const float ur = u_resample[seq];
+        a.ures_ok = ur >= 0.0f && ur < 1.0f;
+    }
+    a.u = 0.0f;
+    a.x = 0;
+    a.tx = a.dx = -INFINITY;
+    if (j < width) {
+        a.u = u_accept[(size_t)seq * width + j];
+        a.x = draft_ids[(size_t)seq * width + j];
+        if (a.x >= 0 && a.x < vocab) {
+            a.tx = target[(size_t)r * (size_t)stride + a.x];
+            a.dx = draft[(size_t)r * (size_t)stride + a.x];
+        }
+    }
+    return a;
+}
+
+// Row r (row j of its sequence): its parameters and flags, and for a draft the test by the float bounds (its state and
+// the token's masses are stored in the row's record). Returns state | flags << 4 (flags: 1 invalid parameter, 2 NaN,
+// 4 no candidate).
+__device__ __forceinline__ unsigned row_check(int r, int j, int width, int vocab, const RowArgs& a, const RowInfo& ri, float fp, float fq,
+                                              SpecWs ws) {
+    const float Tj = a.T;
+    bool bad = !temp_ok(Tj) || !a.ures_ok;
+    unsigned state = ACC_NO;
+    if (j < width) {
+        const float u = a.u;
+        const int x = a.x;
+        bad |= !(u >= 0.0f && u < 1.0f) || x < 0 || x >= vocab;
+        if (!bad && !ri.nan && ri.tkey != 0ull && ri.dkey != 0ull) {
+            if (Tj == 0.0f) state = x == (int)key_id(ri.tkey) ? ACC_YES : ACC_NO;
+            else {
+                const float cj = temp_scale(Tj);
+                const float Mp = key_value(ri.tkey), Mq = key_value(ri.dkey);
+                const u64 ep = a.tx > -INFINITY ? mass(a.tx, Mp, cj) : 0ull;
+                const u64 eq = a.dx > -INFINITY ? mass(a.dx, Mq, cj) : 0ull;
+                state = (mass_fast_ok(Mp, cj) && mass_fast_ok(Mq, cj)) ? accept_bounds(u, ep, eq, fp, fq, vocab) : ACC_OPEN;
+                st_agent(&ws.rows[r].ep, ep);
+                st_agent(&ws.rows[r].eq, eq);
+            }
+        }
+        st_agent(&ws.rows[r].state, state);
+    }
+    unsigned f = bad ? 1u : 0u;
+    f |= ri.nan != 0u ? 2u : 0u;
+    f |= (ri.tkey == 0ull || (j < width && ri.dkey == 0ull)) ? 4u : 0u;
+    return state | f << 4;
+}
+
 // The sequence's decisions, by the block that completes the sequence's last row. Thread j checks
-// row j (its parameters, flags and the draft's bounded test); the first row whose test is not ACC_YES is j0, the first
+// row j (its parameters, flags and the draft's bounded test; pretested: the row block checked it already); the first row whose test is not ACC_YES is j0, the first
 // ACC_NO (or the bonus row) j1. With j0 == j1 the accepted count is final; the draw then needs row j1's exact sums
 // (pending), unless its temperature is 0. With j0 < j1 the tests from j0 on wait for exact sums (pending).
 // Returns, on thread 0, whether the draw row's sweep can run in the exact pass's one-read form with the fast masses
 // (the row blocks may then sweep it themselves).
 __device__ bool decide_rows(int seq, int width, int vocab, long long stride, const float* __restrict__ target, const float* __restrict__ draft,
                             const int* __restrict__ draft_ids, const float* __restrict__ temps, const float* __restrict__ u_accept,
-                            const float* __restrict__ u_resample, SpecWs ws) {
+                            const float* __restrict__ u_resample, SpecWs ws, bool pretested) {
     const int W1 = width + 1;
     __shared__ int s_all, s_first, s_rej;
     if (threadIdx.x == 0) {
@@ -446,36 +511,20 @@ __device__ bool decide_rows(int seq, int width, int vocab, long long stride, con
     __syncthreads();
     const int r0 = seq * W1;
     for (int j = (int)threadIdx.x; j <= width; j += (int)blockDim.x) {
-        const RowInfo ri = load_row(ws.rows, r0 + j);
-        const float Tj = temps[r0 + j];
-        bool bad = !temp_ok(Tj);
-        if (j == 0) bad |= !(u_resample[seq] >= 0.0f && u_resample[seq] < 1.0f);
+        unsigned c;
+        if (pretested) {
+            c = ld_agent(&ws.rows[r0 + j].check);
+        } else {
+            const RowArgs a = row_args(seq, j, width, vocab, stride, target, draft, draft_ids, temps, u_accept, u_resample);
+            const float fp = ld_agent((const float*)&ws.rows[r0 + j].fp), fq = ld_agent((const float*)&ws.rows[r0 + j].fq);
+            c = row_check(r0 + j, j, width, vocab, a, load_row(ws.rows, r0 + j), fp, fq, ws);
+        }
+        const unsigned state = c & 15u;
+        const int f = (int)(c >> 4);
         if (j < width) {
-            const float u = u_accept[(size_t)seq * width + j];
-            const int x = draft_ids[(size_t)seq * width + j];
-            bad |= !(u >= 0.0f && u < 1.0f) || x < 0 || x >= vocab;
-            unsigned state = ACC_NO;
-            if (!bad && !ri.nan && ri.tkey != 0ull && ri.dkey != 0ull) {
-                if (Tj == 0.0f) state = x == (int)key_id(ri.tkey) ? ACC_YES : ACC_NO;
-                else {
-                    const float cj = temp_scale(Tj);
-                    const float Mp = key_value(ri.tkey), Mq = key_value(ri.dkey);
-                    const float tx = target[(size_t)(r0 + j) * (size_t)stride + x], dx = draft[(size_t)(r0 + j) * (size_t)stride + x];
-                    const u64 ep = tx > -INFINITY ? mass(tx, Mp, cj) : 0ull;
-                    const u64 eq = dx > -INFINITY ? mass(dx, Mq, cj) : 0ull;
-                    const float fp = ld_agent((const float*)&ws.rows[r0 + j].fp), fq = ld_agent((const float*)&ws.rows[r0 + j].fq);
-                    state = (mass_fast_ok(Mp, cj) && mass_fast_ok(Mq, cj)) ? accept_bounds(u, ep, eq, fp, fq, vocab) : ACC_OPEN;
-                    st_agent(&ws.rows[r0 + j].ep, ep);
-                    st_agent(&ws.rows[r0 + j].eq, eq);
-                }
-            }
-            st_agent(&ws.rows[r0 + j].state, state);
             if (state != ACC_YES) atomicMin(&s_first, j);
             if (state == ACC_NO) atomicMin(&s_rej, j);
         }
-        int f = bad ? 1 : 0;
-        f |= ri.nan != 0u ? 2 : 0;
-        f |= (ri.tkey == 0ull || (j < width && ri.dkey == 0ull)) ? 4 : 0;
         if (f) atomicOr(&s_all, f);
     }
     __syncthreads();
@@ -646,6 +695,10 @@ __global__ void __launch_bounds__(RNT) spec_rows_k(const float* __restrict__ tar
     bool nanf = false;
     if (draw) rows_sweep<true, RNT>(tr, dr, has_draft, vocab, 0, vocab, vec, c2, tm, ti, dm, nanf, om_t, s_t, om_d, s_d);
     else rows_sweep<false, RNT>(tr, dr, has_draft, vocab, 0, vocab, vec, c2, tm, ti, dm, nanf, om_t, s_t, om_d, s_d);
+    // the row's own check: its inputs are loaded while the block reduces
+    const int j = r - seq * W1;
+    RowArgs ra{};
+    if (threadIdx.x == 0) ra = row_args(seq, j, width, vocab, stride, target, draft, draft_ids, temps, u_accept, u_resample);
     // the draft's key carries no index (only its maximum's value is used)
     const u64 tkey = block_max_u64<RNT>(tm == -INFINITY ? 0ull : make_key(okey_f32(tm), (u32)ti), s_red);
     const u64 dkey = block_max_u64<RNT>(dm == -INFINITY ? 0ull : make_key(okey_f32(dm), 0u), s_red);
@@ -663,9 +716,14 @@ __global__ void __launch_bounds__(RNT) spec_rows_k(const float* __restrict__ tar
         st_agent(&ws.rows[r].nan, nan ? 1u : 0u);
         st_agent((u32*)&ws.rows[r].fp, __float_as_uint(fp));
         st_agent((u32*)&ws.rows[r].fq, __float_as_uint(fq));
+        RowInfo ri{};
+        ri.tkey = tkey;
+        ri.dkey = dkey;
+        ri.nan = nan ? 1u : 0u;
+        st_agent(&ws.rows[r].check, row_check(r, j, width, vocab, ra, ri, fp, fq, ws));
     }
     const bool last = arrive_last(&ws.seq_counters[seq], (unsigned)W1, &s_flag);
-    const bool go = last && decide_rows(seq, width, vocab, stride, target, draft, draft_ids, temps, u_accept, u_resample, ws);
+    const bool go = last && decide_rows(seq, width, vocab, stride, target, draft, draft_ids, temps, u_accept, u_resample, ws, true);
     if (!fuse) return;
     if (threadIdx.x == 0) {
         unsigned* word = &ws.fstate[seq];
@@ -993,7 +1051,7 @@ __global__ void __launch_bounds__(NT) spec_split_k(const float* __restrict__ tar
         st_agent((u32*)&ws.rows[r].fq, __float_as_uint(fq));
     }
     if (!arrive_last(&ws.seq_counters[seq], (unsigned)W1, &s_flag)) return;
-    decide_rows(seq, width, vocab, stride, target, draft, draft_ids, temps, u_accept, u_resample, ws);
+    decide_rows(seq, width, vocab, stride, target, draft, draft_ids, temps, u_accept, u_resample, ws, false);
 }
 
 // ---- the exact pass ----
@@ -1428,7 +1486,7 @@ GBS_EXPORT int gbs_spec_verify(const float* target, const float* draft, int n_se
     if (p.R >= ROWS_KERNEL_MIN) {
         // the row blocks sweep the draw rows only when all of them are resident at once (one per CU) and the exact
         // pass's per-block sums have room for one per row of a sequence
-        const bool fuse = p.R <= cu_count() && !getenv("GBS_SPEC_FUSE_OFF");
+        const bool fuse = p.R <= cu_count();
         hipLaunchKernelGGL(spec_rows_k, dim3(p.R), dim3(RNT), 0, st, target, dr, width, vocab, ld, vec, draft_ids, temperatures, u_accept,
                            u_resample, w, fuse, p.SZ);
         rc = launch_status();
