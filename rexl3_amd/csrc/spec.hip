@@ -1165,13 +1165,13 @@ __global__ void __launch_bounds__(NT) spec_exact_k(const float* __restrict__ tar
     const int W1 = width + 1, r0 = seq * W1;
     const int tiles = (vocab + TILE - 1) / TILE;
     const int nsub = tiles * NWD;
+    // swept: the row blocks summed the draw row (its blocks' sums are parts 0..width of zparts); block 0 finishes
+    const bool swept = uni(ld_agent(&ws.fstate[seq])) == FS_GO;
+    if (swept && sp != 0) return;
     const SeqInfo si = load_seq(ws.seqs, seq);
     const int pending = uni(ld_agent(&ws.seqs[seq].pending));
     const int j0 = uni(ld_agent(&ws.seqs[seq].j0)), j1 = uni(ld_agent(&ws.seqs[seq].j1));
     const bool work = si.status == GBS_ROW_OK && pending != 0;
-    // swept: the row blocks summed the draw row (its blocks' sums are parts 0..width of zparts); block 0 finishes
-    const bool swept = uni(ld_agent(&ws.fstate[seq])) == FS_GO;
-    if (swept && sp != 0) return;
     if (work && j0 == j1) {
         const int mode = si.mode;
         const float* tr = target + (size_t)si.row * (size_t)stride;
@@ -1417,10 +1417,10 @@ __global__ void __launch_bounds__(NT) spec_draw_k(const float* __restrict__ targ
     const int S = gridDim.x, sp = blockIdx.x, seq = blockIdx.y;
     const int tiles = (vocab + TILE - 1) / TILE;
     const int nsub = tiles * NWD;
-    const SeqInfo si = load_seq(ws.seqs, seq);
-    const bool drawing = si.status == GBS_ROW_OK && si.mode != 0;
     if (sp == 0 && threadIdx.x == 0) st_agent(&ws.fstate[seq], FS_OPEN);  // read for the last time by the exact pass
+    const bool drawing = uni(ld_agent(&ws.seqs[seq].status)) == GBS_ROW_OK && uni(ld_agent(&ws.seqs[seq].mode)) != 0;
     if (final_written && !drawing) return;  // the exact pass wrote this sequence's outputs
+    const SeqInfo si = load_seq(ws.seqs, seq);
     const float* tr = target + (size_t)si.row * (size_t)stride;
     const float* dr = draft + (size_t)si.row * (size_t)stride;
     u128* wp = ws.wparts + (size_t)seq * nsub;
