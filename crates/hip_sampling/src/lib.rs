@@ -173,6 +173,7 @@ pub mod ffi {
         pub fn gbs_spec_verify(target: *const f32, draft: *const f32, n_seq: i32, width: i32, vocab: i32, stride: i32, draft_ids: *const i32,
                                temperatures: *const f32, u_accept: *const f32, u_resample: *const f32, out_accepted: *mut i32,
                                out_tokens: *mut i32, out_status: *mut i32, ws: *mut c_void, ws_bytes: usize, stream: *mut c_void) -> i32;
+        pub fn gbs_spec_set_fuse_wait(ticks: i64) -> i64;
         pub fn gbs_version() -> *const c_char;
     }
 }

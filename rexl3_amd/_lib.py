@@ -48,6 +48,7 @@ SIGNATURES = {
     "gbs_sample_rows_noalloc": (I, [P, I, I, I, I, P, P, P, P, I, P, P, P, P, P, P]),
     "gbs_spec_verify_workspace_bytes": (Z, [I, I, I]),
     "gbs_spec_verify": (I, [P, P, I, I, I, I, P, P, P, P, P, P, P, P, Z, P]),
+    "gbs_spec_set_fuse_wait": (C.c_longlong, [C.c_longlong]),
     "gbs_version": (C.c_char_p, []),
 }
 

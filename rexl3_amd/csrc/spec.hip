@@ -667,13 +667,14 @@ __device__ __forceinline__ void exact_subtiles(const float* tr, const float* dr,
                                                u64& zq);
 
 constexpr long long FUSE_WAIT_TICKS = 10000;  // a row block's wait for its sequence's decision: 100 us of the 100 MHz clock
+long long g_fuse_wait = FUSE_WAIT_TICKS;     // the limit the launches pass (gbs_spec_set_fuse_wait)
 
 // fuse: the row blocks sweep their sequence's draw row once it is decided (every block of the launch resident at once),
 // writing the exact pass's per-block sums at [row][sz] of zparts, its sub-tile sums and its list of undecided tokens
 __global__ void __launch_bounds__(RNT) spec_rows_k(const float* __restrict__ target, const float* __restrict__ draft, int width, int vocab, long long stride,
                                                    bool vec, const int* __restrict__ draft_ids, const float* __restrict__ temps,
                                                    const float* __restrict__ u_accept, const float* __restrict__ u_resample, SpecWs ws,
-                                                   bool fuse, int sz) {
+                                                   bool fuse, int sz, long long wait_ticks) {
     __shared__ u64 s_red[RNT / WAVE];
     __shared__ float s_redf[RNT / WAVE];
     __shared__ unsigned s_flag, s_go, s_namb;
@@ -737,7 +738,7 @@ __global__ void __launch_bounds__(RNT) spec_rows_k(const float* __restrict__ tar
                                                                   __HIP_MEMORY_SCOPE_AGENT);
             v = set ? (go ? FS_GO : FS_NO) : expect;
         } else {
-            const long long t_end = (long long)wall_clock64() + FUSE_WAIT_TICKS;
+            const long long t_end = (long long)wall_clock64() + wait_ticks;
             while ((v = __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) == FS_OPEN) {
                 if ((long long)wall_clock64() > t_end) {
                     unsigned expect = FS_OPEN;
@@ -1462,6 +1463,12 @@ int cu_count() {
 
 }  // namespace
 
+GBS_EXPORT int64_t gbs_spec_set_fuse_wait(int64_t ticks) {
+    const long long prev = g_fuse_wait;
+    if (ticks >= 0) g_fuse_wait = ticks;
+    return prev;
+}
+
 GBS_EXPORT size_t gbs_spec_verify_workspace_bytes(int n_seq, int width, int vocab) {
     if (n_seq <= 0 || width < 0 || vocab <= 0 || vocab > GBS_MAX_VOCAB) return 0;
     return plan(n_seq, width, vocab).bytes;
@@ -1488,7 +1495,7 @@ GBS_EXPORT int gbs_spec_verify(const float* target, const float* draft, int n_se
         // pass's per-block sums have room for one per row of a sequence
         const bool fuse = p.R <= cu_count();
         hipLaunchKernelGGL(spec_rows_k, dim3(p.R), dim3(RNT), 0, st, target, dr, width, vocab, ld, vec, draft_ids, temperatures, u_accept,
-                           u_resample, w, fuse, p.SZ);
+                           u_resample, w, fuse, p.SZ, g_fuse_wait);
         rc = launch_status();
         if (rc) return rc;
     } else {

@@ -180,3 +180,24 @@ def test_spec_one_read_acceptance_on_the_boundary(vocab):
     assert near >= n_seq
     assert np.array_equal(s, ws) and np.array_equal(a, wa) and np.array_equal(t, wt)
     log(f"accepted lengths {np.bincount(a, minlength=W1)}")
+
+
+@pytest.mark.parametrize("n_seq,width,vocab", [(32, 7, 151_936), (50, 3, 8196)])
+def test_spec_row_block_sweep_given_up(n_seq, width, vocab):
+    """The row blocks' sweep of the draw rows with a wait limit of 0: a block that looks before its sequence is decided
+    gives up at once, so sequences mix the row-block sweep and the exact pass's own (forced from the host through the
+    library's wait limit; every kernel exits normally). Results must equal the oracle's, then again with the default
+    limit on the same workspace."""
+    need_gpu()
+    from rexl3_amd import _lib
+    lib = _lib.load()
+    cfg = W.config5(seed=77 + n_seq, n_seq=n_seq, width=width, vocab=vocab)
+    log(f"spec sweep given up n_seq={n_seq} width={width} vocab={vocab}")
+    prev = lib.gbs_spec_set_fuse_wait(0)
+    try:
+        (a, t, s), (wa, wt, ws) = run(cfg)
+    finally:
+        assert lib.gbs_spec_set_fuse_wait(prev) == 0
+    assert np.array_equal(s, ws) and np.array_equal(a, wa) and np.array_equal(t, wt)
+    (a, t, s), _ = run(cfg)
+    assert np.array_equal(s, ws) and np.array_equal(a, wa) and np.array_equal(t, wt)

@@ -12,7 +12,7 @@ C_TO_RUST = {
     "int": "i32", "size_t": "usize", "void*": "*mut c_void", "const void*": "*const c_void", "int*": "*mut i32",
     "const int*": "*const i32", "float*": "*mut f32", "const float*": "*const f32", "const int32_t*": "*const i32",
     "const uint32_t*": "*const u32", "unsigned long long": "u64", "double": "f64", "const char*": "*const c_char",
-    "const GbsKeyedRow*": "*const KeyedRow", "const GbsRowParams*": "*const RowParams",
+    "const GbsKeyedRow*": "*const KeyedRow", "const GbsRowParams*": "*const RowParams", "int64_t": "i64",
 }
 
 
