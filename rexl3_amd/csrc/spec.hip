@@ -492,9 +492,9 @@ __device__ __forceinline__ unsigned row_check(int r, int j, int width, int vocab
     return state | f << 4;
 }
 
-// The sequence's decisions, by the block that completes the sequence's last row. Thread j checks
-// row j (its parameters, flags and the draft's bounded test; pretested: the row block checked it already); the first row whose test is not ACC_YES is j0, the first
-// ACC_NO (or the bonus row) j1. With j0 == j1 the accepted count is final; the draw then needs row j1's exact sums
+// The sequence's decisions, by the block that completes the sequence's last row. Thread j checks row j (its
+// parameters, flags and the draft's bounded test; pretested: the row block checked it already). The first row whose
+// test is not ACC_YES is j0, the first ACC_NO (or the bonus row) j1. With j0 == j1 the accepted count is final; the draw then needs row j1's exact sums
 // (pending), unless its temperature is 0. With j0 < j1 the tests from j0 on wait for exact sums (pending).
 // Returns, on thread 0, whether the draw row's sweep can run in the exact pass's one-read form with the fast masses
 // (the row blocks may then sweep it themselves).
