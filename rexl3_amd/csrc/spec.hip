@@ -134,7 +134,7 @@ constexpr int FAMB_CAP = 256;  // undecided tokens a row block keeps while it sw
 constexpr size_t SPEC_CTL_BYTES = 4 * (size_t)65536 * 4;
 
 struct Plan {
-    int R, S, S3, tpb, SZ;
+    int R, S, S3, tpb, SZ, F;  // F: blocks of the row pass per sequence
     size_t bytes;
 };
 
@@ -149,7 +149,8 @@ Plan plan(int n_seq, int width, int vocab) {
     p.tpb = (tiles + want - 1) / want;
     p.S3 = (tiles + p.tpb - 1) / p.tpb;
     // per-block exact sums per row: one per block of the exact pass's grid, or per row of a sequence (the row blocks')
-    p.SZ = p.S3 > width + 1 ? p.S3 : width + 1;
+    p.F = (p.R >= ROWS_KERNEL_MIN ? 1 : p.S) * (width + 1);
+    p.SZ = p.S3 > p.F ? p.S3 : p.F;
     p.bytes = SPEC_CTL_BYTES + align256((size_t)p.R * p.S * 16) + align256((size_t)p.R * p.S * 4) + align256((size_t)p.R * p.S * 16) +
               align256((size_t)p.R * sizeof(RowInfo)) + align256((size_t)n_seq * sizeof(SeqInfo)) +
               align256((size_t)n_seq * tiles * NWD * 16) + align256((size_t)p.R * p.SZ * 16) +
@@ -661,7 +662,7 @@ __device__ __forceinline__ void rows_sweep(const float* tr, const float* dr, boo
     });
 }
 
-template <int MODE, bool FAST, int CAP>
+template <int MODE, bool FAST, int CAP, bool PRE = true>
 __device__ __forceinline__ void exact_subtiles(const float* tr, const float* dr, int vocab, int p0, int step, int p1, bool vec, float Mp, float Mq,
                                                float c2, float rho_hi, float rho_lo, SubRec* recs, AmbRec* s_amb, unsigned* s_namb, u64& zp,
                                                u64& zq);
@@ -669,16 +670,90 @@ __device__ __forceinline__ void exact_subtiles(const float* tr, const float* dr,
 constexpr long long FUSE_WAIT_TICKS = 10000;  // a row block's wait for its sequence's decision: 100 us of the 100 MHz clock
 long long g_fuse_wait = FUSE_WAIT_TICKS;     // the limit the launches pass (gbs_spec_set_fuse_wait)
 
-// fuse: the row blocks sweep their sequence's draw row once it is decided (every block of the launch resident at once),
-// writing the exact pass's per-block sums at [row][sz] of zparts, its sub-tile sums and its list of undecided tokens
+// The sequence's sweep of its draw row by the row pass's own blocks, once the sequence is decided (every block of the
+// launch resident at once): block blk of the sequence's nblk takes its share of the draw row's sub-tiles, one per wave
+// at a time, and writes the exact pass's per-block sums at [row][blk] of zparts (sz per row), the sub-tile sums and
+// the list of undecided tokens. The decider publishes the sequence's state word (FS_GO when go), the other blocks wait
+// for it at most wait_ticks, and give up past that; whoever moves the word from FS_OPEN first decides.
+template <int NTH>
+__device__ void coop_sweep(bool decider, bool go, int seq, int blk, int nblk, int vocab, long long stride, bool vec, const float* target,
+                           const float* draft, SpecWs ws, int sz, long long wait_ticks) {
+    __shared__ u64 s_red[NTH / WAVE];
+    __shared__ unsigned s_flag, s_go, s_namb;
+    __shared__ AmbRec s_amb[FAMB_CAP];
+    if (threadIdx.x == 0) {
+        unsigned* word = &ws.fstate[seq];
+        unsigned v;
+        if (decider) {
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            __builtin_amdgcn_s_waitcnt(0);  // the sequence's record has been stored
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            unsigned expect = FS_OPEN;
+            const bool set = __hip_atomic_compare_exchange_strong(word, &expect, go ? FS_GO : FS_NO, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                                  __HIP_MEMORY_SCOPE_AGENT);
+            v = set ? (go ? FS_GO : FS_NO) : expect;
+        } else {
+            const long long t_end = (long long)wall_clock64() + wait_ticks;
+            while ((v = __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) == FS_OPEN) {
+                if ((long long)wall_clock64() > t_end) {
+                    unsigned expect = FS_OPEN;
+                    const bool set = __hip_atomic_compare_exchange_strong(word, &expect, FS_GIVEN_UP, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                                          __HIP_MEMORY_SCOPE_AGENT);
+                    v = set ? FS_GIVEN_UP : expect;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(8);
+            }
+        }
+        s_go = v == FS_GO ? 1u : 0u;
+        s_namb = 0u;
+    }
+    __syncthreads();
+    if (!s_go) return;
+    // this block's share of the draw row's sub-tiles, one per wave at a time
+    const SeqInfo si = load_seq(ws.seqs, seq);
+    const int nsub = (vocab + TILE - 1) / TILE * NWD;
+    const int per = (nsub + nblk - 1) / nblk;
+    const int pb = min(nsub, blk * per), pe = min(nsub, pb + per);
+    const int p0 = pb + (int)threadIdx.x / WAVE;
+    const float* tq = target + (size_t)si.row * (size_t)stride;
+    const float* dq = draft + (size_t)si.row * (size_t)stride;
+    SubRec* recs = ws.subrecs + (size_t)seq * nsub;
+    u64 zp = 0, zq = 0;
+    if (si.mode == 1) {
+        float hi, lo;
+        ratio_bounds(si.fp, si.fq, vocab, hi, lo);
+        exact_subtiles<1, true, FAMB_CAP, (NTH > NT)>(tq, dq, vocab, p0, NTH / WAVE, pe, vec, si.Mp, si.Mq, si.c2, hi, lo, recs, s_amb, &s_namb, zp, zq);
+    } else {
+        exact_subtiles<2, true, FAMB_CAP, (NTH > NT)>(tq, dq, vocab, p0, NTH / WAVE, pe, vec, si.Mp, si.Mq, si.c2, 0.0f, 0.0f, recs, s_amb, &s_namb, zp, zq);
+    }
+    zp = block_sum_u64<NTH>(zp, s_red);  // (its barriers also publish s_namb and s_amb)
+    zq = block_sum_u64<NTH>(zq, s_red);
+    const unsigned nb = s_namb < (unsigned)FAMB_CAP ? s_namb : (unsigned)FAMB_CAP;
+    if (threadIdx.x == 0) {
+        st_agent(&ws.zparts[((size_t)si.row * sz + blk) * 2], zp);
+        st_agent(&ws.zparts[((size_t)si.row * sz + blk) * 2 + 1], zq);
+        s_flag = s_namb != 0u ? atomicAdd(&ws.draw_counters[seq], s_namb > (unsigned)FAMB_CAP ? (unsigned)AMB_SEQ_CAP + 1u : s_namb) : 0u;
+    }
+    __syncthreads();
+    AmbRec* list = ws.ambs + (size_t)seq * AMB_SEQ_CAP;
+    for (unsigned i = threadIdx.x; i < nb; i += NTH) {
+        if (s_flag + i < (unsigned)AMB_SEQ_CAP) {
+            st_agent(&list[s_flag + i].ep, s_amb[i].ep);
+            st_agent(&list[s_flag + i].eq, s_amb[i].eq);
+            st_agent(&list[s_flag + i].p, s_amb[i].p);
+        }
+    }
+}
+
+// fuse: the row blocks sweep their sequence's draw row once it is decided (coop_sweep)
 __global__ void __launch_bounds__(RNT) spec_rows_k(const float* __restrict__ target, const float* __restrict__ draft, int width, int vocab, long long stride,
                                                    bool vec, const int* __restrict__ draft_ids, const float* __restrict__ temps,
                                                    const float* __restrict__ u_accept, const float* __restrict__ u_resample, SpecWs ws,
                                                    bool fuse, int sz, long long wait_ticks) {
     __shared__ u64 s_red[RNT / WAVE];
     __shared__ float s_redf[RNT / WAVE];
-    __shared__ unsigned s_flag, s_go, s_namb;
-    __shared__ AmbRec s_amb[FAMB_CAP];
+    __shared__ unsigned s_flag;
     const int r = blockIdx.x;
     const int W1 = width + 1;
     const int seq = r / W1;
@@ -725,70 +800,7 @@ __global__ void __launch_bounds__(RNT) spec_rows_k(const float* __restrict__ tar
     }
     const bool last = arrive_last(&ws.seq_counters[seq], (unsigned)W1, &s_flag);
     const bool go = last && decide_rows(seq, width, vocab, stride, target, draft, draft_ids, temps, u_accept, u_resample, ws, true);
-    if (!fuse) return;
-    if (threadIdx.x == 0) {
-        unsigned* word = &ws.fstate[seq];
-        unsigned v;
-        if (last) {
-            __atomic_signal_fence(__ATOMIC_SEQ_CST);
-            __builtin_amdgcn_s_waitcnt(0);  // the sequence's record has been stored
-            __atomic_signal_fence(__ATOMIC_SEQ_CST);
-            unsigned expect = FS_OPEN;
-            const bool set = __hip_atomic_compare_exchange_strong(word, &expect, go ? FS_GO : FS_NO, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                                                  __HIP_MEMORY_SCOPE_AGENT);
-            v = set ? (go ? FS_GO : FS_NO) : expect;
-        } else {
-            const long long t_end = (long long)wall_clock64() + wait_ticks;
-            while ((v = __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) == FS_OPEN) {
-                if ((long long)wall_clock64() > t_end) {
-                    unsigned expect = FS_OPEN;
-                    const bool set = __hip_atomic_compare_exchange_strong(word, &expect, FS_GIVEN_UP, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                                                          __HIP_MEMORY_SCOPE_AGENT);
-                    v = set ? FS_GIVEN_UP : expect;
-                    break;
-                }
-                __builtin_amdgcn_s_sleep(8);
-            }
-        }
-        s_go = v == FS_GO ? 1u : 0u;
-        s_namb = 0u;
-    }
-    __syncthreads();
-    if (!s_go) return;
-    // this block's share of the draw row's sub-tiles, one per wave at a time
-    const SeqInfo si = load_seq(ws.seqs, seq);
-    const int nsub = (vocab + TILE - 1) / TILE * NWD;
-    const int sp = r - seq * W1, per = (nsub + W1 - 1) / W1;
-    const int pb = min(nsub, sp * per), pe = min(nsub, pb + per);
-    const int p0 = pb + (int)threadIdx.x / WAVE;
-    const float* tq = target + (size_t)si.row * (size_t)stride;
-    const float* dq = draft + (size_t)si.row * (size_t)stride;
-    SubRec* recs = ws.subrecs + (size_t)seq * nsub;
-    u64 zp = 0, zq = 0;
-    if (si.mode == 1) {
-        float hi, lo;
-        ratio_bounds(si.fp, si.fq, vocab, hi, lo);
-        exact_subtiles<1, true, FAMB_CAP>(tq, dq, vocab, p0, RNT / WAVE, pe, vec, si.Mp, si.Mq, si.c2, hi, lo, recs, s_amb, &s_namb, zp, zq);
-    } else {
-        exact_subtiles<2, true, FAMB_CAP>(tq, dq, vocab, p0, RNT / WAVE, pe, vec, si.Mp, si.Mq, si.c2, 0.0f, 0.0f, recs, s_amb, &s_namb, zp, zq);
-    }
-    zp = block_sum_u64<RNT>(zp, s_red);  // (its barriers also publish s_namb and s_amb)
-    zq = block_sum_u64<RNT>(zq, s_red);
-    const unsigned nb = s_namb < (unsigned)FAMB_CAP ? s_namb : (unsigned)FAMB_CAP;
-    if (threadIdx.x == 0) {
-        st_agent(&ws.zparts[((size_t)si.row * sz + sp) * 2], zp);
-        st_agent(&ws.zparts[((size_t)si.row * sz + sp) * 2 + 1], zq);
-        s_flag = s_namb != 0u ? atomicAdd(&ws.draw_counters[seq], s_namb > (unsigned)FAMB_CAP ? (unsigned)AMB_SEQ_CAP + 1u : s_namb) : 0u;
-    }
-    __syncthreads();
-    AmbRec* list = ws.ambs + (size_t)seq * AMB_SEQ_CAP;
-    for (unsigned i = threadIdx.x; i < nb; i += RNT) {
-        if (s_flag + i < (unsigned)AMB_SEQ_CAP) {
-            st_agent(&list[s_flag + i].ep, s_amb[i].ep);
-            st_agent(&list[s_flag + i].eq, s_amb[i].eq);
-            st_agent(&list[s_flag + i].p, s_amb[i].p);
-        }
-    }
+    if (fuse) coop_sweep<RNT>(last, go, seq, r - seq * W1, W1, vocab, stride, vec, target, draft, ws, sz, wait_ticks);
 }
 
 // inclusive prefix sum of a u128 over the wave
@@ -984,7 +996,8 @@ __device__ int pick_token(const u128 (&sub)[SPT], int nsub, int vocab, float u, 
 __global__ void __launch_bounds__(NT) spec_split_k(const float* __restrict__ target, const float* __restrict__ draft, int width, int vocab,
                                                    long long stride, int chunk, bool vec, const int* __restrict__ draft_ids,
                                                    const float* __restrict__ temps, const float* __restrict__ u_accept,
-                                                   const float* __restrict__ u_resample, SpecWs ws) {
+                                                   const float* __restrict__ u_resample, SpecWs ws, bool fuse, int sz,
+                                                   long long wait_ticks) {
     __shared__ u64 s_red[NT / WAVE];
     __shared__ float s_redf[NT / WAVE];
     __shared__ unsigned s_flag;
@@ -1019,40 +1032,45 @@ __global__ void __launch_bounds__(NT) spec_split_k(const float* __restrict__ tar
         st_agent(&ws.sumparts[((size_t)r * S + sp) * 2], (u64)__float_as_uint(fp));
         st_agent(&ws.sumparts[((size_t)r * S + sp) * 2 + 1], (u64)__float_as_uint(fq));
     }
-    if (!arrive_last(&ws.row_counters[r], (unsigned)S, &s_flag)) return;
-    // the row: maxima over the chunks, then each chunk's sums rescaled to them (thread o takes chunks o, o + NT, ...)
-    u64 a = 0, b = 0, n = 0;
-    for (int o = (int)threadIdx.x; o < S; o += NT) {
-        const u64 x = ld_agent(&ws.maxparts[((size_t)r * S + o) * 2]), y = ld_agent(&ws.maxparts[((size_t)r * S + o) * 2 + 1]);
-        a = x > a ? x : a;
-        b = y > b ? y : b;
-        n |= ld_agent(&ws.nanparts[(size_t)r * S + o]);
-    }
-    a = block_max_u64<NT>(a, s_red);
-    b = block_max_u64<NT>(b, s_red);
-    n = block_max_u64<NT>(n, s_red);
-    if (draw && a != 0ull && n == 0ull) {
-        const float Mp = key_value(a), Mq = b != 0ull ? key_value(b) : Mp;
-        float xp = 0.0f, xq = 0.0f;
+    const bool row_last = arrive_last(&ws.row_counters[r], (unsigned)S, &s_flag);
+    bool seq_last = false, go = false;
+    if (row_last) {
+        // the row: maxima over the chunks, then each chunk's sums rescaled to them (thread o takes chunks o, o + NT, ...)
+        u64 a = 0, b = 0, n = 0;
         for (int o = (int)threadIdx.x; o < S; o += NT) {
             const u64 x = ld_agent(&ws.maxparts[((size_t)r * S + o) * 2]), y = ld_agent(&ws.maxparts[((size_t)r * S + o) * 2 + 1]);
-            const float gp = __uint_as_float((u32)ld_agent(&ws.sumparts[((size_t)r * S + o) * 2]));
-            const float gq = __uint_as_float((u32)ld_agent(&ws.sumparts[((size_t)r * S + o) * 2 + 1]));
-            xp += (x != 0ull && gp > 0.0f) ? gp * __builtin_amdgcn_exp2f((key_value(x) - Mp) * c2) : 0.0f;
-            xq += (y != 0ull && gq > 0.0f) ? gq * __builtin_amdgcn_exp2f((key_value(y) - Mq) * c2) : 0.0f;
+            a = x > a ? x : a;
+            b = y > b ? y : b;
+            n |= ld_agent(&ws.nanparts[(size_t)r * S + o]);
         }
-        fp = block_sum_f32<NT>(xp, s_redf);
-        fq = block_sum_f32<NT>(xq, s_redf);
+        a = block_max_u64<NT>(a, s_red);
+        b = block_max_u64<NT>(b, s_red);
+        n = block_max_u64<NT>(n, s_red);
+        if (draw && a != 0ull && n == 0ull) {
+            const float Mp = key_value(a), Mq = b != 0ull ? key_value(b) : Mp;
+            float xp = 0.0f, xq = 0.0f;
+            for (int o = (int)threadIdx.x; o < S; o += NT) {
+                const u64 x = ld_agent(&ws.maxparts[((size_t)r * S + o) * 2]), y = ld_agent(&ws.maxparts[((size_t)r * S + o) * 2 + 1]);
+                const float gp = __uint_as_float((u32)ld_agent(&ws.sumparts[((size_t)r * S + o) * 2]));
+                const float gq = __uint_as_float((u32)ld_agent(&ws.sumparts[((size_t)r * S + o) * 2 + 1]));
+                xp += (x != 0ull && gp > 0.0f) ? gp * __builtin_amdgcn_exp2f((key_value(x) - Mp) * c2) : 0.0f;
+                xq += (y != 0ull && gq > 0.0f) ? gq * __builtin_amdgcn_exp2f((key_value(y) - Mq) * c2) : 0.0f;
+            }
+            fp = block_sum_f32<NT>(xp, s_redf);
+            fq = block_sum_f32<NT>(xq, s_redf);
+        }
+        if (threadIdx.x == 0) {
+            st_agent(&ws.rows[r].tkey, a);
+            st_agent(&ws.rows[r].dkey, b);
+            st_agent(&ws.rows[r].nan, (unsigned)n);
+            st_agent((u32*)&ws.rows[r].fp, __float_as_uint(fp));
+            st_agent((u32*)&ws.rows[r].fq, __float_as_uint(fq));
+        }
+        seq_last = arrive_last(&ws.seq_counters[seq], (unsigned)W1, &s_flag);
+        go = seq_last && decide_rows(seq, width, vocab, stride, target, draft, draft_ids, temps, u_accept, u_resample, ws, false);
     }
-    if (threadIdx.x == 0) {
-        st_agent(&ws.rows[r].tkey, a);
-        st_agent(&ws.rows[r].dkey, b);
-        st_agent(&ws.rows[r].nan, (unsigned)n);
-        st_agent((u32*)&ws.rows[r].fp, __float_as_uint(fp));
-        st_agent((u32*)&ws.rows[r].fq, __float_as_uint(fq));
-    }
-    if (!arrive_last(&ws.seq_counters[seq], (unsigned)W1, &s_flag)) return;
-    decide_rows(seq, width, vocab, stride, target, draft, draft_ids, temps, u_accept, u_resample, ws, false);
+    // every chunk block of the sequence sweeps its share of the draw row
+    if (fuse) coop_sweep<NT>(seq_last, go, seq, (r - seq * W1) * S + sp, W1 * S, vocab, stride, vec, target, draft, ws, sz, wait_ticks);
 }
 
 // ---- the exact pass ----
@@ -1074,7 +1092,7 @@ __device__ __forceinline__ float to_float(u64 v) { return fmaf((float)(u32)(v >>
 
 // Sub-tiles p0, p0 + step, ... below p1 (a sub-tile is one wave's SUB elements; sub-tile p starts at element p SUB),
 // each summed by the calling wave; undecided tokens go to s_amb (CAP entries, *s_namb counts them all).
-template <int MODE, bool FAST, int CAP>
+template <int MODE, bool FAST, int CAP, bool PRE>
 __device__ __forceinline__ void exact_subtiles(const float* tr, const float* dr, int vocab, int p0, int step, int p1, bool vec, float Mp, float Mq,
                                                float c2, float rho_hi, float rho_lo, SubRec* recs, AmbRec* s_amb, unsigned* s_namb, u64& zp,
                                                u64& zq) {
@@ -1103,16 +1121,21 @@ __device__ __forceinline__ void exact_subtiles(const float* tr, const float* dr,
         }
     };
     constexpr float LO = 1.0f - 1.0f / 524288.0f, HI = 1.0f + 1.0f / 524288.0f;  // 1 -+ 2^-19, over the float roundings
+    // PRE: the next sub-tile's loads go out before this one is summed (twice the registers)
     float tn[DU * 4], dn[DU * 4];
-    if (p0 < p1) issue(p0, tn, dn);
+    if (PRE && p0 < p1) issue(p0, tn, dn);
     for (int p = p0; p < p1; p += step) {
         float t[DU * 4], d[DU * 4];
+        if (PRE) {
 #pragma unroll
-        for (int i = 0; i < DU * 4; ++i) {
-            t[i] = tn[i];
-            d[i] = dn[i];
+            for (int i = 0; i < DU * 4; ++i) {
+                t[i] = tn[i];
+                d[i] = dn[i];
+            }
+            if (p + step < p1) issue(p + step, tn, dn);
+        } else {
+            issue(p, t, d);
         }
-        if (p + step < p1) issue(p + step, tn, dn);
         u64 A = 0, B = 0;
 #pragma unroll
         for (int j = 0; j < DU; ++j) {
@@ -1150,7 +1173,7 @@ __device__ __forceinline__ void exact_subtiles(const float* tr, const float* dr,
 }
 
 __global__ void __launch_bounds__(NT) spec_exact_k(const float* __restrict__ target, const float* __restrict__ draft, int width, int vocab,
-                                                   long long stride, int tpb, int zs, bool vec, const int* __restrict__ draft_ids,
+                                                   long long stride, int tpb, int zs, int fparts, bool vec, const int* __restrict__ draft_ids,
                                                    const float* __restrict__ temps, const float* __restrict__ u_accept,
                                                    const float* __restrict__ u_resample, SpecWs ws, int* __restrict__ out_accepted,
                                                    int* __restrict__ out_tokens, int* __restrict__ out_status) {
@@ -1166,7 +1189,7 @@ __global__ void __launch_bounds__(NT) spec_exact_k(const float* __restrict__ tar
     const int W1 = width + 1, r0 = seq * W1;
     const int tiles = (vocab + TILE - 1) / TILE;
     const int nsub = tiles * NWD;
-    // swept: the row blocks summed the draw row (its blocks' sums are parts 0..width of zparts); block 0 finishes
+    // swept: the row pass's blocks summed the draw row (their sums are parts 0..fparts - 1 of zparts); block 0 finishes
     const bool swept = uni(ld_agent(&ws.fstate[seq])) == FS_GO;
     if (swept && sp != 0) return;
     const SeqInfo si = load_seq(ws.seqs, seq);
@@ -1232,7 +1255,7 @@ __global__ void __launch_bounds__(NT) spec_exact_k(const float* __restrict__ tar
         // the last block: every load at once (the blocks' sums, the sub-tile sums, the list's length and its first
         // 2 NT entries), then the exact sums, the sub-tile weights and the draw
         u64 a = 0, b = 0;
-        const int parts = swept ? W1 : S;
+        const int parts = swept ? fparts : S;
         for (int o = (int)threadIdx.x; o < parts; o += NT) {
             a += ld_agent(&ws.zparts[((size_t)si.row * zs + o) * 2]);
             b += ld_agent(&ws.zparts[((size_t)si.row * zs + o) * 2 + 1]);
@@ -1461,6 +1484,19 @@ int cu_count() {
     return counts[dev];
 }
 
+// blocks of spec_split_k the current device holds at once (0 when a query fails: its blocks then never sweep)
+int split_resident() {
+    static int counts[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    if (counts[dev] == 0) {
+        int per_cu = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, spec_split_k, NT, 0) != hipSuccess) return 0;
+        counts[dev] = per_cu * cu_count();
+    }
+    return counts[dev];
+}
+
 }  // namespace
 
 GBS_EXPORT int64_t gbs_spec_set_fuse_wait(int64_t ticks) {
@@ -1499,12 +1535,14 @@ GBS_EXPORT int gbs_spec_verify(const float* target, const float* draft, int n_se
         rc = launch_status();
         if (rc) return rc;
     } else {
+        // the same sweep when the whole grid is resident at once
+        const bool fuse = (long long)p.S * p.R <= (long long)split_resident();
         hipLaunchKernelGGL(spec_split_k, dim3(p.S, p.R), dim3(NT), 0, st, target, dr, width, vocab, ld, chunk, vec, draft_ids, temperatures,
-                           u_accept, u_resample, w);
+                           u_accept, u_resample, w, fuse, p.SZ, g_fuse_wait);
         rc = launch_status();
         if (rc) return rc;
     }
-    hipLaunchKernelGGL(spec_exact_k, dim3(p.S3, n_seq), dim3(NT), 0, st, target, dr, width, vocab, ld, p.tpb, p.SZ, vec, draft_ids, temperatures,
+    hipLaunchKernelGGL(spec_exact_k, dim3(p.S3, n_seq), dim3(NT), 0, st, target, dr, width, vocab, ld, p.tpb, p.SZ, p.F, vec, draft_ids, temperatures,
                        u_accept, u_resample, w, out_accepted, out_tokens, out_status);
     rc = launch_status();
     if (rc) return rc;

@@ -182,9 +182,9 @@ def test_spec_one_read_acceptance_on_the_boundary(vocab):
     log(f"accepted lengths {np.bincount(a, minlength=W1)}")
 
 
-@pytest.mark.parametrize("n_seq,width,vocab", [(32, 7, 151_936), (50, 3, 8196)])
+@pytest.mark.parametrize("n_seq,width,vocab", [(32, 7, 151_936), (50, 3, 8196), (8, 7, 151_936), (12, 3, 12_288)])
 def test_spec_row_block_sweep_given_up(n_seq, width, vocab):
-    """The row blocks' sweep of the draw rows with a wait limit of 0: a block that looks before its sequence is decided
+    """(256 and 200 rows: one block per row; 64 and 48 rows: the split row pass.) The row pass's sweep of the draw rows with a wait limit of 0: a block that looks before its sequence is decided
     gives up at once, so sequences mix the row-block sweep and the exact pass's own (forced from the host through the
     library's wait limit; every kernel exits normally). Results must equal the oracle's, then again with the default
     limit on the same workspace."""
