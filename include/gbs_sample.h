@@ -309,11 +309,12 @@ int gbs_spec_verify(const float* target, const float* draft, int n_seq, int widt
                     const float* temperatures, const float* u_accept, const float* u_resample, int* out_accepted,
                     int* out_tokens, int* out_status, void* ws, size_t ws_bytes, void* stream);
 
-/* Test hook (no counterpart in the reference): with 256 rows or fewer, the row blocks of gbs_spec_verify sweep their
- * sequence's draw row themselves once the sequence is decided, each waiting at most `ticks` of the device's 100 MHz
- * clock for the decision (default 10000, 100 us; a block that waits longer leaves the sweep to the exact pass). Sets the
- * limit for later calls from this process (ticks >= 0) and returns the previous one. A limit of 0 forces the
- * fallback on every sequence whose deciding block is not the first to look; the results are the same either way. */
+/* Test hook (no counterpart in the reference). When the row pass's grid is resident at once, the row-pass blocks of
+ * gbs_spec_verify sweep their sequence's draw row themselves once the sequence is decided. Each waits at most `ticks`
+ * of the device's 100 MHz clock for the decision (default 10000, 100 us); a block that waits longer leaves the sweep
+ * to the exact pass. Sets the limit for later calls from this process (ticks >= 0) and returns the previous one. A
+ * limit of 0 forces the fallback on every sequence whose deciding block is not the first to look; the results are
+ * the same either way. */
 int64_t gbs_spec_set_fuse_wait(int64_t ticks);
 
 /* Library version string. */
