@@ -55,11 +55,19 @@ __device__ __forceinline__ double pairwise_lanes(double a, int n) {
     double r[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) r[j] = readlane_f64(a, j);
-    int i = 8;
-    for (; i < n - (n % 8); i += 8) {
+    const int full = n - (n % 8);
+    // (unrolled: each block's reads are issued ahead of its additions)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) r[j] += readlane_f64(a, i + j);
+    for (int b = 1; b < 8; ++b) {
+        if (b * 8 < full) {
+            double v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = readlane_f64(a, b * 8 + j);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) r[j] += v[j];
+        }
     }
+    int i = full;
     double res = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
     for (; i < n; ++i) res += readlane_f64(a, i);
     return res;
@@ -79,13 +87,38 @@ __device__ int keyed_choose_wave(const float* vals, const u32* ids, int k, u64 s
         // the maximum of `scaled` is its first entry: the values are sorted and t > 0
         const double e = l < k ? exp(sc - sc0) : 0.0;
         const double total = pairwise_lanes(e, k);
-        // the quotients probs[i] / total on their own lanes (the same IEEE divisions), then the running sum in order
+        // the quotients probs[i] / total on their own lanes (the same IEEE divisions)
         const double q = l < k ? e / total : 0.0;
-        double c = 0.0;
-        int below = 0;
-        for (int i = 0; i < k; ++i) {
-            c += readlane_f64(q, i);
-            below += c < top_p ? 1 : 0;
+        // below = the count of running sums c_i = q_0 + ... + q_i (added in order, rounded at each step) under top_p.
+        // A scan across the lanes gives each lane a sum of the same terms in another order (a tree of depth 6): with
+        // nonnegative terms both are within 63u and 6u of the exact sum (u = 2^-53), so a lane whose scan value is
+        // below top_p / (1 + 2^-45), or at least top_p / (1 - 2^-45), has its c_i on the same side. Only when some
+        // lane falls between does the ordered chain run.
+        double sp = q;
+#pragma unroll
+        for (int m = 1; m < WAVE; m <<= 1) {
+            const double o = __shfl_up(sp, (unsigned)m, WAVE);
+            if (l >= m) sp += o;
+        }
+        const bool sure_below = sp * (1.0 + 0x1p-45) < top_p, sure_above = sp * (1.0 - 0x1p-45) >= top_p;
+        int below = __popcll(ballot(l < k && sure_below));
+        if (ballot(l < k && !sure_below && !sure_above)) {
+            // Eight quotients at a time are read into scalar registers ahead of their additions, and the running
+            // sums are compared after the chain. Lanes from k on hold 0, and adding 0 leaves a sum unchanged.
+            double c = 0.0;
+            below = 0;
+            for (int i0 = 0; i0 < k; i0 += 8) {
+                double v[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) v[j] = readlane_f64(q, i0 + j);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    c += v[j];
+                    v[j] = c;
+                }
+#pragma unroll
+                for (int j = 0; j < 8; ++j) below += (i0 + j < k && v[j] < top_p) ? 1 : 0;
+            }
         }
         keep = below + 1 < k ? below + 1 : k;
     }

@@ -299,3 +299,25 @@ def test_tree_verify_on_device():
         assert st[t] == 0 and list(path[t, :plen[t]]) == want and (path[t, plen[t]:] == -1).all()
         deep += len(want) > 2
     assert st[5] == 2 and deep > 5
+
+
+def test_device_keyed_pick_top_p_on_exact_running_sums():
+    """Rows whose running probability sums land exactly on top_p (equal values: the quotients are exact powers of two)
+    and a hair either side of it, so the device takes the ordered running sum rather than its lane-scan shortcut;
+    against the oracle's try_choose."""
+    need_gpu()
+    rows, count = 96, 16
+    ids = np.tile(np.arange(100, 100 + count, dtype=np.int32), (rows, 1))
+    vals = np.zeros((rows, count), dtype=np.float32)
+    vals[:, :8] = 1.0            # 8 equal leaders: probabilities sum to exact multiples of 1/8 of their mass
+    vals[:, 8:] = -40.0
+    recs = np.zeros(rows, dtype=S.KEYED_ROW_DTYPE)
+    for r in range(rows):
+        top_p = [0.25, 0.5, 0.75, 0.125 * (1 + r % 7)][r % 4]
+        top_p = float(np.nextafter(top_p, 0.0 if r % 3 == 1 else 1.0)) if r % 3 else top_p
+        recs[r] = (1000 + r, r, 1.0, top_p, 0.0, count, 1)
+    gi, gv = S.keyed_pick(dev(ids), dev(vals), recs, 0)
+    wi, wv = O.keyed_pick_rows(ids, vals, recs, 0)
+    gi, gv = host(gi), host(gv)
+    assert np.array_equal(gi, wi), np.nonzero(gi != wi)[0][:10]
+    assert np.array_equal(gv.view(np.uint32), wv.view(np.uint32))
